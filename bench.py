@@ -1,0 +1,205 @@
+"""Benchmark: Mixtral-8x7B-shaped Q4_K MoE layer on one MI355X.
+
+A step is one MoE-layer forward (router, dispatch, expert products, combine)
+over one batch of T synthetic tokens whose activations already sit in HBM.
+The headline line is T=64; the JSON also carries T=1 and T=8.  Layer
+replicas (separate device copies of the same bytes) are cycled from step to
+step so that re-reads cannot be served from the 256 MB Infinity Cache.
+
+Prints ONE JSON line (rank 0, N=1).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20
+
+
+def algorithmic_bytes(cfg, counts, T):
+    """Per-call bytes: quant blocks of every touched expert (gate, up, down),
+    the f32 router, x in and y out.  Intermediates excluded."""
+    from leafcutterllm_amd.configs import tensor_size
+    touched = int(sum(1 for c in counts if c > 0))
+    gu = 2 * tensor_size(cfg.qtype_gate, cfg.d_ff * cfg.d_model)
+    dn = tensor_size(cfg.qtype_down, cfg.d_model * cfg.d_ff)
+    layer = touched * (gu + dn) + 4 * cfg.d_model * cfg.n_expert + 8 * T * cfg.d_model
+    gateup = touched * gu + 4 * T * cfg.d_model + 4 * T * cfg.n_expert_used * cfg.d_ff
+    return layer, gateup, touched
+
+
+def cpu_baseline(cfg, layer, x, budget_s=15.0):
+    """The oracle's reference-order CPU path (experts dequantised to f32 once,
+    then forwards), timed on this host; bounded to about `budget_s`."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import lcoracle as O
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    od = O.Desc()
+    for name, _ in od._fields_:
+        setattr(od, name, getattr(cfg.desc(x.shape[0]), name))
+    t0 = time.perf_counter()
+    res = O.Resident(od, layer, threads)
+    t_load = time.perf_counter() - t0
+    times = []
+    while len(times) < 5 and sum(times) < budget_s:
+        t0 = time.perf_counter()
+        res.forward(x, threads)
+        times.append(time.perf_counter() - t0)
+    res.close()
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": round(x.shape[0] / med, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+        "sample": (f"{len(times)} forward(s) of the same layer at T={x.shape[0]} after a "
+                   f"{t_load:.1f} s one-time f32 dequantisation; median {med * 1e3:.1f} ms; "
+                   "reference f32 GEMM order, column-parallel over all threads"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--tokens", type=int, default=64, help="headline batch")
+    ap.add_argument("--sweep", default="1,8,64")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel-events", type=int, default=1,
+                    help="record HIP events around each kernel inside the timed region")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
+              "(the MoE layer would shard by expert across GPUs, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+
+    import leafcutterllm_amd as L
+    from leafcutterllm_amd import hip
+
+    cfg = L.CONFIGS[args.config]
+    sweep = sorted({int(t) for t in args.sweep.split(",") if t} | {args.tokens})
+    Tmax = max(sweep)
+    t0 = time.perf_counter()
+    layer = L.synth_layer(cfg, seed=0)
+    t_synth = time.perf_counter() - t0
+
+    # replicas: reuse distance of the smallest touched set >= 2x the MALL
+    min_touched = min(cfg.n_expert, cfg.n_expert_used) * cfg.expert_bytes()
+    R = max(2, math.ceil(2 * MALL_BYTES / min_touched) + 1)
+    moes = [L.MoeFfn(cfg.desc(Tmax), layer) for _ in range(R)]
+    stream = hip.Stream()
+    xbufs = {}
+    ybufs = [hip.DeviceBuffer(4 * Tmax * cfg.d_model) for _ in range(R)]
+    for T in sweep:
+        for r in range(R):
+            x = L.synth_x(cfg, T, seed=0, index=1000 * r + T)
+            xbufs[(r, T)] = hip.DeviceBuffer(x.nbytes).upload(x)
+
+    per_batch = {}
+    for T in sweep:
+        # realised routing of every replica's input -> algorithmic bytes
+        call_bytes, gu_bytes, touched = [], [], []
+        for r in range(R):
+            moes[r].forward_dev(xbufs[(r, T)].ptr, T, ybufs[r].ptr, stream.ptr)
+            stream.synchronize()
+            counts = moes[r].dispatch()["counts"]
+            b, g, n = algorithmic_bytes(cfg, counts, T)
+            call_bytes.append(b)
+            gu_bytes.append(g)
+            touched.append(n)
+        for i in range(args.warmup):
+            r = i % R
+            moes[r].forward_dev(xbufs[(r, T)].ptr, T, ybufs[r].ptr, stream.ptr)
+        stream.synchronize()
+        for m in moes:
+            m.set_timing(bool(args.kernel_events))
+            m.get_timing()  # reset
+        ev0, ev1 = hip.Event(), hip.Event()
+        stream.synchronize()
+        ev0.record(stream)
+        for i in range(args.steps):
+            r = i % R
+            moes[r].forward_dev(xbufs[(r, T)].ptr, T, ybufs[r].ptr, stream.ptr)
+        ev1.record(stream)
+        stream.synchronize()
+        ms = ev0.elapsed_ms(ev1) / args.steps
+        kern = {}
+        for m in moes:
+            for name, (kms, n) in m.get_timing().items():
+                a, b = kern.get(name, (0.0, 0))
+                kern[name] = (a + kms, b + n)
+            m.set_timing(False)
+        bytes_per_step = sum(call_bytes[i % R] for i in range(args.steps)) / args.steps
+        gu_per_launch = sum(gu_bytes[i % R] for i in range(args.steps)) / args.steps
+        gu_ms = kern["gateup"][0] / max(1, kern["gateup"][1])
+        per_batch[T] = {
+            "tokens_per_s": T / (ms * 1e-3),
+            "ms_per_step": ms,
+            "layer_GBps": bytes_per_step / (ms * 1e-3) / 1e9,
+            "layer_bytes": bytes_per_step,
+            "touched_experts": sum(touched) / len(touched),
+            "gateup_ms": gu_ms,
+            "gateup_bytes": gu_per_launch,
+            "gateup_GBps": gu_per_launch / (gu_ms * 1e-3) / 1e9,
+            "kernel_ms": {k: v[0] / max(1, v[1]) for k, v in kern.items()},
+        }
+
+    head = per_batch[args.tokens]
+    out = {
+        "metric": "MoE-layer tokens/s + % HBM roofline, Mixtral-shape Q4_K, batch 1-64",
+        "value": round(head["tokens_per_s"], 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k weights, f32 activations/accumulate",
+        "data": "synthetic (seeded splitmix64 N(0,1) activations, N(0,0.02) weights quantised to Q4_K)",
+        "config": {
+            "workload": f"config {args.config}: {cfg.note}, d_model={cfg.d_model}, d_ff={cfg.d_ff}, "
+                        f"E={cfg.n_expert}, top-{cfg.n_expert_used}, T={args.tokens} tokens/step",
+            "batch": args.tokens, "d_model": cfg.d_model, "d_ff": cfg.d_ff,
+            "n_expert": cfg.n_expert, "top_k": cfg.n_expert_used, "replicas": R,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "k_gateup (fused Q4_K dequant-dot gate+up + SwiGLU)",
+            "achieved": round(head["gateup_GBps"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(head["gateup_GBps"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "layer_roofline_frac": round(head["layer_GBps"] / HBM_PEAK_GBS, 4),
+        "per_batch": {str(T): {k: (round(v, 4) if isinstance(v, float) else v)
+                               for k, v in d.items() if k != "kernel_ms"} |
+                      {"kernel_ms": {k: round(v, 5) for k, v in d["kernel_ms"].items()},
+                       "layer_frac": round(d["layer_GBps"] / HBM_PEAK_GBS, 4)}
+                      for T, d in per_batch.items()},
+        "synth_s": round(t_synth, 2),
+    }
+    for m in moes:
+        m.close()
+    if not args.no_cpu:
+        x = L.synth_x(cfg, args.tokens, seed=0, index=args.tokens)
+        out["cpu_baseline"] = cpu_baseline(cfg, layer, x)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,177 @@
+/*
+ * lcmoe.h -- C ABI of the MI355X (gfx950) MoE feed-forward layer.
+ *
+ * Drop-in boundary for the reference engine's FFN call:
+ *   Engine::ffn_forward(&self, x: &Tensor, weights) -> Tensor
+ *     rust/src/inference/engine.rs:146-164 (called at engine.rs:114), and its
+ *     twin ShardEngine::ffn_forward, rust/src/inference/shard_engine.rs:181-198
+ *     (called at shard_engine.rs:146).
+ * The arithmetic under it replaces Tensor::matmul's dispatch
+ * (rust/src/model/tensor.rs:107-135) into Backend::matmul
+ * (rust/src/backend/mod.rs:18-46, CpuBackend at rust/src/backend/cpu.rs:13-23)
+ * and the quantised GEMMs (rust/src/kernels/int8_gemm.rs:172-194), with the
+ * GGUF block decoders (rust/src/kernels/mod.rs:37-180) running on the GPU.
+ *
+ * Plain C: pointers, sizes, integer status codes.  No C++ or HIP types cross
+ * the boundary (a stream is passed as void*).
+ *
+ * Threading: one handle = one HIP stream + one workspace; a handle serves one
+ * caller at a time (the reference already serialises through
+ * Arc<Mutex<Engine>>, rust/src/main.rs:41).  Distinct handles may be used
+ * concurrently.  lcmoe_last_error() is per thread.
+ */
+#ifndef LCMOE_H
+#define LCMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LCMOE_ABI_VERSION 1
+
+typedef enum {
+    LCMOE_OK = 0,
+    LCMOE_ERR_INVALID_ARG = 1,    /* null pointer, bad shape or size         */
+    LCMOE_ERR_UNSUPPORTED = 2,    /* quant type / router kind not supported  */
+    LCMOE_ERR_CORRUPT = 3,        /* non-finite or absurd block scale        */
+    LCMOE_ERR_HIP = 4,            /* HIP runtime error (incl. no device)     */
+    LCMOE_ERR_OUT_OF_MEMORY = 5,  /* device allocation failed                */
+    LCMOE_ERR_STATE = 6           /* e.g. query before any forward           */
+} lcmoe_status;
+
+/* GGUF ggml_type codes, QuantType::code, rust/src/model/quant.rs:45-73. */
+enum {
+    LCMOE_TYPE_F32 = 0,
+    LCMOE_TYPE_Q8_0 = 8,
+    LCMOE_TYPE_Q4_K = 12,
+    LCMOE_TYPE_Q6_K = 14
+};
+
+/* Router kinds.  The reference has no router; these are the written
+ * semantics this library implements (selection ties -> lower expert index,
+ * NaN ranks as -inf). */
+enum {
+    /* z = l (+bias); top-K of z; w = softmax over the K selected z (Mixtral) */
+    LCMOE_ROUTE_SOFTMAX_RENORM = 0,
+    /* z = l (+bias); top-K of z; w = full-E softmax(z) at the selected      */
+    LCMOE_ROUTE_SOFTMAX = 1,
+    /* s = sigmoid(l); z = s (+bias); groups of E/n_group experts scored by
+     * their top-2 z; top topk_group groups kept; top-K z inside them;
+     * w = routed_scale * s / sum(s over the K)      (DeepSeek-V3 noaux_tc)  */
+    LCMOE_ROUTE_SIGMOID_GROUP = 2
+};
+
+/* Layer descriptor.  Limits: n_expert <= 256, n_expert_used <= 16,
+ * n_shared <= 8, d_model % 256 == 0, d_ff % 32 == 0. */
+typedef struct {
+    int32_t d_model;       /* d                                           */
+    int32_t d_ff;          /* F, routed expert hidden size                */
+    int32_t n_expert;      /* E                                           */
+    int32_t n_expert_used; /* K                                           */
+    int32_t n_shared;      /* S, always-on shared experts (weight 1.0)   */
+    int32_t d_ff_shared;   /* hidden size of each shared expert           */
+    int32_t route_kind;    /* LCMOE_ROUTE_*                               */
+    int32_t n_group;       /* sigmoid-group router only                   */
+    int32_t topk_group;    /* sigmoid-group router only                   */
+    float routed_scale;    /* multiplies every routed weight (1.0 = none) */
+    int32_t has_bias;      /* bias[E] added to the selection score        */
+    int32_t type_gate, type_up, type_down;          /* LCMOE_TYPE_*     */
+    int32_t type_gate_sh, type_up_sh, type_down_sh; /* shared experts   */
+    int32_t max_tokens;    /* largest T a forward call may pass           */
+} lcmoe_desc;
+
+/* Host weight pointers, copied to the device by lcmoe_create (the caller
+ * keeps ownership).  Expert tensors use the GGUF stacked layout
+ * (ffn_{gate,up,down}_exps): expert e's [rows, cols] matrix is the e-th
+ * contiguous slice of tensor_size(type, rows*cols) bytes, quant blocks along
+ * cols (the input dimension) over the flattened matrix, exactly what
+ * GGUFile::get_tensor_raw (rust/src/model/gguf.rs:121-127) returns.
+ *   gate, up : E x [d_ff rows, d_model cols]
+ *   down     : E x [d_model rows, d_ff cols]
+ *   *_sh     : the same for the S shared experts with d_ff_shared.
+ * router is f32 [d_model, n_expert] row-major, the post-load [in,out] form
+ * produced by load_layer (rust/src/model/loader.rs:155-160). */
+typedef struct {
+    const float *router;
+    const float *bias; /* [n_expert] f32, or NULL when has_bias == 0 */
+    const uint8_t *gate, *up, *down;
+    const uint8_t *gate_sh, *up_sh, *down_sh;
+} lcmoe_weights;
+
+typedef struct lcmoe_handle lcmoe_handle;
+
+/* Validates desc, scans every block scale on the host (the per-block test of
+ * scan_for_corruption, rust/src/model/loader.rs:301-422), uploads all
+ * weights once to the current HIP device and keeps them resident.
+ * Replaces the per-forward GGUFModel::load_layer ingest
+ * (rust/src/model/loader.rs:145-168, called from engine.rs:96). */
+lcmoe_status lcmoe_create(const lcmoe_desc *desc, const lcmoe_weights *w, lcmoe_handle **out);
+void lcmoe_destroy(lcmoe_handle *h);
+
+/* y[T, d] = MoE FFN of x[T, d] (f32, host memory, row-major).  Synchronous:
+ * returns after y is written, like ffn_forward (engine.rs:146-164).  The
+ * residual add of engine.rs:115 stays with the caller.  topk_idx [T, K] and
+ * topk_w [T, K] are optional (NULL to skip).  T may be 0. */
+lcmoe_status lcmoe_forward(lcmoe_handle *h, const float *x, int32_t T, float *y,
+                           int32_t *topk_idx, float *topk_w);
+
+/* Same on device pointers, enqueued on `stream` (a hipStream_t, NULL = the
+ * handle's own stream); returns without waiting.  x_dev / y_dev must stay
+ * valid until the stream reaches this work. */
+lcmoe_status lcmoe_forward_dev(lcmoe_handle *h, const float *x_dev, int32_t T, float *y_dev,
+                               void *stream);
+
+/* Routing and dispatch of the most recent forward (waits for it):
+ * topk_idx/topk_w [T, K]; counts [E]; offsets [E+1] (exclusive scan, offsets[E]
+ * = T*K); perm [T*K]: position -> assignment a = t*K + k (stable by a within
+ * an expert); inv [T*K]: assignment -> position.  Any pointer may be NULL. */
+lcmoe_status lcmoe_get_dispatch(lcmoe_handle *h, int32_t *T_out, int32_t *topk_idx,
+                                float *topk_w, int32_t *counts, int32_t *offsets,
+                                int32_t *perm, int32_t *inv);
+
+/* Kernel timing.  When enabled, each forward records HIP events around each
+ * of its kernels on the stream it runs on; lcmoe_get_timing returns, per
+ * kernel slot, the accumulated milliseconds and launch count since the last
+ * reset (waits for the stream).  Slot names come from lcmoe_timing_name. */
+lcmoe_status lcmoe_set_timing(lcmoe_handle *h, int32_t enable);
+lcmoe_status lcmoe_get_timing(lcmoe_handle *h, int32_t n_slots, double *ms, int64_t *launches);
+const char *lcmoe_timing_name(int32_t slot);
+int32_t lcmoe_timing_slots(void);
+
+/* Per-thread message for the last non-OK status ("" if none). */
+const char *lcmoe_last_error(void);
+
+/* ---- host utilities (no GPU needed) ------------------------------------ */
+
+/* QuantType::tensor_size, rust/src/model/quant.rs:256-261 (0 if unknown). */
+size_t lcmoe_tensor_size(int32_t type, int64_t count);
+
+/* Number of blocks whose scale(s) are non-finite or |.| > 1e4
+ * (scan_for_corruption's test, rust/src/model/loader.rs:389-398). */
+int64_t lcmoe_scan_blocks(int32_t type, const uint8_t *data, int64_t count);
+
+/* Quantise f32 to GGUF blocks.  Q8_0 is quantize_f32_to_q8_0
+ * (rust/src/kernels/q8_0.rs:90-122); Q4_K and Q6_K are this project's own
+ * encoders (the reference has none).  count % block size must be 0.
+ * Multithreaded; the bytes do not depend on the thread count. */
+lcmoe_status lcmoe_quantize(int32_t type, const float *src, uint8_t *dst, int64_t count);
+
+/* Synthetic N(0, stddev^2) data: counter-based splitmix64 + Box-Muller in
+ * float64; element i depends only on (seed, stream, i). */
+void lcmoe_synth_normal(uint64_t seed, uint64_t stream, float stddev, float *out, int64_t n);
+
+/* ---- device self-tests (need a GPU; used by the parity tests) ---------- */
+
+/* Decode `count` elements of a GGUF tensor with the device decoders and
+ * return them as f32 (bit-exact with dequantize_* in kernels/mod.rs). */
+lcmoe_status lcmoe_debug_dequant(int32_t type, const uint8_t *data, int64_t count, float *out);
+/* The router's sigmoid evaluated on the device, for host/device bit parity. */
+lcmoe_status lcmoe_debug_sigmoid(const float *x, int64_t n, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,55 @@
+"""Build recipe for the product library leafcutterllm_amd/liblcmoe.so.
+
+hipcc compiles the HIP translation unit for gfx950 only; g++ compiles the
+host-only utilities.  Every build compiles from source (no caching), so a
+call always reflects the current sources.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(PKG, "csrc")
+ROOT = os.path.dirname(PKG)
+BUILD = os.path.join(ROOT, "_build")
+LIB = os.path.join(PKG, "liblcmoe.so")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.path.join(ROCM, "bin", "hipcc")
+
+HIP_FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
+    # every fused multiply-add is explicit (__builtin_fmaf); nothing else fuses
+    "-ffp-contract=off",
+    # no packed-FP32 instructions (v_pk_*_f32)
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-fno-gpu-flush-denormals-to-zero",
+    "-Wall", "-Wno-unused-function",
+]
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", "-pthread", "-Wall",
+              "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include"]
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    dev_o = os.path.join(BUILD, "lcmoe.o")
+    host_o = os.path.join(BUILD, "lcmoe_host.o")
+    _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, "lcmoe.hip"), "-o", dev_o], verbose)
+    _run(["g++", *HOST_FLAGS, "-c", os.path.join(CSRC, "lcmoe_host.cpp"), "-o", host_o], verbose)
+    tmp = LIB + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-pthread", dev_o, host_o,
+          "-o", tmp], verbose)
+    shutil.move(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

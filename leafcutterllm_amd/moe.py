@@ -1,0 +1,123 @@
+"""Host-side mirror of the reference layer API over the C ABI.
+
+`MoeFfn.ffn_forward(x) -> y` has the contract of the reference's
+Engine::ffn_forward (rust/src/inference/engine.rs:146-164): x [T, d_model]
+f32 in, y [T, d_model] f32 out, synchronous, residual add left to the caller
+(engine.rs:115).  Errors raise LcmoeError carrying the ABI status (the
+reference panics; a caller that wants that can let the exception propagate).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from ._lib import Desc, LcmoeError, Weights, check, lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+class MoeFfn:
+    """One resident MoE layer on the current HIP device."""
+
+    def __init__(self, desc: Desc, layer: dict):
+        self.desc = desc
+        w = Weights()
+        router = np.ascontiguousarray(layer["router"], np.float32)
+        keep = [router]  # the arrays must outlive lcmoe_create, which copies them
+        w.router = _ptr(router)
+        bias = layer.get("bias")
+        if bias is not None:
+            bias = np.ascontiguousarray(bias, np.float32)
+            keep.append(bias)
+        w.bias = _ptr(bias)
+        for k in ("gate", "up", "down", "gate_sh", "up_sh", "down_sh"):
+            a = layer.get(k)
+            if a is not None:
+                a = np.ascontiguousarray(a, np.uint8)
+                keep.append(a)
+            setattr(w, k, _ptr(a))
+        h = C.c_void_p()
+        check(lib().lcmoe_create(C.byref(desc), C.byref(w), C.byref(h)), "lcmoe_create")
+        self._h = h
+
+    @property
+    def handle(self) -> int:
+        return self._h.value
+
+    def ffn_forward(self, x: np.ndarray) -> np.ndarray:
+        return self.forward(x)[0]
+
+    def forward(self, x: np.ndarray):
+        """Returns (y, topk_idx, topk_w)."""
+        x = np.ascontiguousarray(x, np.float32)
+        if x.ndim != 2 or x.shape[1] != self.desc.d_model:
+            raise LcmoeError(1, "ffn_forward", f"x must be [T, {self.desc.d_model}]")
+        T, K = x.shape[0], self.desc.n_expert_used
+        y = np.empty_like(x)
+        idx = np.empty((T, K), np.int32)
+        w = np.empty((T, K), np.float32)
+        check(lib().lcmoe_forward(self._h, _ptr(x), T, _ptr(y), _ptr(idx), _ptr(w)),
+              "lcmoe_forward")
+        return y, idx, w
+
+    def forward_dev(self, x_dev: int, T: int, y_dev: int, stream: int | None = None) -> None:
+        check(lib().lcmoe_forward_dev(self._h, x_dev, T, y_dev, stream), "lcmoe_forward_dev")
+
+    def dispatch(self) -> dict:
+        E, K = self.desc.n_expert, self.desc.n_expert_used
+        T = C.c_int32()
+        check(lib().lcmoe_get_dispatch(self._h, C.byref(T), None, None, None, None, None, None),
+              "lcmoe_get_dispatch")
+        T = T.value
+        out = {
+            "topk_idx": np.empty((T, K), np.int32), "topk_w": np.empty((T, K), np.float32),
+            "counts": np.empty(E, np.int32), "offsets": np.empty(E + 1, np.int32),
+            "perm": np.empty(T * K, np.int32), "inv": np.empty(T * K, np.int32),
+        }
+        check(lib().lcmoe_get_dispatch(self._h, None, *(_ptr(out[k]) for k in (
+            "topk_idx", "topk_w", "counts", "offsets", "perm", "inv"))), "lcmoe_get_dispatch")
+        return out
+
+    def set_timing(self, on: bool) -> None:
+        check(lib().lcmoe_set_timing(self._h, 1 if on else 0), "lcmoe_set_timing")
+
+    def get_timing(self) -> dict:
+        n = lib().lcmoe_timing_slots()
+        ms = np.zeros(n, np.float64)
+        cnt = np.zeros(n, np.int64)
+        check(lib().lcmoe_get_timing(self._h, n, _ptr(ms), _ptr(cnt)), "lcmoe_get_timing")
+        return {lib().lcmoe_timing_name(i).decode(): (float(ms[i]), int(cnt[i])) for i in range(n)}
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None and self._h.value:
+            lib().lcmoe_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def debug_dequant(qtype: int, data: np.ndarray, count: int) -> np.ndarray:
+    data = np.ascontiguousarray(data, np.uint8)
+    out = np.empty(count, np.float32)
+    check(lib().lcmoe_debug_dequant(qtype, _ptr(data), count, _ptr(out)), "lcmoe_debug_dequant")
+    return out
+
+
+def debug_sigmoid(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    out = np.empty_like(x)
+    check(lib().lcmoe_debug_sigmoid(_ptr(x), x.size, _ptr(out)), "lcmoe_debug_sigmoid")
+    return out

@@ -1,0 +1,141 @@
+/*
+ * lcoracle.h -- CPU oracle for the MoE feed-forward hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker: it may be loaded by
+ * tests/, by __graft_entry__.smoke() and by bench.py's cpu_baseline leg, and by
+ * nothing else.  The product library (leafcutterllm_amd/liblcmoe.so) never
+ * links, loads or calls it.
+ *
+ * It restates, in plain C, the arithmetic of the reference Rust CPU path that
+ * the GPU path replaces (every function cites the reference file:line it
+ * follows; paths are relative to the reference repository root), plus the MoE
+ * routing / dispatch / combine semantics that the reference does not have and
+ * that this project fixes in writing (router kinds, tie rules, slot order).
+ *
+ * Pinning status per function (what checks it besides itself):
+ *   f16 <-> f32          : exhaustive vs numpy float16 (tests/test_oracle_core.py)
+ *   dequant Q8_0         : reference KAT q8_0.rs:128-149, round trip q8_0.rs:151-166
+ *   dequant Q4_K / Q6_K  : reference zero KATs kernels/mod.rs:235-251, block
+ *                          geometry quant.rs:314-335 + gguf.rs:338-346, hand-built
+ *                          layout KATs packed by an independent packer in the test
+ *   quantize Q8_0        : reference round trip q8_0.rs:151-166, KATs
+ *   quantize Q4_K / Q6_K : round-trip error <= half a quantisation step
+ *   matmul (AVX2 order)  : reference KATs simd.rs:430-455 (exact), error bound vs
+ *                          float64, FMA-lane vs mul+add-tail bit behaviour
+ *   silu / softmax       : closed form in float64, tensor.rs:211-217 KAT
+ *   lc_expf / sigmoid    : <= 2 ulp vs float64 exp over a dense sweep
+ *   top-k, group top-k   : brute force (full sort) incl. adversarial ties / NaN
+ *   dispatch             : brute-force stable sort + permutation invariants
+ *   layer forward        : float64 re-computation from dequantised weights,
+ *                          E=1,K=1 reduces to the dense ffn_forward
+ *                          (engine.rs:146-164), all-zero weights -> 0
+ */
+#ifndef LCORACLE_H
+#define LCORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGUF ggml_type codes (rust/src/model/quant.rs:45-73). */
+enum { LCO_F32 = 0, LCO_F16 = 1, LCO_Q8_0 = 8, LCO_Q4_K = 12, LCO_Q6_K = 14 };
+
+/* Router kinds. */
+enum {
+    LCO_ROUTE_SOFTMAX_RENORM = 0, /* softmax over the K selected logits      */
+    LCO_ROUTE_SOFTMAX = 1,        /* full-E softmax probs of the selected    */
+    LCO_ROUTE_SIGMOID_GROUP = 2   /* sigmoid + bias, group-limited, scaled   */
+};
+
+/* Layer descriptor; same field order and types as lcmoe_desc. */
+typedef struct {
+    int32_t d_model, d_ff, n_expert, n_expert_used;
+    int32_t n_shared, d_ff_shared;
+    int32_t route_kind, n_group, topk_group;
+    float routed_scale;
+    int32_t has_bias;
+    int32_t type_gate, type_up, type_down;
+    int32_t type_gate_sh, type_up_sh, type_down_sh;
+    int32_t max_tokens;
+} lco_desc;
+
+/* Layer weights; same field order as lcmoe_weights.  Expert tensors are the
+ * GGUF stacked layout: expert e's [rows, cols] matrix is the e-th contiguous
+ * slice of tensor_size(rows*cols) bytes; blocks run along cols (the input
+ * dimension).  gate/up: [d_ff rows, d_model cols]; down: [d_model, d_ff]. */
+typedef struct {
+    const float *router; /* [d_model, n_expert] f32, the post-load [in,out] form */
+    const float *bias;   /* [n_expert] or NULL                                    */
+    const uint8_t *gate, *up, *down;
+    const uint8_t *gate_sh, *up_sh, *down_sh;
+} lco_weights;
+
+/* ---- formats ---------------------------------------------------------- */
+float lco_f16_to_f32(uint16_t h);
+uint16_t lco_f32_to_f16(float f);
+void lco_f16_to_f32_n(const uint16_t *h, float *f, size_t n);
+void lco_f32_to_f16_n(const float *f, uint16_t *h, size_t n);
+
+size_t lco_block_size(int type);
+size_t lco_block_bytes(int type);
+size_t lco_tensor_size(int type, size_t count);
+
+void lco_dequant_q8_0(const uint8_t *src, float *dst, size_t count);
+void lco_dequant_q4_k(const uint8_t *src, float *dst, size_t count);
+void lco_dequant_q6_k(const uint8_t *src, float *dst, size_t count);
+int lco_dequant(int type, const uint8_t *src, float *dst, size_t count);
+void lco_scale_min_k4(int j, const uint8_t *q, uint8_t *sc, uint8_t *m);
+
+void lco_quantize_q8_0(const float *src, uint8_t *dst, size_t count);
+void lco_quantize_q4_k(const float *src, uint8_t *dst, size_t count);
+void lco_quantize_q6_k(const float *src, uint8_t *dst, size_t count);
+int lco_quantize(int type, const float *src, uint8_t *dst, size_t count);
+
+void lco_sanitize(float *v, size_t n);
+/* scan_for_corruption: number of blocks with a non-finite or |scale|>1e4. */
+size_t lco_scan_blocks(int type, const uint8_t *src, size_t count);
+
+/* ---- synthetic data --------------------------------------------------- */
+void lco_synth_normal(uint64_t seed, uint64_t stream, float stddev, float *out, size_t n);
+
+/* ---- arithmetic --------------------------------------------------------- */
+void lco_matmul(const float *a, const float *b, float *c, int m, int k, int n, int threads);
+void lco_transpose(const float *a, float *b, int rows, int cols);
+float lco_silu(float v);
+void lco_softmax(const float *x, float *y, int n);
+float lco_expf_cw(float x);
+float lco_sigmoid_cw(float x);
+
+/* ---- routing ---------------------------------------------------------- */
+void lco_router_logits(const float *x, const float *w, float *l, int T, int d, int E);
+int lco_route(const lco_desc *desc, const float *logits, const float *bias, int T,
+              int32_t *topk_idx, float *topk_w);
+int lco_dispatch(const int32_t *topk_idx, int T, int K, int E, int32_t *counts,
+                 int32_t *offsets, int32_t *perm, int32_t *inv);
+
+/* ---- whole layer -------------------------------------------------------- */
+/* y[T, d] = MoE FFN of x[T, d].  Optional outputs may be NULL.  Weights are
+ * dequantised one expert at a time (dequant -> transpose -> sanitize, as
+ * loader.rs:145-168 does per tensor).  threads<=0 -> reference row split. */
+int lco_moe_forward(const lco_desc *desc, const lco_weights *w, const float *x, int T,
+                    float *y, int32_t *topk_idx, float *topk_w, int32_t *counts,
+                    int32_t *offsets, int32_t *perm, int32_t *inv, int threads);
+
+/* Dense SwiGLU FFN on f32 weights in the post-load [in,out] layout:
+ * y = (silu(x Wg) * (x Wu)) Wd, engine.rs:146-164. */
+void lco_ffn_dense(const float *x, int m, int d, int F, const float *wg_t,
+                   const float *wu_t, const float *wd_t, float *y, int threads);
+
+/* CPU baseline: experts pre-dequantised to f32 (post-load layout) once,
+ * then timed forwards.  Returns an opaque handle. */
+void *lco_resident_create(const lco_desc *desc, const lco_weights *w, int threads);
+int lco_resident_forward(void *h, const float *x, int T, float *y, int threads);
+void lco_resident_destroy(void *h);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

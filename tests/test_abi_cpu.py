@@ -1,0 +1,144 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol
+include/lcmoe.h declares, rejects bad descriptors and corrupt weights before
+touching a device, and its host encoders / generator reproduce the oracle's
+bytes."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+import lcoracle as O
+import leafcutterllm_amd as L
+from leafcutterllm_amd import _lib
+from leafcutterllm_amd.configs import quantize, synth_normal
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    txt = open(os.path.join(ROOT, "include", "lcmoe.h")).read()
+    return sorted(set(re.findall(r"\b(lcmoe_[a-z_]+)\s*\(", txt)))
+
+
+def test_exports_every_declared_symbol():
+    syms = header_symbols()
+    assert len(syms) >= 16
+    lib = C.CDLL(_lib.LIB_PATH)
+    for s in syms:
+        assert hasattr(lib, s), s
+    assert sorted(_lib.EXPORTS) == syms
+
+
+def test_desc_layout_matches_oracle():
+    assert C.sizeof(L.Desc) == C.sizeof(O.Desc) == 18 * 4
+    assert [f[0] for f in L.Desc._fields_] == [f[0] for f in O.Desc._fields_]
+
+
+def test_tensor_size_and_scan_match_oracle():
+    for qt in (L.TYPE_Q8_0, L.TYPE_Q4_K, L.TYPE_Q6_K, L.TYPE_F32):
+        for n in (256, 512, 2048 * 1408, 4096 * 14336):
+            assert L.lib().lcmoe_tensor_size(qt, n) == O.tensor_size(qt, n)
+    x = synth_normal(1, 2, 0.02, 256 * 8)
+    for qt in (L.TYPE_Q8_0, L.TYPE_Q4_K, L.TYPE_Q6_K):
+        b = quantize(qt, x)
+        bb = b.copy()
+        off = 208 if qt == L.TYPE_Q6_K else 0
+        bb[off:off + 2] = np.frombuffer(np.array([np.inf], np.float16).tobytes(), np.uint8)
+        for data in (b, bb):
+            assert L.lib().lcmoe_scan_blocks(qt, data.ctypes.data, x.size) == \
+                O.scan_blocks(qt, data, x.size)
+        assert L.lib().lcmoe_scan_blocks(qt, bb.ctypes.data, x.size) == 1
+
+
+@pytest.mark.parametrize("qt", [L.TYPE_Q8_0, L.TYPE_Q4_K, L.TYPE_Q6_K])
+def test_product_encoder_bytes_equal_oracle(qt):
+    x = synth_normal(7, 3, 0.02, 256 * 200)
+    x[:256] *= 1e-6
+    x[256:512] = 0.0
+    x[512:768] = np.abs(x[512:768])
+    assert np.array_equal(quantize(qt, x), O.quantize(qt, x))
+
+
+def test_product_generator_equals_oracle():
+    n = 100_003
+    assert np.array_equal(synth_normal(42, 7 << 32, 0.02, n), O.synth_normal(42, 7 << 32, 0.02, n))
+
+
+def _layer(cfg):
+    return L.synth_layer(cfg, seed=1)
+
+
+def _create(desc, layer):
+    w = L.Weights()
+    keep = []
+    for k in ("router", "bias", "gate", "up", "down", "gate_sh", "up_sh", "down_sh"):
+        a = layer.get(k)
+        if a is not None:
+            keep.append(a)
+        setattr(w, k, None if a is None else a.ctypes.data)
+    h = C.c_void_p()
+    st = L.lib().lcmoe_create(C.byref(desc), C.byref(w), C.byref(h))
+    if st == 0:
+        L.lib().lcmoe_destroy(h)
+    return st, L.lib().lcmoe_last_error().decode()
+
+
+SMALL = L.configs.small_config("abi", 256, 256, 8, 2, L.ROUTE_SOFTMAX_RENORM, L.TYPE_Q4_K,
+                               L.TYPE_Q4_K)
+
+
+@pytest.mark.parametrize("field,value,status", [
+    ("d_model", 100, 1), ("d_model", 0, 1), ("d_ff", 33, 1), ("n_expert", 0, 1),
+    ("n_expert", 257, 1), ("n_expert_used", 0, 1), ("n_expert_used", 9, 1),
+    ("route_kind", 7, 2), ("type_gate", 2, 2), ("type_down", 99, 2), ("max_tokens", 0, 1),
+    ("n_shared", 9, 1), ("routed_scale", float("nan"), 1),
+])
+def test_create_rejects_bad_desc(field, value, status):
+    layer = _layer(SMALL)
+    d = SMALL.desc(4)
+    setattr(d, field, value)
+    st, msg = _create(d, layer)
+    assert st == status and msg
+
+
+def test_create_rejects_bad_group_router():
+    cfg = L.configs.small_config("g", 256, 256, 32, 8, L.ROUTE_SIGMOID_GROUP, L.TYPE_Q4_K,
+                                 L.TYPE_Q4_K, n_group=5, topk_group=2)
+    st, msg = _create(cfg.desc(4), _layer(L.configs.small_config(
+        "g2", 256, 256, 32, 8, L.ROUTE_SOFTMAX, L.TYPE_Q4_K, L.TYPE_Q4_K)))
+    assert st == 1 and "n_group" in msg
+
+
+def test_create_rejects_corrupt_block_and_null():
+    layer = _layer(SMALL)
+    bad = dict(layer)
+    bad["down"] = layer["down"].copy()
+    sz = L.configs.tensor_size(L.TYPE_Q4_K, 256 * 256)
+    bad["down"][3 * sz + 144 * 5 + 2: 3 * sz + 144 * 5 + 4] = np.frombuffer(
+        np.array([np.nan], np.float16).tobytes(), np.uint8)
+    st, msg = _create(SMALL.desc(4), bad)
+    assert st == 3 and "down[3]" in msg
+    bad = dict(layer)
+    bad["gate"] = None
+    st, msg = _create(SMALL.desc(4), bad)
+    assert st == 1 and "gate" in msg
+    d = SMALL.desc(4)
+    d.has_bias = 1
+    st, msg = _create(d, layer)
+    assert st == 1 and "bias" in msg
+
+
+def test_create_without_gpu_fails_cleanly_or_succeeds():
+    st, msg = _create(SMALL.desc(4), _layer(SMALL))
+    assert st in (0, 4)
+    if st == 4:
+        assert "device" in msg
+
+
+def test_quantize_errors():
+    x = np.zeros(33, np.float32)
+    out = np.zeros(64, np.uint8)
+    assert L.lib().lcmoe_quantize(L.TYPE_Q8_0, x.ctypes.data, out.ctypes.data, 33) == 1
+    assert L.lib().lcmoe_quantize(3, x.ctypes.data, out.ctypes.data, 32) == 2

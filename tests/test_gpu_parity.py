@@ -1,0 +1,188 @@
+"""GPU parity: the HIP path through the C ABI against the CPU oracle.
+
+Bar: topk_idx / counts / offsets / perm / inv bit-identical; routed weights
+within 1e-5 relative; layer output within 1e-3 relative L2 over [T, d];
+device decoders and the router sigmoid bit-identical to the oracle.
+"""
+import numpy as np
+import pytest
+
+import lcoracle as O
+import leafcutterllm_amd as L
+from kquant_pack import pack_q4_k, pack_q6_k, pack_q8_0
+from leafcutterllm_amd.configs import small_config
+from parity_util import oracle_desc, rel_l2, run_and_check
+
+pytestmark = pytest.mark.gpu
+
+Q4, Q6, Q8 = L.TYPE_Q4_K, L.TYPE_Q6_K, L.TYPE_Q8_0
+
+
+def u8(b):
+    return np.frombuffer(b, np.uint8).copy()
+
+
+# ----------------------------------------------------------- decoders ------
+
+@pytest.mark.parametrize("qtype", [Q8, Q4, Q6])
+def test_device_decoder_bit_exact(qtype):
+    x = L.configs.synth_normal(3, 9, 0.02, 256 * 96)
+    x[:256] *= 1e-6   # tiny scales: f16 subnormal d
+    x[256:512] *= 300.0
+    data = L.configs.quantize(qtype, x)
+    dev = L.debug_dequant(qtype, data, x.size)
+    ref = O.dequant(qtype, data, x.size)
+    assert np.array_equal(dev.view(np.uint32), ref.view(np.uint32))
+
+
+def test_device_decoder_hand_built_blocks():
+    rng = np.random.default_rng(5)
+    q4 = b"".join(pack_q4_k(float(d), float(m), rng.integers(0, 64, 8), rng.integers(0, 64, 8),
+                            rng.integers(0, 16, 256))
+                  for d, m in [(1.0, 0.5), (6e-8, 3e-5), (0.01, 0.0), (-0.25, -1.0)])
+    q6 = b"".join(pack_q6_k(float(d), rng.integers(-128, 128, 16), rng.integers(-32, 32, 256))
+                  for d in [1.0, 6e-8, -0.5])
+    q8 = b"".join(pack_q8_0(float(d), rng.integers(-128, 128, 32)) for d in [0.5, -3e-6, 100.0])
+    for qt, blob, n in [(Q4, q4, 4 * 256), (Q6, q6, 3 * 256), (Q8, q8, 3 * 32)]:
+        dev = L.debug_dequant(qt, u8(blob), n)
+        ref = O.dequant(qt, u8(blob), n)
+        assert np.array_equal(dev.view(np.uint32), ref.view(np.uint32)), qt
+
+
+def test_device_sigmoid_bit_exact():
+    x = np.concatenate([np.linspace(-110, 110, 150001, dtype=np.float32),
+                        np.linspace(-1, 1, 50001, dtype=np.float32),
+                        np.array([0.0, -0.0, np.inf, -np.inf, 88.7, -88.7, 1e-30], np.float32)])
+    dev = L.debug_sigmoid(x)
+    ref = O.sigmoid_cw(x)
+    assert np.array_equal(dev.view(np.uint32), ref.view(np.uint32))
+
+
+# ------------------------------------------------------- small layers ------
+
+SMALL = {
+    "q4k-renorm": small_config("q4k-renorm", 256, 512, 8, 2, L.ROUTE_SOFTMAX_RENORM, Q4, Q4),
+    "q8-renorm": small_config("q8-renorm", 256, 384, 8, 2, L.ROUTE_SOFTMAX_RENORM, Q8, Q8),
+    "q4k-straddle-shared-bias": small_config(
+        "q4k-straddle", 256, 352, 12, 3, L.ROUTE_SOFTMAX, Q4, Q4, n_shared=2, d_ff_shared=352,
+        bias="plus2_first8"),
+    "sigmoid-group-q6k": small_config(
+        "sig", 512, 256, 32, 4, L.ROUTE_SIGMOID_GROUP, Q4, Q6, n_shared=1, d_ff_shared=256,
+        n_group=4, topk_group=2, routed_scale=2.5, bias="normal0.1"),
+    "e60-tail": small_config("e60", 256, 256, 60, 4, L.ROUTE_SOFTMAX, Q4, Q4),
+    "q6k-all": small_config("q6", 512, 512, 16, 8, L.ROUTE_SOFTMAX_RENORM, Q6, Q6),
+    "f32": small_config("f32", 128, 256, 4, 2, L.ROUTE_SOFTMAX_RENORM, L.TYPE_F32, L.TYPE_F32),
+}
+
+
+@pytest.mark.parametrize("name", sorted(SMALL))
+@pytest.mark.parametrize("T", [1, 3, 8, 17, 64])
+def test_small_layer_parity(name, T):
+    cfg = SMALL[name]
+    layer = L.synth_layer(cfg, seed=11)
+    x = L.synth_x(cfg, T, seed=11, index=T)
+    res = run_and_check(cfg, layer, x)
+    assert res["rel_l2"] < 1e-3
+
+
+def test_handle_reuse_and_determinism():
+    cfg = SMALL["sigmoid-group-q6k"]
+    layer = L.synth_layer(cfg, seed=2)
+    with L.MoeFfn(cfg.desc(64), layer) as moe:
+        for T in (64, 5, 1, 64, 0, 33):
+            x = L.synth_x(cfg, T, seed=2, index=100 + T)
+            if T == 0:
+                y, idx, w = moe.forward(x.reshape(0, cfg.d_model))
+                assert y.shape == (0, cfg.d_model)
+                continue
+            r1 = run_and_check(cfg, layer, x, moe=moe)
+            y2, idx2, _ = moe.forward(x)
+            assert np.array_equal(r1["y"], y2)          # run-to-run bit identical
+            assert np.array_equal(r1["topk_idx"], idx2)
+
+
+def test_adversarial_router_ties():
+    """Equal logits, +-0, -inf and NaN inputs: ties go to the lower expert."""
+    cfg = small_config("ties", 256, 256, 16, 4, L.ROUTE_SOFTMAX_RENORM, Q4, Q4)
+    layer = L.synth_layer(cfg, seed=4)
+    r = np.zeros((256, 16), np.float32)
+    r[0, :] = 1.0          # x[:,0] drives all logits equally
+    r[1, 3] = r[1, 9] = 1.0
+    layer["router"] = r
+    x = np.zeros((8, 256), np.float32)
+    x[0, 0] = 1.0                    # all equal -> experts 0..3
+    x[1, 1] = 2.0                    # 3 and 9 lead, then ties -> 0, 1
+    x[2, 0] = -0.0                   # all zero
+    x[3, 0] = np.inf                 # all +inf, ties -> 0..3
+    x[4, 0] = -np.inf                # all -inf
+    x[5, 0] = np.nan                 # all NaN -> ranks as -inf, 0..3
+    x[6, 0], x[6, 1] = 1.0, -1.0     # logits 1 except 3, 9 at 0
+    x[7, 1] = 1e-30
+    moe = L.MoeFfn(cfg.desc(8), layer)
+    try:
+        _, idx, _ = moe.forward(x)
+        od = oracle_desc(cfg.desc(8))
+        with np.errstate(all="ignore"):
+            r_idx, _ = O.route(od, O.router_logits(x, r))
+        assert np.array_equal(idx, r_idx)
+        assert list(idx[0]) == [0, 1, 2, 3] and list(idx[1]) == [3, 9, 0, 1]
+        disp = moe.dispatch()
+        counts, offsets, perm, inv = O.dispatch(r_idx, 16)
+        assert np.array_equal(disp["perm"], perm) and np.array_equal(disp["inv"], inv)
+    finally:
+        moe.close()
+
+
+def test_e1_k1_reduces_to_dense_ffn():
+    """E = 1, K = 1, renormalised: weight exactly 1.0 and the layer is the
+    dense SwiGLU ffn_forward (engine.rs:146-164) of the one expert."""
+    cfg = small_config("dense", 256, 512, 1, 1, L.ROUTE_SOFTMAX_RENORM, Q4, Q4)
+    layer = L.synth_layer(cfg, seed=8)
+    x = L.synth_x(cfg, 9, seed=8)
+    with L.MoeFfn(cfg.desc(9), layer) as moe:
+        y, idx, w = moe.forward(x)
+    assert np.all(idx == 0) and np.all(w == 1.0)
+    wg = O.dequant(Q4, layer["gate"], 512 * 256).reshape(512, 256).T
+    wu = O.dequant(Q4, layer["up"], 512 * 256).reshape(512, 256).T
+    wd = O.dequant(Q4, layer["down"], 256 * 512).reshape(256, 512).T
+    ref = O.ffn_dense(x, wg, wu, wd)
+    assert rel_l2(y, ref) < 1e-5
+
+
+# ------------------------------------------------- full BASELINE shapes -----
+
+FULL_T = [(1, 1), (1, 16), (2, 1), (2, 8), (2, 64), (5, 1), (5, 16)]
+
+
+@pytest.fixture(scope="module")
+def full_layers():
+    cache = {}
+
+    def get(c):
+        if c not in cache:
+            cache.clear()
+            cfg = L.CONFIGS[c]
+            layer = L.synth_layer(cfg, seed=0)
+            cache[c] = (cfg, layer, L.MoeFfn(cfg.desc(max(cfg.tokens + (64,))), layer))
+        return cache[c]
+    yield get
+    for v in cache.values():
+        v[2].close()
+
+
+@pytest.mark.parametrize("c,T", FULL_T)
+def test_full_config_parity(full_layers, c, T):
+    cfg, layer, moe = full_layers(c)
+    x = L.synth_x(cfg, T, seed=0, index=T)
+    subset = None if T <= 16 else [0, T // 3, T - 1]
+    res = run_and_check(cfg, layer, x, moe=moe, y_subset=subset)
+    print(f"config {c} T={T}: rel_l2={res['rel_l2']:.2e} touched={int((res['counts'] > 0).sum())}")
+
+
+def test_full_config3_prefill_parity(full_layers):
+    cfg, layer, moe = full_layers(3)
+    x = L.synth_x(cfg, 2048, seed=0, index=2048)
+    res = run_and_check(cfg, layer, x, moe=moe, y_subset=[0, 1, 777, 2047])
+    counts = res["counts"]
+    assert counts[:8].sum() > counts[8:].sum()   # the +2.0 bias skews routing
+    print(f"config 3 T=2048: rel_l2={res['rel_l2']:.2e} biased-share={counts[:8].sum() / counts.sum():.2f}")
