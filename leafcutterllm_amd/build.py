@@ -40,12 +40,16 @@ def _run(cmd, verbose):
 
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
-    dev_o = os.path.join(BUILD, "lcmoe.o")
+    objs = []
+    for src in sorted(os.listdir(CSRC)):
+        if src.endswith(".hip"):
+            o = os.path.join(BUILD, src[:-4] + ".o")
+            _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", o], verbose)
+            objs.append(o)
     host_o = os.path.join(BUILD, "lcmoe_host.o")
-    _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, "lcmoe.hip"), "-o", dev_o], verbose)
     _run(["g++", *HOST_FLAGS, "-c", os.path.join(CSRC, "lcmoe_host.cpp"), "-o", host_o], verbose)
     tmp = LIB + ".tmp"
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-pthread", dev_o, host_o,
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-pthread", *objs, host_o,
           "-o", tmp], verbose)
     shutil.move(tmp, LIB)
     return LIB

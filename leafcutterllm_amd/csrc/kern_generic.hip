@@ -1,0 +1,202 @@
+// Generic expert products on GGUF-layout tensors (any supported quant type,
+// any shape, including rows that straddle super-blocks), the combine, and the
+// device decoder self-test.
+//
+// Each wave owns kRB/4 output rows; its lanes stride the input dimension 8
+// elements at a time, decode those weights to registers (Dec<QT>, bit-exact
+// with the reference decoders) and accumulate up to kNT tokens in f32, then
+// reduce across the wave.  This is the correctness path for shapes the
+// specialised kernels do not cover; it re-reads each weight row once per
+// kNT tokens from L2.
+
+#include "device_common.h"
+#include "kernels.h"
+
+namespace lcmoe {
+namespace {
+
+constexpr int kRB = 16;  // output rows per block (4 per wave)
+constexpr int kNT = 4;   // tokens per pass
+
+template <int QT>
+__global__ __launch_bounds__(256) void k_gateup(const uint8_t *__restrict__ gate,
+                                                const uint8_t *__restrict__ up, int64_t estride,
+                                                const float *__restrict__ x, SlotArgs sa, int d,
+                                                int F, float *__restrict__ H) {
+    int e, p0, n;
+    if (!slot_info(sa, blockIdx.y, e, p0, n)) return;
+    const uint8_t *G = gate + (int64_t)e * estride, *U = up + (int64_t)e * estride;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int ng = d >> 3;
+    for (int r = 0; r < kRB / 4; r++) {
+        const int f = blockIdx.x * kRB + wave * (kRB / 4) + r;
+        if (f >= F) break;
+        const int64_t rowbase = (int64_t)f * d;
+        for (int c = 0; c < n; c += kNT) {
+            const float *xr[kNT];
+#pragma unroll
+            for (int t = 0; t < kNT; t++) {
+                int q = min(c + t, n - 1);
+                xr[t] = x + (int64_t)slot_token(sa, p0, q) * d;
+            }
+            float ag[kNT] = {}, au[kNT] = {};
+            for (int g = lane; g < ng; g += 64) {
+                float wg[8], wu[8];
+                Dec<QT>::run(G, rowbase + 8 * g, wg);
+                Dec<QT>::run(U, rowbase + 8 * g, wu);
+#pragma unroll
+                for (int t = 0; t < kNT; t++) {
+                    const float4 *xp = reinterpret_cast<const float4 *>(xr[t] + 8 * g);
+                    float4 a = xp[0], b = xp[1];
+                    float xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        ag[t] = __builtin_fmaf(wg[i], xv[i], ag[t]);
+                        au[t] = __builtin_fmaf(wu[i], xv[i], au[t]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < kNT; t++) {
+                float gs = wave_sum(ag[t]), us = wave_sum(au[t]);
+                if (lane == 0 && c + t < n) H[(int64_t)(p0 + c + t) * F + f] = silu(gs) * us;
+            }
+        }
+    }
+}
+
+template <int QT>
+__global__ __launch_bounds__(256) void k_down(const uint8_t *__restrict__ down, int64_t estride,
+                                              const float *__restrict__ H, SlotArgs sa, int d,
+                                              int F, float *__restrict__ Y) {
+    int e, p0, n;
+    if (!slot_info(sa, blockIdx.y, e, p0, n)) return;
+    const uint8_t *W = down + (int64_t)e * estride;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int ng = F >> 3;
+    for (int r = 0; r < kRB / 4; r++) {
+        const int row = blockIdx.x * kRB + wave * (kRB / 4) + r;
+        if (row >= d) break;
+        const int64_t rowbase = (int64_t)row * F;
+        for (int c = 0; c < n; c += kNT) {
+            float acc[kNT] = {};
+            for (int g = lane; g < ng; g += 64) {
+                float w[8];
+                Dec<QT>::run(W, rowbase + 8 * g, w);
+#pragma unroll
+                for (int t = 0; t < kNT; t++) {
+                    int q = min(c + t, n - 1);
+                    const float4 *hp =
+                        reinterpret_cast<const float4 *>(H + (int64_t)(p0 + q) * F + 8 * g);
+                    float4 a = hp[0], b = hp[1];
+                    float hv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                    for (int i = 0; i < 8; i++) acc[t] = __builtin_fmaf(w[i], hv[i], acc[t]);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < kNT; t++) {
+                float s = wave_sum(acc[t]);
+                if (lane == 0 && c + t < n) Y[(int64_t)(p0 + c + t) * d + row] = s;
+            }
+        }
+    }
+}
+
+// y[t] = sum_k w[t,k] * (sum over splits Yr[s][inv[t*K+k]]) + shared terms,
+// slot order then shared order; each term rounded then added.
+__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ Yr, int ks_r,
+                                                 int64_t stride_r, const float *__restrict__ Ys,
+                                                 int ks_s, int64_t stride_s,
+                                                 const int32_t *__restrict__ inv,
+                                                 const float *__restrict__ topk_w, int T, int K,
+                                                 int S, int d, float *__restrict__ y) {
+    const int t = blockIdx.x;
+    __shared__ int s_pos[kMaxK];
+    __shared__ float s_w[kMaxK];
+    if (threadIdx.x < K) {
+        s_pos[threadIdx.x] = inv[(int64_t)t * K + threadIdx.x];
+        s_w[threadIdx.x] = topk_w[(int64_t)t * K + threadIdx.x];
+    }
+    __syncthreads();
+    for (int c = threadIdx.x; c < d; c += blockDim.x) {
+        float acc = 0.0f;
+        for (int k = 0; k < K; k++) {
+            const float *src = Yr + (int64_t)s_pos[k] * d + c;
+            float v = src[0];
+            for (int s = 1; s < ks_r; s++) v = v + src[s * stride_r];
+            float p = s_w[k] * v;
+            acc = acc + p;
+        }
+        for (int j = 0; j < S; j++) {
+            const float *src = Ys + ((int64_t)j * T + t) * d + c;
+            float v = src[0];
+            for (int s = 1; s < ks_s; s++) v = v + src[s * stride_s];
+            acc = acc + v;
+        }
+        y[(int64_t)t * d + c] = acc;
+    }
+}
+
+template <int QT>
+__global__ void k_debug_dequant(const uint8_t *__restrict__ src, int64_t count,
+                                float *__restrict__ out) {
+    int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (8 * g >= count) return;
+    float o[8];
+    Dec<QT>::run(src, 8 * g, o);
+    for (int i = 0; i < 8; i++) out[8 * g + i] = o[i];
+}
+
+template <template <int> class K, class... Args>
+hipError_t launch_typed(int qt, dim3 grid, dim3 block, hipStream_t st, Args... args) {
+    switch (qt) {
+    case LCMOE_TYPE_F32: hipLaunchKernelGGL(K<LCMOE_TYPE_F32>::fn, grid, block, 0, st, args...); break;
+    case LCMOE_TYPE_Q8_0: hipLaunchKernelGGL(K<LCMOE_TYPE_Q8_0>::fn, grid, block, 0, st, args...); break;
+    case LCMOE_TYPE_Q4_K: hipLaunchKernelGGL(K<LCMOE_TYPE_Q4_K>::fn, grid, block, 0, st, args...); break;
+    case LCMOE_TYPE_Q6_K: hipLaunchKernelGGL(K<LCMOE_TYPE_Q6_K>::fn, grid, block, 0, st, args...); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int QT> struct GateUpK { static constexpr auto fn = k_gateup<QT>; };
+template <int QT> struct DownK { static constexpr auto fn = k_down<QT>; };
+template <int QT> struct DeqK { static constexpr auto fn = k_debug_dequant<QT>; };
+
+SlotArgs dev_slots(const SlotArgsHost &s) {
+    return SlotArgs{s.perm, s.counts, s.offsets, s.touched, s.E, s.K, s.T, s.shared};
+}
+
+}  // namespace
+
+hipError_t launch_generic_gateup(int qt, const uint8_t *gate, const uint8_t *up, int64_t estride,
+                                 const float *x, const SlotArgsHost &sa, int slots, int d, int F,
+                                 float *Hf, int8_t *, int8_t *, float *, float *, hipStream_t st) {
+    return launch_typed<GateUpK>(qt, dim3((F + kRB - 1) / kRB, slots), dim3(256), st, gate, up,
+                                 estride, x, dev_slots(sa), d, F, Hf);
+}
+
+hipError_t launch_generic_down(int qt, const uint8_t *down, int64_t estride, const float *Hf,
+                               const SlotArgsHost &sa, int slots, int d, int F, float *Y,
+                               hipStream_t st) {
+    return launch_typed<DownK>(qt, dim3((d + kRB - 1) / kRB, slots), dim3(256), st, down, estride,
+                               Hf, dev_slots(sa), d, F, Y);
+}
+
+hipError_t launch_combine(const float *Yr, int ks_r, int64_t stride_r, const float *Ys, int ks_s,
+                          int64_t stride_s, const int32_t *inv, const float *topk_w, int T, int K,
+                          int S, int d, float *y, hipStream_t st) {
+    hipLaunchKernelGGL(k_combine, dim3(T), dim3(256), 0, st, Yr, ks_r, stride_r, Ys, ks_s,
+                       stride_s, inv, topk_w, T, K, S, d, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_debug_dequant(int qt, const uint8_t *src, int64_t count, float *out,
+                                hipStream_t st) {
+    int64_t groups = count / 8;
+    return launch_typed<DeqK>(qt, dim3((unsigned)((groups + 255) / 256)), dim3(256), st, src, count,
+                              out);
+}
+
+}  // namespace lcmoe

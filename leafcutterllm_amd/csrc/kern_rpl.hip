@@ -1,0 +1,322 @@
+// Decode-regime expert products for Q4_K weights in the RPL64 layout.
+//
+// RPL64: a Q4_K matrix [rows, cols] is stored as 64-row tiles; inside a tile,
+// for each 256-column super-block kb, its 144-byte blocks are split into nine
+// 16-byte chunks and chunk c of the 64 rows is contiguous (1 KB):
+//   byte offset = ((tile * NB + kb) * 9 + c) * 1024 + row_in_tile * 16.
+// A wave owns one tile, one lane one row, so each 16-byte load instruction
+// moves 1 KB of contiguous HBM.  The byte count equals the GGUF tensor's.
+//
+// Activations arrive as two int8 limbs per 32-element sub-block
+// (v ~= s * (128*hi + lo), exact to 1/32512 of the sub-block's max|v|), with
+// s and s*sum(128*hi+lo) per sub-block.  They are wave-uniform (every lane of
+// the wave needs the same token and columns), so they are scalar loads and
+// v_dot4 takes them as its SGPR operand.  With q the 4-bit quants of a
+// sub-block j of a row, d*sc_j and dmin*m_j its scale and min:
+//   sum_k w_k v_k = (d*sc_j) * s * sum_k q_k (128*hi_k + lo_k) - (dmin*m_j) * s*sum(...)
+// The integer part is exact (|.| < 2^24); only the last two products round.
+//
+// The four waves of a block split the super-blocks of the row; their partial
+// sums meet in LDS in a fixed order, so results are deterministic.
+
+#include "device_common.h"
+#include "kernels.h"
+
+namespace lcmoe {
+namespace {
+
+constexpr int kWaves = 4;
+
+__device__ __forceinline__ void unpack_hdr(uint4 h, float (&dl)[8], float (&ml)[8]) {
+    const float d = dh2f(h.x & 0xffff), dmin = dh2f(h.x >> 16);
+    // get_scale_min_k4 (rust/src/kernels/mod.rs:54-63) for all 8 sub-blocks
+    const uint32_t sc03 = h.y & 0x3F3F3F3Fu, m03 = h.z & 0x3F3F3F3Fu;
+    const uint32_t sc47 = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+    const uint32_t m47 = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        dl[i] = d * (float)((sc03 >> (8 * i)) & 0xffu);
+        dl[4 + i] = d * (float)((sc47 >> (8 * i)) & 0xffu);
+        ml[i] = dmin * (float)((m03 >> (8 * i)) & 0xffu);
+        ml[4 + i] = dmin * (float)((m47 >> (8 * i)) & 0xffu);
+    }
+}
+
+// One 256-element super-block of this lane's row against NT token rows.
+// xh/xl point at the tokens' limbs for this super-block (as ints), xs/xm at
+// their 8 sub-block scales / quantised sums.
+template <int NT>
+__device__ __forceinline__ void q4_block_dot(const uint4 (&c)[9], const int *const (&xh)[NT],
+                                             const int *const (&xl)[NT],
+                                             const float *const (&xs)[NT],
+                                             const float *const (&xm)[NT], float (&acc)[NT]) {
+    float dl[8], ml[8];
+    unpack_hdr(c[0], dl, ml);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint4 a = c[1 + 2 * j], b = c[2 + 2 * j];
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        int lo[8], hi[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            lo[i] = (int)(w[i] & 0x0F0F0F0Fu);
+            hi[i] = (int)((w[i] >> 4) & 0x0F0F0F0Fu);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const int *ph = xh[t] + 16 * j, *pl = xl[t] + 16 * j;
+            int sh0 = 0, sl0 = 0, sh1 = 0, sl1 = 0;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                sh0 = __builtin_amdgcn_sdot4(lo[i], ph[i], sh0, false);
+                sl0 = __builtin_amdgcn_sdot4(lo[i], pl[i], sl0, false);
+                sh1 = __builtin_amdgcn_sdot4(hi[i], ph[8 + i], sh1, false);
+                sl1 = __builtin_amdgcn_sdot4(hi[i], pl[8 + i], sl1, false);
+            }
+            const float f0 = (float)(sh0 * 128 + sl0), f1 = (float)(sh1 * 128 + sl1);
+            acc[t] = __builtin_fmaf(dl[2 * j] * xs[t][2 * j], f0, acc[t]);
+            acc[t] = __builtin_fmaf(-ml[2 * j], xm[t][2 * j], acc[t]);
+            acc[t] = __builtin_fmaf(dl[2 * j + 1] * xs[t][2 * j + 1], f1, acc[t]);
+            acc[t] = __builtin_fmaf(-ml[2 * j + 1], xm[t][2 * j + 1], acc[t]);
+        }
+    }
+}
+
+struct Limbs {
+    const int8_t *h, *l;
+    const float *s, *m;
+    int len;  // row length (elements) of the limb arrays
+};
+
+template <int NT>
+__device__ __forceinline__ void token_ptrs(const Limbs &X, const int (&row)[NT], int kb,
+                                           const int *(&xh)[NT], const int *(&xl)[NT],
+                                           const float *(&xs)[NT], const float *(&xm)[NT]) {
+    const int nsb = X.len >> 5;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const int64_t off = (int64_t)row[t] * X.len + 256 * kb;
+        xh[t] = reinterpret_cast<const int *>(X.h + off);
+        xl[t] = reinterpret_cast<const int *>(X.l + off);
+        xs[t] = X.s + (int64_t)row[t] * nsb + 8 * kb;
+        xm[t] = X.m + (int64_t)row[t] * nsb + 8 * kb;
+    }
+}
+
+// gate and up rows of this lane over super-blocks [kb0, kb1).
+template <int NT>
+__device__ __forceinline__ void pass2(const uint4 *__restrict__ G, const uint4 *__restrict__ U,
+                                      int kb0, int kb1, const Limbs &X, const int (&row)[NT],
+                                      float (&ag)[NT], float (&au)[NT]) {
+    for (int kb = kb0; kb < kb1; kb++) {
+        uint4 cg[9], cu[9];
+        const uint4 *pg = G + (int64_t)kb * 9 * 64, *pu = U + (int64_t)kb * 9 * 64;
+#pragma unroll
+        for (int i = 0; i < 9; i++) {
+            cg[i] = pg[i * 64];
+            cu[i] = pu[i * 64];
+        }
+        const int *xh[NT], *xl[NT];
+        const float *xs[NT], *xm[NT];
+        token_ptrs<NT>(X, row, kb, xh, xl, xs, xm);
+        q4_block_dot<NT>(cg, xh, xl, xs, xm, ag);
+        q4_block_dot<NT>(cu, xh, xl, xs, xm, au);
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void pass1(const uint4 *__restrict__ W, int kb0, int kb1,
+                                      const Limbs &X, const int (&row)[NT], float (&acc)[NT]) {
+    for (int kb = kb0; kb < kb1; kb++) {
+        uint4 cw[9];
+        const uint4 *pw = W + (int64_t)kb * 9 * 64;
+#pragma unroll
+        for (int i = 0; i < 9; i++) cw[i] = pw[i * 64];
+        const int *xh[NT], *xl[NT];
+        const float *xs[NT], *xm[NT];
+        token_ptrs<NT>(X, row, kb, xh, xl, xs, xm);
+        q4_block_dot<NT>(cw, xh, xl, xs, xm, acc);
+    }
+}
+
+struct HOut {
+    float *f;       // H f32 [positions, F] or null
+    int8_t *h, *l;  // H limbs [positions, F] or null
+    float *s, *m;   // [positions, F/32]
+};
+
+// Token rows c .. c+NT-1 of one gate/up tile: partial sums of the 4 waves
+// meet in LDS; wave t finishes token t (SwiGLU, then H out).
+template <int NT>
+__device__ __forceinline__ void gateup_chunk(const uint4 *G, const uint4 *U, int kb0, int kb1,
+                                             const Limbs &X, const SlotArgs &sa, int p0, int n,
+                                             int c, int F, int f, const HOut &out,
+                                             float (*s_red)[2][4][64]) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    int row[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) row[t] = __builtin_amdgcn_readfirstlane(slot_token(sa, p0, c + t));
+    float ag[NT], au[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) ag[t] = au[t] = 0.0f;
+    pass2<NT>(G, U, kb0, kb1, X, row, ag, au);
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        s_red[wave][0][t][lane] = ag[t];
+        s_red[wave][1][t][lane] = au[t];
+    }
+    __syncthreads();
+    if (wave < NT) {
+        const int t = wave;
+        float g = s_red[0][0][t][lane], u = s_red[0][1][t][lane];
+#pragma unroll
+        for (int w = 1; w < kWaves; w++) {
+            g = g + s_red[w][0][t][lane];
+            u = u + s_red[w][1][t][lane];
+        }
+        const float h = silu(g) * u;
+        const int64_t p = p0 + c + t;
+        if (out.f) out.f[p * F + f] = h;
+        if (out.h) {
+            int hi, lo;
+            float s, sum;
+            quant2_half(h, hi, lo, s, sum);
+            out.h[p * F + f] = (int8_t)hi;
+            out.l[p * F + f] = (int8_t)lo;
+            if ((lane & 31) == 0) {
+                out.s[p * (F >> 5) + (f >> 5)] = s;
+                out.m[p * (F >> 5) + (f >> 5)] = sum;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(256) void k_rpl_gateup(
+    const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up, int64_t estride,
+    const int8_t *__restrict__ xh, const int8_t *__restrict__ xl, const float *__restrict__ xs,
+    const float *__restrict__ xm, SlotArgs sa, int d, int F, float *__restrict__ hf,
+    int8_t *__restrict__ hh, int8_t *__restrict__ hl, float *__restrict__ hs,
+    float *__restrict__ hm) {
+    const Limbs X{xh, xl, xs, xm, d};
+    const HOut out{hf, hh, hl, hs, hm};
+    int e, p0, n;
+    if (!slot_info(sa, blockIdx.y, e, p0, n)) return;
+    e = __builtin_amdgcn_readfirstlane(e);
+    p0 = __builtin_amdgcn_readfirstlane(p0);
+    n = __builtin_amdgcn_readfirstlane(n);
+    __shared__ float s_red[kWaves][2][4][64];
+    // wave index made provably uniform so block indices and x addresses stay scalar
+    const int NB = d >> 8, rt = blockIdx.x, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kb0 = NB * wave / kWaves, kb1 = NB * (wave + 1) / kWaves;
+    const int64_t tile = (int64_t)rt * NB * 9 * 64 + lane;
+    const uint4 *G = reinterpret_cast<const uint4 *>(gate + (int64_t)e * estride) + tile;
+    const uint4 *U = reinterpret_cast<const uint4 *>(up + (int64_t)e * estride) + tile;
+    const int f = rt * 64 + lane;
+    for (int c = 0; c < n;) {
+        const int left = n - c;
+        if (left >= 4) {
+            gateup_chunk<4>(G, U, kb0, kb1, X, sa, p0, n, c, F, f, out, s_red);
+            c += 4;
+        } else if (left == 3) {
+            gateup_chunk<3>(G, U, kb0, kb1, X, sa, p0, n, c, F, f, out, s_red);
+            c += 3;
+        } else if (left == 2) {
+            gateup_chunk<2>(G, U, kb0, kb1, X, sa, p0, n, c, F, f, out, s_red);
+            c += 2;
+        } else {
+            gateup_chunk<1>(G, U, kb0, kb1, X, sa, p0, n, c, F, f, out, s_red);
+            c += 1;
+        }
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void down_chunk(const uint4 *W, int kb0, int kb1, const Limbs &X,
+                                           int p0, int c, int d, int r, float *Y,
+                                           float (*s_red)[4][64]) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    int row[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) row[t] = __builtin_amdgcn_readfirstlane(p0 + c + t);
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = 0.0f;
+    pass1<NT>(W, kb0, kb1, X, row, acc);
+#pragma unroll
+    for (int t = 0; t < NT; t++) s_red[wave][t][lane] = acc[t];
+    __syncthreads();
+    if (wave < NT) {
+        const int t = wave;
+        float v = s_red[0][t][lane];
+#pragma unroll
+        for (int w = 1; w < kWaves; w++) v = v + s_red[w][t][lane];
+        Y[(int64_t)(p0 + c + t) * d + r] = v;
+    }
+    __syncthreads();
+}
+
+// grid (d/64 tiles, slots, ksplit): block z covers super-block slices
+// 4z .. 4z+3 of the 4*ksplit slices of the F dimension; its partial row sums
+// go to Y + z * split_stride and the combine adds the splits in order.
+__global__ __launch_bounds__(256) void k_rpl_down(
+    const uint8_t *__restrict__ down, int64_t estride, const int8_t *__restrict__ xh,
+    const int8_t *__restrict__ xl, const float *__restrict__ xs, const float *__restrict__ xm,
+    SlotArgs sa, int d, int F, float *__restrict__ Y, int64_t split_stride) {
+    const Limbs X{xh, xl, xs, xm, F};
+    int e, p0, n;
+    if (!slot_info(sa, blockIdx.y, e, p0, n)) return;
+    e = __builtin_amdgcn_readfirstlane(e);
+    p0 = __builtin_amdgcn_readfirstlane(p0);
+    n = __builtin_amdgcn_readfirstlane(n);
+    __shared__ float s_red[kWaves][4][64];
+    const int NB = F >> 8, rt = blockIdx.x, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int slices = kWaves * gridDim.z, s = blockIdx.z * kWaves + wave;
+    const int kb0 = (int)((int64_t)NB * s / slices), kb1 = (int)((int64_t)NB * (s + 1) / slices);
+    const uint4 *W = reinterpret_cast<const uint4 *>(down + (int64_t)e * estride) +
+                     (int64_t)rt * NB * 9 * 64 + lane;
+    float *Yz = Y + (int64_t)blockIdx.z * split_stride;
+    const int r = rt * 64 + lane;
+    for (int c = 0; c < n;) {
+        const int left = n - c;
+        if (left >= 4) {
+            down_chunk<4>(W, kb0, kb1, X, p0, c, d, r, Yz, s_red);
+            c += 4;
+        } else if (left == 3) {
+            down_chunk<3>(W, kb0, kb1, X, p0, c, d, r, Yz, s_red);
+            c += 3;
+        } else if (left == 2) {
+            down_chunk<2>(W, kb0, kb1, X, p0, c, d, r, Yz, s_red);
+            c += 2;
+        } else {
+            down_chunk<1>(W, kb0, kb1, X, p0, c, d, r, Yz, s_red);
+            c += 1;
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_rpl_gateup(const uint8_t *gate, const uint8_t *up, int64_t estride,
+                             const int8_t *xh, const int8_t *xl, const float *xs, const float *xm,
+                             const SlotArgsHost &sa, int slots, int d, int F, float *Hf, int8_t *hh,
+                             int8_t *hl, float *hs, float *hm, hipStream_t st) {
+    SlotArgs s{sa.perm, sa.counts, sa.offsets, sa.touched, sa.E, sa.K, sa.T, sa.shared};
+    hipLaunchKernelGGL(k_rpl_gateup, dim3(F / 64, slots), dim3(256), 0, st, gate, up, estride, xh,
+                       xl, xs, xm, s, d, F, Hf, hh, hl, hs, hm);
+    return hipGetLastError();
+}
+
+hipError_t launch_rpl_down(const uint8_t *down, int64_t estride, const int8_t *hh,
+                           const int8_t *hl, const float *hs, const float *hm,
+                           const SlotArgsHost &sa, int slots, int d, int F, int ksplit, float *Y,
+                           int64_t split_stride, hipStream_t st) {
+    SlotArgs s{sa.perm, sa.counts, sa.offsets, sa.touched, sa.E, sa.K, sa.T, sa.shared};
+    hipLaunchKernelGGL(k_rpl_down, dim3(d / 64, slots, ksplit), dim3(256), 0, st, down, estride, hh,
+                       hl, hs, hm, s, d, F, Y, split_stride);
+    return hipGetLastError();
+}
+
+}  // namespace lcmoe

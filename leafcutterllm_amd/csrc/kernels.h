@@ -1,0 +1,74 @@
+// Host-side launchers of the device kernels (one declaration per kernel
+// family).  Internal to the library; not part of the ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace lcmoe {
+
+struct RouteParams {
+    int kind, n_group, topk_group, has_bias;
+    float scale;
+};
+
+// Router + x limb quantisation + top-k + dispatch, one launch.
+struct RouterArgs {
+    const float *x;    // [T, d]
+    const float *wrt;  // router transposed on the device: [E, d]
+    const float *bias; // [E] or null
+    int T, d, E, K;
+    RouteParams rp;
+    float *logits;        // [T, E] workspace
+    int32_t *topk_idx;    // [T, K]
+    float *topk_w;        // [T, K]
+    int8_t *xh, *xl;      // [T, d] limbs, or null
+    float *xs, *xm;       // [T, d/32] scale and quantised-sum
+    int32_t *counts, *offsets, *perm, *inv, *touched;
+    uint32_t *sync;       // [n_token_groups + 1] zero-initialised counters
+};
+hipError_t launch_router(const RouterArgs &a, hipStream_t st);
+int router_token_groups(int T, int d, int E);
+
+struct SlotArgsHost {
+    const int32_t *perm, *counts, *offsets, *touched;
+    int E, K, T, shared;
+};
+
+// Generic decode path on GGUF-layout tensors (any supported type, any
+// shape): f32 activations in, f32 H / Y out.
+hipError_t launch_generic_gateup(int qt, const uint8_t *gate, const uint8_t *up, int64_t estride,
+                                 const float *x, const SlotArgsHost &sa, int slots, int d, int F,
+                                 float *Hf, int8_t *hh, int8_t *hl, float *hs, float *hm,
+                                 hipStream_t st);
+hipError_t launch_generic_down(int qt, const uint8_t *down, int64_t estride, const float *Hf,
+                               const SlotArgsHost &sa, int slots, int d, int F, float *Y,
+                               hipStream_t st);
+
+// Row-per-lane Q4_K decode path on the RPL64 layout: int8-limb activations,
+// exact integer dot products.
+hipError_t launch_rpl_gateup(const uint8_t *gate, const uint8_t *up, int64_t estride,
+                             const int8_t *xh, const int8_t *xl, const float *xs, const float *xm,
+                             const SlotArgsHost &sa, int slots, int d, int F, float *Hf, int8_t *hh,
+                             int8_t *hl, float *hs, float *hm, hipStream_t st);
+hipError_t launch_rpl_down(const uint8_t *down, int64_t estride, const int8_t *hh,
+                           const int8_t *hl, const float *hs, const float *hm,
+                           const SlotArgsHost &sa, int slots, int d, int F, int ksplit, float *Y,
+                           int64_t split_stride, hipStream_t st);
+
+// y[t] = sum_k w[t,k] * sum_s Yr[s][inv[t,k]] + sum_j sum_s Ys[s][j*T + t].
+hipError_t launch_combine(const float *Yr, int ks_r, int64_t stride_r, const float *Ys, int ks_s,
+                          int64_t stride_s, const int32_t *inv, const float *topk_w, int T, int K,
+                          int S, int d, float *y, hipStream_t st);
+
+hipError_t launch_debug_dequant(int qt, const uint8_t *src, int64_t count, float *out,
+                                hipStream_t st);
+hipError_t launch_debug_sigmoid(const float *x, int64_t n, float *out, hipStream_t st);
+
+// RPL64 eligibility: Q4_K, rows tile by 64, columns are whole super-blocks.
+inline bool rpl64_ok(int qt, int64_t rows, int64_t cols) {
+    return qt == 12 && rows % 64 == 0 && cols % 256 == 0;
+}
+
+}  // namespace lcmoe

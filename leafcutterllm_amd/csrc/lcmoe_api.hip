@@ -1,0 +1,496 @@
+// C ABI entry points (include/lcmoe.h): resident weights, workspace, and the
+// per-forward launch sequence on one stream:
+//   router (logits, x limbs, top-k, dispatch) -> gate/up (+SwiGLU) -> down
+//   -> combine.
+// Layout decisions are made once at lcmoe_create: Q4_K matrices whose rows
+// tile by 64 and whose columns are whole super-blocks are repacked to RPL64
+// and served by the integer row-per-lane kernels; everything else keeps the
+// GGUF layout and the generic kernels.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <new>
+#include <thread>
+#include <vector>
+
+#include "kernels.h"
+#include "lcmoe_internal.h"
+
+using namespace lcmoe;
+
+#define HIP_TRY(expr)                                                                    \
+    do {                                                                                 \
+        hipError_t e_ = (expr);                                                          \
+        if (e_ != hipSuccess)                                                            \
+            return fail(LCMOE_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_));          \
+    } while (0)
+
+namespace {
+
+enum Slot { kSlotRouter, kSlotGateUp, kSlotGateUpSh, kSlotDown, kSlotDownSh, kSlotCombine, kNumSlots };
+const char *kSlotNames[kNumSlots] = {"router", "gateup", "gateup_shared", "down", "down_shared",
+                                     "combine"};
+constexpr int kMaxKSplit = 4;
+
+struct ExpertSet {  // one family of experts (routed or shared)
+    int n = 0, F = 0, qt_gu = 0, qt_dn = 0;
+    bool rpl_gu = false, rpl_dn = false;
+    uint8_t *gate = nullptr, *up = nullptr, *down = nullptr;
+    int64_t sz_gu = 0, sz_dn = 0;
+    // H between the two products
+    float *Hf = nullptr;
+    int8_t *hh = nullptr, *hl = nullptr;
+    float *hs = nullptr, *hm = nullptr;
+    // down output partials [kmax][positions][d]
+    float *Y = nullptr;
+    int kmax = 1;
+    int64_t positions = 0;
+};
+
+}  // namespace
+
+struct lcmoe_handle {
+    lcmoe_desc desc{};
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::vector<void *> allocs;
+    float *wrt = nullptr, *bias = nullptr;
+    ExpertSet routed, shared;
+    float *x_dev = nullptr, *y_dev = nullptr, *logits = nullptr;
+    int8_t *xh = nullptr, *xl = nullptr;
+    float *xs = nullptr, *xm = nullptr;
+    int32_t *topk_idx = nullptr, *counts = nullptr, *offsets = nullptr, *perm = nullptr,
+            *inv = nullptr, *touched = nullptr;
+    float *topk_w = nullptr;
+    uint32_t *sync = nullptr;
+    int last_T = -1;
+    hipStream_t last_stream = nullptr;
+    bool timing = false;
+    struct Pending { int slot; hipEvent_t a, b; };
+    std::vector<Pending> pending;
+    std::vector<hipEvent_t> event_pool;
+    double t_ms[kNumSlots] = {};
+    int64_t t_n[kNumSlots] = {};
+};
+
+namespace {
+
+lcmoe_status dev_alloc(lcmoe_handle *h, void **p, size_t bytes) {
+    *p = nullptr;
+    if (bytes == 0) bytes = 256;
+    hipError_t e = hipMalloc(p, bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(e == hipErrorOutOfMemory ? LCMOE_ERR_OUT_OF_MEMORY : LCMOE_ERR_HIP,
+                    "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    }
+    h->allocs.push_back(*p);
+    return LCMOE_OK;
+}
+
+template <class T>
+lcmoe_status alloc_n(lcmoe_handle *h, T **dst, size_t n) {
+    void *p;
+    lcmoe_status st = dev_alloc(h, &p, n * sizeof(T));
+    *dst = static_cast<T *>(p);
+    return st;
+}
+
+// Uploads n stacked expert matrices [rows, cols] of type qt, repacking each
+// to RPL64 when `rpl` (one expert at a time through a host staging buffer).
+lcmoe_status upload_stack(lcmoe_handle *h, uint8_t **dst, const uint8_t *src, int n, int qt,
+                          int64_t rows, int64_t cols, bool rpl, int64_t *sz_out) {
+    const int64_t sz = (int64_t)lcmoe_tensor_size(qt, rows * cols);
+    *sz_out = sz;
+    lcmoe_status st = alloc_n(h, dst, (size_t)sz * n);
+    if (st) return st;
+    if (!rpl) {
+        HIP_TRY(hipMemcpy(*dst, src, (size_t)sz * n, hipMemcpyHostToDevice));
+        return LCMOE_OK;
+    }
+    std::vector<uint8_t> buf((size_t)sz);
+    for (int e = 0; e < n; e++) {
+        const uint8_t *s = src + (size_t)e * sz;
+        // repack 64-row tiles in parallel
+        const int64_t tiles = rows / 64;
+        unsigned nth = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+        std::vector<std::thread> th;
+        for (unsigned t = 0; t < nth; t++)
+            th.emplace_back([&, t] {
+                const int64_t NB = cols / 256, tb = (int64_t)NB * 9 * 1024;
+                for (int64_t rt = t; rt < tiles; rt += nth)
+                    repack_rpl64_q4k(s + rt * 64 * NB * 144, buf.data() + rt * tb, 64, cols);
+            });
+        for (auto &x : th) x.join();
+        HIP_TRY(hipMemcpy(*dst + (size_t)e * sz, buf.data(), (size_t)sz, hipMemcpyHostToDevice));
+    }
+    return LCMOE_OK;
+}
+
+void free_handle(lcmoe_handle *h) {
+    if (!h) return;
+    if (h->stream) (void)hipStreamSynchronize(h->stream);
+    for (auto &p : h->pending) {
+        (void)hipEventDestroy(p.a);
+        (void)hipEventDestroy(p.b);
+    }
+    for (auto ev : h->event_pool) (void)hipEventDestroy(ev);
+    for (void *p : h->allocs) (void)hipFree(p);
+    if (h->stream) (void)hipStreamDestroy(h->stream);
+    delete h;
+}
+
+hipEvent_t take_event(lcmoe_handle *h) {
+    if (!h->event_pool.empty()) {
+        hipEvent_t e = h->event_pool.back();
+        h->event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+template <class Fn>
+hipError_t timed(lcmoe_handle *h, hipStream_t st, int slot, Fn fn) {
+    if (!h->timing) return fn();
+    hipEvent_t a = take_event(h), b = take_event(h);
+    if (!a || !b) return fn();
+    (void)hipEventRecord(a, st);
+    hipError_t e = fn();
+    (void)hipEventRecord(b, st);
+    h->pending.push_back({slot, a, b});
+    return e;
+}
+
+// Column splits of the down product so that small batches still launch
+// enough waves: each wave keeps >= 2 super-blocks.
+int choose_ksplit(const ExpertSet &s, int d, int active) {
+    if (!s.rpl_dn) return 1;
+    const int NB = s.F / 256, tiles = (d / 64) * std::max(1, active);
+    int ks = 1;
+    while (ks < s.kmax && tiles * ks < 256 && NB >= 8 * ks * 2) ks *= 2;
+    return ks;
+}
+
+lcmoe_status setup_set(lcmoe_handle *h, ExpertSet &s, int n, int F, int qgu, int qdn,
+                       const uint8_t *gate, const uint8_t *up, const uint8_t *down, int64_t positions) {
+    const int64_t d = h->desc.d_model;
+    s.n = n;
+    s.F = F;
+    s.qt_gu = qgu;
+    s.qt_dn = qdn;
+    s.positions = positions;
+    s.rpl_gu = rpl64_ok(qgu, F, d);
+    s.rpl_dn = s.rpl_gu && rpl64_ok(qdn, d, F);
+    s.kmax = s.rpl_dn ? kMaxKSplit : 1;
+    int64_t szu = 0;
+    lcmoe_status st;
+    if ((st = upload_stack(h, &s.gate, gate, n, qgu, F, d, s.rpl_gu, &s.sz_gu))) return st;
+    if ((st = upload_stack(h, &s.up, up, n, qgu, F, d, s.rpl_gu, &szu))) return st;
+    if ((st = upload_stack(h, &s.down, down, n, qdn, d, F, s.rpl_dn, &s.sz_dn))) return st;
+    if (s.rpl_dn) {
+        if ((st = alloc_n(h, &s.hh, positions * F))) return st;
+        if ((st = alloc_n(h, &s.hl, positions * F))) return st;
+        if ((st = alloc_n(h, &s.hs, positions * F / 32))) return st;
+        if ((st = alloc_n(h, &s.hm, positions * F / 32))) return st;
+    } else {
+        if ((st = alloc_n(h, &s.Hf, positions * F))) return st;
+    }
+    return alloc_n(h, &s.Y, (size_t)s.kmax * positions * d);
+}
+
+}  // namespace
+
+extern "C" lcmoe_status lcmoe_create(const lcmoe_desc *desc, const lcmoe_weights *w,
+                                     lcmoe_handle **out) {
+    clear_error();
+    if (!out) return fail(LCMOE_ERR_INVALID_ARG, "out is NULL");
+    *out = nullptr;
+    lcmoe_status st = validate_desc(desc);
+    if (st) return st;
+    if (desc->type_gate != desc->type_up || (desc->n_shared && desc->type_gate_sh != desc->type_up_sh))
+        return fail(LCMOE_ERR_UNSUPPORTED, "gate and up must share a quant type");
+    if ((st = scan_weights(desc, w))) return st;
+
+    int ndev = 0;
+    hipError_t he = hipGetDeviceCount(&ndev);
+    if (he != hipSuccess || ndev < 1) {
+        (void)hipGetLastError();
+        return fail(LCMOE_ERR_HIP, "no HIP device available (%s)", hipGetErrorString(he));
+    }
+    lcmoe_handle *h = new (std::nothrow) lcmoe_handle();
+    if (!h) return fail(LCMOE_ERR_OUT_OF_MEMORY, "host allocation failed");
+    h->desc = *desc;
+    const lcmoe_desc &D = h->desc;
+    auto bail = [&](lcmoe_status s) {
+        free_handle(h);
+        return s;
+    };
+    if (hipGetDevice(&h->device) != hipSuccess) return bail(fail(LCMOE_ERR_HIP, "hipGetDevice failed"));
+    if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess)
+        return bail(fail(LCMOE_ERR_HIP, "hipStreamCreate failed"));
+
+    const int64_t d = D.d_model, E = D.n_expert, K = D.n_expert_used, S = D.n_shared,
+                  Tm = D.max_tokens, A = Tm * K;
+    // router, transposed to [E, d] so each expert's row is contiguous
+    {
+        std::vector<float> wt((size_t)E * d);
+        for (int64_t k = 0; k < d; k++)
+            for (int64_t e = 0; e < E; e++) wt[e * d + k] = w->router[k * E + e];
+        if ((st = alloc_n(h, &h->wrt, wt.size()))) return bail(st);
+        if (hipMemcpy(h->wrt, wt.data(), wt.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+            return bail(fail(LCMOE_ERR_HIP, "router upload failed"));
+    }
+    if (D.has_bias) {
+        if ((st = alloc_n(h, &h->bias, E))) return bail(st);
+        if (hipMemcpy(h->bias, w->bias, E * 4, hipMemcpyHostToDevice) != hipSuccess)
+            return bail(fail(LCMOE_ERR_HIP, "bias upload failed"));
+    }
+    if ((st = setup_set(h, h->routed, (int)E, D.d_ff, D.type_gate, D.type_down, w->gate, w->up,
+                        w->down, A)))
+        return bail(st);
+    if (S > 0 && (st = setup_set(h, h->shared, (int)S, D.d_ff_shared, D.type_gate_sh,
+                                 D.type_down_sh, w->gate_sh, w->up_sh, w->down_sh, S * Tm)))
+        return bail(st);
+    const bool limbs = h->routed.rpl_gu || (S > 0 && h->shared.rpl_gu);
+    if ((st = alloc_n(h, &h->x_dev, Tm * d))) return bail(st);
+    if ((st = alloc_n(h, &h->y_dev, Tm * d))) return bail(st);
+    if ((st = alloc_n(h, &h->logits, Tm * E))) return bail(st);
+    if (limbs) {
+        if ((st = alloc_n(h, &h->xh, Tm * d))) return bail(st);
+        if ((st = alloc_n(h, &h->xl, Tm * d))) return bail(st);
+        if ((st = alloc_n(h, &h->xs, Tm * d / 32))) return bail(st);
+        if ((st = alloc_n(h, &h->xm, Tm * d / 32))) return bail(st);
+    }
+    if ((st = alloc_n(h, &h->topk_idx, A))) return bail(st);
+    if ((st = alloc_n(h, &h->topk_w, A))) return bail(st);
+    if ((st = alloc_n(h, &h->counts, E))) return bail(st);
+    if ((st = alloc_n(h, &h->offsets, E + 1))) return bail(st);
+    if ((st = alloc_n(h, &h->perm, A))) return bail(st);
+    if ((st = alloc_n(h, &h->inv, A))) return bail(st);
+    if ((st = alloc_n(h, &h->touched, E + 1))) return bail(st);
+    const int nsync = router_token_groups((int)Tm, (int)d, (int)E) + 1;
+    if ((st = alloc_n(h, &h->sync, nsync))) return bail(st);
+    if (hipMemset(h->sync, 0, sizeof(uint32_t) * nsync) != hipSuccess)
+        return bail(fail(LCMOE_ERR_HIP, "workspace clear failed"));
+    *out = h;
+    return LCMOE_OK;
+}
+
+extern "C" void lcmoe_destroy(lcmoe_handle *h) { free_handle(h); }
+
+static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const float *x, int T,
+                            hipStream_t st) {
+    const lcmoe_desc &D = h->desc;
+    const int d = D.d_model, K = D.n_expert_used, E = D.n_expert;
+    const int slots = shared ? s.n : std::min(E, T * K);
+    SlotArgsHost sa{h->perm, h->counts, h->offsets, h->touched, E, K, T, shared ? 1 : 0};
+    HIP_TRY(timed(h, st, shared ? kSlotGateUpSh : kSlotGateUp, [&] {
+        if (s.rpl_gu)
+            return launch_rpl_gateup(s.gate, s.up, s.sz_gu, h->xh, h->xl, h->xs, h->xm, sa, slots,
+                                     d, s.F, s.Hf, s.hh, s.hl, s.hs, s.hm, st);
+        return launch_generic_gateup(s.qt_gu, s.gate, s.up, s.sz_gu, x, sa, slots, d, s.F, s.Hf,
+                                     nullptr, nullptr, nullptr, nullptr, st);
+    }));
+    const int ks = choose_ksplit(s, d, slots);
+    HIP_TRY(timed(h, st, shared ? kSlotDownSh : kSlotDown, [&] {
+        if (s.rpl_dn)
+            return launch_rpl_down(s.down, s.sz_dn, s.hh, s.hl, s.hs, s.hm, sa, slots, d, s.F, ks,
+                                   s.Y, s.positions * d, st);
+        return launch_generic_down(s.qt_dn, s.down, s.sz_dn, s.Hf, sa, slots, d, s.F, s.Y, st);
+    }));
+    return LCMOE_OK;
+}
+
+static int last_ksplit(lcmoe_handle *h, ExpertSet &s, bool shared, int T) {
+    const int slots = shared ? s.n : std::min(h->desc.n_expert, T * h->desc.n_expert_used);
+    return choose_ksplit(s, h->desc.d_model, slots);
+}
+
+static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, float *y,
+                                    hipStream_t st) {
+    const lcmoe_desc &D = h->desc;
+    const int d = D.d_model, E = D.n_expert, K = D.n_expert_used, S = D.n_shared;
+    RouterArgs ra{};
+    ra.x = x;
+    ra.wrt = h->wrt;
+    ra.bias = h->bias;
+    ra.T = T;
+    ra.d = d;
+    ra.E = E;
+    ra.K = K;
+    ra.rp = RouteParams{D.route_kind, D.n_group, D.topk_group, D.has_bias, D.routed_scale};
+    ra.logits = h->logits;
+    ra.topk_idx = h->topk_idx;
+    ra.topk_w = h->topk_w;
+    ra.xh = h->xh;
+    ra.xl = h->xl;
+    ra.xs = h->xs;
+    ra.xm = h->xm;
+    ra.counts = h->counts;
+    ra.offsets = h->offsets;
+    ra.perm = h->perm;
+    ra.inv = h->inv;
+    ra.touched = h->touched;
+    ra.sync = h->sync;
+    HIP_TRY(timed(h, st, kSlotRouter, [&] { return launch_router(ra, st); }));
+    lcmoe_status s;
+    if ((s = run_set(h, h->routed, false, x, T, st))) return s;
+    if (S > 0 && (s = run_set(h, h->shared, true, x, T, st))) return s;
+    const int ks_r = last_ksplit(h, h->routed, false, T);
+    const int ks_s = S > 0 ? last_ksplit(h, h->shared, true, T) : 1;
+    HIP_TRY(timed(h, st, kSlotCombine, [&] {
+        return launch_combine(h->routed.Y, ks_r, h->routed.positions * d, h->shared.Y, ks_s,
+                              h->shared.positions * d, h->inv, h->topk_w, T, K, S, d, y, st);
+    }));
+    h->last_T = T;
+    h->last_stream = st;
+    return LCMOE_OK;
+}
+
+extern "C" lcmoe_status lcmoe_forward_dev(lcmoe_handle *h, const float *x_dev, int32_t T,
+                                          float *y_dev, void *stream) {
+    clear_error();
+    if (!h) return fail(LCMOE_ERR_INVALID_ARG, "handle is NULL");
+    if (T < 0 || T > h->desc.max_tokens)
+        return fail(LCMOE_ERR_INVALID_ARG, "T=%d outside [0, max_tokens=%d]", T, h->desc.max_tokens);
+    if (T > 0 && (!x_dev || !y_dev)) return fail(LCMOE_ERR_INVALID_ARG, "x or y is NULL");
+    if (((uintptr_t)x_dev | (uintptr_t)y_dev) & 15)
+        return fail(LCMOE_ERR_INVALID_ARG, "x and y must be 16-byte aligned");
+    HIP_TRY(hipSetDevice(h->device));
+    hipStream_t st = stream ? (hipStream_t)stream : h->stream;
+    if (T == 0) {
+        h->last_T = 0;
+        h->last_stream = st;
+        return LCMOE_OK;
+    }
+    return enqueue_forward(h, x_dev, T, y_dev, st);
+}
+
+extern "C" lcmoe_status lcmoe_forward(lcmoe_handle *h, const float *x, int32_t T, float *y,
+                                      int32_t *topk_idx, float *topk_w) {
+    clear_error();
+    if (!h) return fail(LCMOE_ERR_INVALID_ARG, "handle is NULL");
+    if (T < 0 || T > h->desc.max_tokens)
+        return fail(LCMOE_ERR_INVALID_ARG, "T=%d outside [0, max_tokens=%d]", T, h->desc.max_tokens);
+    HIP_TRY(hipSetDevice(h->device));
+    if (T == 0) {
+        h->last_T = 0;
+        h->last_stream = h->stream;
+        return LCMOE_OK;
+    }
+    if (!x || !y) return fail(LCMOE_ERR_INVALID_ARG, "x or y is NULL");
+    const size_t xb = sizeof(float) * (size_t)T * h->desc.d_model;
+    const size_t kb = (size_t)T * h->desc.n_expert_used;
+    HIP_TRY(hipMemcpyAsync(h->x_dev, x, xb, hipMemcpyHostToDevice, h->stream));
+    lcmoe_status st = enqueue_forward(h, h->x_dev, T, h->y_dev, h->stream);
+    if (st) return st;
+    HIP_TRY(hipMemcpyAsync(y, h->y_dev, xb, hipMemcpyDeviceToHost, h->stream));
+    if (topk_idx)
+        HIP_TRY(hipMemcpyAsync(topk_idx, h->topk_idx, kb * 4, hipMemcpyDeviceToHost, h->stream));
+    if (topk_w) HIP_TRY(hipMemcpyAsync(topk_w, h->topk_w, kb * 4, hipMemcpyDeviceToHost, h->stream));
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    return LCMOE_OK;
+}
+
+extern "C" lcmoe_status lcmoe_get_dispatch(lcmoe_handle *h, int32_t *T_out, int32_t *topk_idx,
+                                           float *topk_w, int32_t *counts, int32_t *offsets,
+                                           int32_t *perm, int32_t *inv) {
+    clear_error();
+    if (!h) return fail(LCMOE_ERR_INVALID_ARG, "handle is NULL");
+    if (h->last_T < 0) return fail(LCMOE_ERR_STATE, "no forward has run on this handle");
+    HIP_TRY(hipSetDevice(h->device));
+    HIP_TRY(hipStreamSynchronize(h->last_stream));
+    const int T = h->last_T, K = h->desc.n_expert_used, E = h->desc.n_expert;
+    if (T_out) *T_out = T;
+    const size_t A = (size_t)T * K;
+    if (T == 0) {
+        if (counts) std::memset(counts, 0, sizeof(int32_t) * E);
+        if (offsets) std::memset(offsets, 0, sizeof(int32_t) * (E + 1));
+        return LCMOE_OK;
+    }
+    if (topk_idx) HIP_TRY(hipMemcpy(topk_idx, h->topk_idx, A * 4, hipMemcpyDeviceToHost));
+    if (topk_w) HIP_TRY(hipMemcpy(topk_w, h->topk_w, A * 4, hipMemcpyDeviceToHost));
+    if (counts) HIP_TRY(hipMemcpy(counts, h->counts, (size_t)E * 4, hipMemcpyDeviceToHost));
+    if (offsets) HIP_TRY(hipMemcpy(offsets, h->offsets, (size_t)(E + 1) * 4, hipMemcpyDeviceToHost));
+    if (perm) HIP_TRY(hipMemcpy(perm, h->perm, A * 4, hipMemcpyDeviceToHost));
+    if (inv) HIP_TRY(hipMemcpy(inv, h->inv, A * 4, hipMemcpyDeviceToHost));
+    return LCMOE_OK;
+}
+
+extern "C" lcmoe_status lcmoe_set_timing(lcmoe_handle *h, int32_t enable) {
+    clear_error();
+    if (!h) return fail(LCMOE_ERR_INVALID_ARG, "handle is NULL");
+    h->timing = enable != 0;
+    return LCMOE_OK;
+}
+
+extern "C" lcmoe_status lcmoe_get_timing(lcmoe_handle *h, int32_t n_slots, double *ms,
+                                         int64_t *launches) {
+    clear_error();
+    if (!h) return fail(LCMOE_ERR_INVALID_ARG, "handle is NULL");
+    HIP_TRY(hipSetDevice(h->device));
+    for (auto &p : h->pending) {
+        HIP_TRY(hipEventSynchronize(p.b));
+        float t = 0.0f;
+        HIP_TRY(hipEventElapsedTime(&t, p.a, p.b));
+        h->t_ms[p.slot] += t;
+        h->t_n[p.slot] += 1;
+        h->event_pool.push_back(p.a);
+        h->event_pool.push_back(p.b);
+    }
+    h->pending.clear();
+    for (int i = 0; i < n_slots && i < kNumSlots; i++) {
+        if (ms) ms[i] = h->t_ms[i];
+        if (launches) launches[i] = h->t_n[i];
+    }
+    for (int i = 0; i < kNumSlots; i++) {
+        h->t_ms[i] = 0.0;
+        h->t_n[i] = 0;
+    }
+    return LCMOE_OK;
+}
+
+extern "C" const char *lcmoe_timing_name(int32_t slot) {
+    return (slot >= 0 && slot < kNumSlots) ? kSlotNames[slot] : "";
+}
+
+extern "C" int32_t lcmoe_timing_slots(void) { return kNumSlots; }
+
+extern "C" lcmoe_status lcmoe_debug_dequant(int32_t type, const uint8_t *data, int64_t count,
+                                            float *out) {
+    clear_error();
+    if (!data || !out || count <= 0 || count % 8)
+        return fail(LCMOE_ERR_INVALID_ARG, "bad arguments");
+    int64_t bs = block_size(type);
+    if (!bs) return fail(LCMOE_ERR_UNSUPPORTED, "type %d", type);
+    if (count % bs) return fail(LCMOE_ERR_INVALID_ARG, "count not a whole number of blocks");
+    size_t nbytes = lcmoe_tensor_size(type, count);
+    void *src = nullptr, *dst = nullptr;
+    HIP_TRY(hipMalloc(&src, nbytes + 16));
+    hipError_t e = hipMalloc(&dst, sizeof(float) * count);
+    if (e == hipSuccess) e = hipMemcpy(src, data, nbytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = launch_debug_dequant(type, (const uint8_t *)src, count, (float *)dst, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(out, dst, sizeof(float) * count, hipMemcpyDeviceToHost);
+    (void)hipFree(src);
+    if (dst) (void)hipFree(dst);
+    if (e != hipSuccess) return fail(LCMOE_ERR_HIP, "debug_dequant: %s", hipGetErrorString(e));
+    return LCMOE_OK;
+}
+
+extern "C" lcmoe_status lcmoe_debug_sigmoid(const float *x, int64_t n, float *out) {
+    clear_error();
+    if (!x || !out || n <= 0) return fail(LCMOE_ERR_INVALID_ARG, "bad arguments");
+    void *a = nullptr, *b = nullptr;
+    HIP_TRY(hipMalloc(&a, sizeof(float) * n));
+    hipError_t e = hipMalloc(&b, sizeof(float) * n);
+    if (e == hipSuccess) e = hipMemcpy(a, x, sizeof(float) * n, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = launch_debug_sigmoid((const float *)a, n, (float *)b, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(out, b, sizeof(float) * n, hipMemcpyDeviceToHost);
+    (void)hipFree(a);
+    if (b) (void)hipFree(b);
+    if (e != hipSuccess) return fail(LCMOE_ERR_HIP, "debug_sigmoid: %s", hipGetErrorString(e));
+    return LCMOE_OK;
+}

@@ -61,8 +61,8 @@ lcmoe_status validate_desc(const lcmoe_desc *d) {
     case LCMOE_ROUTE_SOFTMAX_RENORM:
     case LCMOE_ROUTE_SOFTMAX: break;
     case LCMOE_ROUTE_SIGMOID_GROUP:
-        if (d->n_group < 1 || d->n_expert % d->n_group)
-            return fail(LCMOE_ERR_INVALID_ARG, "n_group=%d must divide n_expert=%d", d->n_group,
+        if (d->n_group < 1 || d->n_group > 64 || d->n_expert % d->n_group)
+            return fail(LCMOE_ERR_INVALID_ARG, "n_group=%d must be <= 64 and divide n_expert=%d", d->n_group,
                         d->n_expert);
         if (d->topk_group < 1 || d->topk_group > d->n_group)
             return fail(LCMOE_ERR_INVALID_ARG, "topk_group=%d outside [1, n_group]", d->topk_group);
@@ -290,6 +290,21 @@ static inline uint64_t mix64(uint64_t z) {
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
     z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
     return z ^ (z >> 31);
+}
+
+// RPL64 repack of a GGUF Q4_K [rows, cols] matrix (rows % 64 == 0,
+// cols % 256 == 0): per 64-row tile and 256-column super-block, the 144-byte
+// blocks of the 64 rows are cut into nine 16-byte chunks and chunk c of all
+// 64 rows is stored contiguously.  Same bytes, new order.
+void repack_rpl64_q4k(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t cols) {
+    const int64_t NB = cols / 256, row_bytes = NB * 144;
+    for (int64_t rt = 0; rt < rows / 64; rt++)
+        for (int64_t kb = 0; kb < NB; kb++)
+            for (int c = 0; c < 9; c++) {
+                uint8_t *o = dst + ((rt * NB + kb) * 9 + c) * 1024;
+                for (int r = 0; r < 64; r++)
+                    std::memcpy(o + r * 16, src + (rt * 64 + r) * row_bytes + kb * 144 + c * 16, 16);
+            }
 }
 
 }  // namespace lcmoe

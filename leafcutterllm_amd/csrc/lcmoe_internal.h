@@ -84,5 +84,7 @@ inline uint16_t float_to_half(float f) {
 lcmoe_status validate_desc(const lcmoe_desc *d);
 // Host-side scan of every expert tensor's block scales.
 lcmoe_status scan_weights(const lcmoe_desc *d, const lcmoe_weights *w);
+// RPL64 repack (defined in lcmoe_host.cpp, layout documented there).
+void repack_rpl64_q4k(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t cols);
 
 }  // namespace lcmoe

@@ -146,7 +146,10 @@ def test_e1_k1_reduces_to_dense_ffn():
     wu = O.dequant(Q4, layer["up"], 512 * 256).reshape(512, 256).T
     wd = O.dequant(Q4, layer["down"], 256 * 512).reshape(256, 512).T
     ref = O.ffn_dense(x, wg, wu, wd)
-    assert rel_l2(y, ref) < 1e-5
+    # Q4_K row-per-lane path: x and H enter the integer products as 15-bit
+    # two-limb values (|error| <= max|v| / 32512 per 32-element sub-block),
+    # about 1e-4 relative on y; the layer bar is 1e-3
+    assert rel_l2(y, ref) < 2e-4
 
 
 # ------------------------------------------------- full BASELINE shapes -----
