@@ -143,7 +143,7 @@ def main():
             m.set_timing(False)
         bytes_per_step = sum(call_bytes[i % R] for i in range(args.steps)) / args.steps
         gu_per_launch = sum(gu_bytes[i % R] for i in range(args.steps)) / args.steps
-        gu_ms = kern["gateup"][0] / max(1, kern["gateup"][1])
+        gu_ms = kern["gateup"][0] / kern["gateup"][1] if kern["gateup"][1] else float("nan")
         per_batch[T] = {
             "tokens_per_s": T / (ms * 1e-3),
             "ms_per_step": ms,
@@ -152,7 +152,7 @@ def main():
             "touched_experts": sum(touched) / len(touched),
             "gateup_ms": gu_ms,
             "gateup_bytes": gu_per_launch,
-            "gateup_GBps": gu_per_launch / (gu_ms * 1e-3) / 1e9,
+            "gateup_GBps": gu_per_launch / (gu_ms * 1e-3) / 1e9 if gu_ms == gu_ms else float("nan"),
             "kernel_ms": {k: v[0] / max(1, v[1]) for k, v in kern.items()},
         }
 

@@ -104,38 +104,42 @@ __global__ __launch_bounds__(256) void k_down(const uint8_t *__restrict__ down, 
 }
 
 // y[t] = sum_k w[t,k] * (sum over splits Yr[s][inv[t*K+k]]) + shared terms,
-// slot order then shared order; each term rounded then added.
+// slot order then shared order; each term rounded then added.  Grid
+// (column blocks of 1024, tokens); one float4 of columns per thread.
 __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ Yr, int ks_r,
                                                  int64_t stride_r, const float *__restrict__ Ys,
                                                  int ks_s, int64_t stride_s,
                                                  const int32_t *__restrict__ inv,
                                                  const float *__restrict__ topk_w, int T, int K,
                                                  int S, int d, float *__restrict__ y) {
-    const int t = blockIdx.x;
-    __shared__ int s_pos[kMaxK];
-    __shared__ float s_w[kMaxK];
-    if (threadIdx.x < K) {
-        s_pos[threadIdx.x] = inv[(int64_t)t * K + threadIdx.x];
-        s_w[threadIdx.x] = topk_w[(int64_t)t * K + threadIdx.x];
-    }
-    __syncthreads();
-    for (int c = threadIdx.x; c < d; c += blockDim.x) {
-        float acc = 0.0f;
-        for (int k = 0; k < K; k++) {
-            const float *src = Yr + (int64_t)s_pos[k] * d + c;
-            float v = src[0];
-            for (int s = 1; s < ks_r; s++) v = v + src[s * stride_r];
-            float p = s_w[k] * v;
-            acc = acc + p;
+    const int t = blockIdx.y, c4 = blockIdx.x * blockDim.x + threadIdx.x;
+    if (4 * c4 >= d) return;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int k = 0; k < K; k++) {
+        const int pos = inv[(int64_t)t * K + k];
+        const float w = topk_w[(int64_t)t * K + k];
+        const float4 *src = reinterpret_cast<const float4 *>(Yr + (int64_t)pos * d) + c4;
+        float4 v = src[0];
+        for (int s = 1; s < ks_r; s++) {
+            const float4 u = src[s * stride_r / 4];
+            v.x = v.x + u.x; v.y = v.y + u.y; v.z = v.z + u.z; v.w = v.w + u.w;
         }
-        for (int j = 0; j < S; j++) {
-            const float *src = Ys + ((int64_t)j * T + t) * d + c;
-            float v = src[0];
-            for (int s = 1; s < ks_s; s++) v = v + src[s * stride_s];
-            acc = acc + v;
-        }
-        y[(int64_t)t * d + c] = acc;
+        float p;
+        p = w * v.x; acc.x = acc.x + p;
+        p = w * v.y; acc.y = acc.y + p;
+        p = w * v.z; acc.z = acc.z + p;
+        p = w * v.w; acc.w = acc.w + p;
     }
+    for (int j = 0; j < S; j++) {
+        const float4 *src = reinterpret_cast<const float4 *>(Ys + ((int64_t)j * T + t) * d) + c4;
+        float4 v = src[0];
+        for (int s = 1; s < ks_s; s++) {
+            const float4 u = src[s * stride_s / 4];
+            v.x = v.x + u.x; v.y = v.y + u.y; v.z = v.z + u.z; v.w = v.w + u.w;
+        }
+        acc.x = acc.x + v.x; acc.y = acc.y + v.y; acc.z = acc.z + v.z; acc.w = acc.w + v.w;
+    }
+    reinterpret_cast<float4 *>(y + (int64_t)t * d)[c4] = acc;
 }
 
 template <int QT>
@@ -187,8 +191,8 @@ hipError_t launch_generic_down(int qt, const uint8_t *down, int64_t estride, con
 hipError_t launch_combine(const float *Yr, int ks_r, int64_t stride_r, const float *Ys, int ks_s,
                           int64_t stride_s, const int32_t *inv, const float *topk_w, int T, int K,
                           int S, int d, float *y, hipStream_t st) {
-    hipLaunchKernelGGL(k_combine, dim3(T), dim3(256), 0, st, Yr, ks_r, stride_r, Ys, ks_s,
-                       stride_s, inv, topk_w, T, K, S, d, y);
+    hipLaunchKernelGGL(k_combine, dim3((d / 4 + 255) / 256, T), dim3(256), 0, st, Yr, ks_r,
+                       stride_r, Ys, ks_s, stride_s, inv, topk_w, T, K, S, d, y);
     return hipGetLastError();
 }
 

@@ -1,7 +1,7 @@
 // Router, activation quantisation, top-k and dispatch: one launch.
 //
 // Grid (token groups, expert groups).  A block owns TB tokens x EG experts:
-//   1. stages its x rows and, chunk by chunk, its experts' router rows in LDS
+//   1. stages its x rows and its experts' router rows in LDS
 //      (router transposed to [E, d] at upload so an expert's row is
 //      contiguous);
 //   2. one thread per (token, expert) runs the logit as the reference GEMM
@@ -24,10 +24,10 @@ namespace lcmoe {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kEG = 8;        // experts per block
-constexpr int kKC = 1024;     // router columns per LDS chunk
-constexpr int kPad = 4;       // LDS row padding (floats) against bank conflicts
-constexpr int kMaxXFloats = 16384;
+constexpr int kEG = 8;             // max experts per block
+constexpr int kPad = 4;            // LDS row padding (floats) against bank conflicts
+constexpr int kSlack = 16;         // floats past the last LDS row (chain prefetch overrun)
+constexpr int kLdsFloats = 32768;  // dynamic LDS budget: x rows + router rows
 
 __device__ void select_token(const RouterArgs &a, int t, float *s_z, float *s_s, float *s_g,
                              unsigned char *s_ok, int *s_sel) {
@@ -205,11 +205,75 @@ __device__ void dispatch_block(const RouterArgs &a, int (*s_cw)[kMaxE], int *s_o
     }
 }
 
-__global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB) {
+// rows x d floats from global (row-major) into LDS rows of `stride` floats
+__device__ __forceinline__ void stage_rows(const float *__restrict__ src, float *dst, int rows,
+                                           int d, int stride, int tid) {
+    const int d4 = d / 4, n = rows * d4;
+    for (int base = 0; base < n; base += 8 * kThreads) {
+        float4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            v[i] = reinterpret_cast<const float4 *>(src)[min(base + tid + i * kThreads, n - 1)];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int q = base + tid + i * kThreads;
+            if (q < n) *reinterpret_cast<float4 *>(&dst[(q / d4) * stride + 4 * (q % d4)]) = v[i];
+        }
+    }
+}
+
+template <bool FMA>
+__device__ __forceinline__ float step4(float4 x, float4 w, float acc) {
+    if (FMA) {
+        acc = __builtin_fmaf(x.x, w.x, acc);
+        acc = __builtin_fmaf(x.y, w.y, acc);
+        acc = __builtin_fmaf(x.z, w.z, acc);
+        return __builtin_fmaf(x.w, w.w, acc);
+    }
+    float p;
+    p = x.x * w.x; acc = acc + p;
+    p = x.y * w.y; acc = acc + p;
+    p = x.z * w.z; acc = acc + p;
+    p = x.w * w.w; acc = acc + p;
+    return acc;
+}
+
+// Ascending-k chain over n4 float4 steps (n4 % 8 == 0), operands fetched in
+// groups of 4 float4 (16 k) one group ahead of use.
+template <bool FMA>
+__device__ __forceinline__ float chain16(const float4 *xr, const float4 *wr, int n4, float acc) {
+    float4 xa[4], wa[4], xb[4], wb[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        xa[i] = xr[i];
+        wa[i] = wr[i];
+    }
+    // the last iteration prefetches 4 float4 past the row: the LDS rows are
+    // padded (kSlack) so those reads stay inside the allocation and are unused
+    for (int q = 0; q < n4; q += 8) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            xb[i] = xr[q + 4 + i];
+            wb[i] = wr[q + 4 + i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc = step4<FMA>(xa[i], wa[i], acc);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            xa[i] = xr[q + 8 + i];
+            wa[i] = wr[q + 8 + i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc = step4<FMA>(xb[i], wb[i], acc);
+    }
+    return acc;
+}
+
+__global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB, int EG) {
     extern __shared__ float smem[];
-    const int d = a.d, E = a.E, xstride = d + kPad, wstride = kKC + kPad;
-    float *s_x = smem;                     // [TB][d + pad]
-    float *s_w = smem + TB * xstride;      // [2][EG][KC + pad]
+    const int d = a.d, E = a.E, stride = d + kPad;
+    float *s_x = smem;                // [TB][d + pad]
+    float *s_w = smem + TB * stride;  // [EG][d + pad], this block's router rows
     __shared__ float s_z[4][kMaxE], s_s[4][kMaxE], s_g[4][kMaxE];
     __shared__ unsigned char s_ok[4][kMaxE];
     __shared__ int s_sel[4][kMaxK];
@@ -219,42 +283,11 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB) {
 
     const int tid = threadIdx.x, tg = blockIdx.x, eg = blockIdx.y;
     const int t0 = tg * TB, nt = min(TB, a.T - t0);
-    const int e0 = eg * kEG, ne = min(kEG, E - e0);
+    const int e0 = eg * EG, ne = min(EG, E - e0);
 
-    for (int i = tid; i < nt * (d / 4); i += kThreads) {
-        int t = i / (d / 4), c = i % (d / 4);
-        float4 v = reinterpret_cast<const float4 *>(a.x + (int64_t)(t0 + t) * d)[c];
-        *reinterpret_cast<float4 *>(&s_x[t * xstride + 4 * c]) = v;
-    }
-
-    // chunked router rows: registers -> LDS, one chunk ahead
-    const int nchunks = (d + kKC - 1) / kKC;
-    float4 stage[(kEG * kKC / 4 + kThreads - 1) / kThreads];
-    auto load_chunk = [&](int c) {
-        const int k0 = c * kKC, kn = min(kKC, d - k0), n4 = ne * (kn / 4);
-#pragma unroll
-        for (int i = 0; i < (int)(sizeof(stage) / sizeof(stage[0])); i++) {
-            int q = tid + i * kThreads;
-            if (q < n4) {
-                int e = q / (kn / 4), c4 = q % (kn / 4);
-                stage[i] = reinterpret_cast<const float4 *>(a.wrt + (int64_t)(e0 + e) * d + k0)[c4];
-            }
-        }
-    };
-    auto store_chunk = [&](int c, int buf) {
-        const int k0 = c * kKC, kn = min(kKC, d - k0), n4 = ne * (kn / 4);
-        float *w = s_w + buf * kEG * wstride;
-#pragma unroll
-        for (int i = 0; i < (int)(sizeof(stage) / sizeof(stage[0])); i++) {
-            int q = tid + i * kThreads;
-            if (q < n4) {
-                int e = q / (kn / 4), c4 = q % (kn / 4);
-                *reinterpret_cast<float4 *>(&w[e * wstride + 4 * c4]) = stage[i];
-            }
-        }
-    };
-    load_chunk(0);
-    store_chunk(0, 0);
+    // stage x rows and router rows; 8 loads in flight per thread
+    stage_rows(a.x + (int64_t)t0 * d, s_x, nt, d, stride, tid);
+    stage_rows(a.wrt + (int64_t)e0 * d, s_w, ne, d, stride, tid);
     __syncthreads();
 
     // x limbs for the integer decode path (expert group 0 only)
@@ -262,19 +295,18 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB) {
         const int nsb = d / 32;
         for (int q = tid; q < nt * nsb; q += kThreads) {
             int t = q / nsb, sb = q % nsb;
-            const float *v = &s_x[t * xstride + 32 * sb];
+            const float *v = &s_x[t * stride + 32 * sb];
             float amax = 0.0f;
             for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
-            float s = amax * (1.0f / 16256.0f);
+            float s = amax * (1.0f / 16256.0f), inv = amax > 0.0f ? 16256.0f / amax : 0.0f;
             int isum = 0;
             uint32_t hw[8], lw[8];
+#pragma unroll
             for (int i = 0; i < 8; i++) hw[i] = lw[i] = 0;
+#pragma unroll
             for (int i = 0; i < 32; i++) {
-                int xi = 0;
-                if (amax > 0.0f) {
-                    xi = (int)rintf(v[i] / s);
-                    xi = xi > 16256 ? 16256 : (xi < -16256 ? -16256 : xi);
-                }
+                int xi = (int)rintf(v[i] * inv);  // inv == 0 when the sub-block is all zero
+                xi = xi > 16256 ? 16256 : (xi < -16256 ? -16256 : xi);
                 int hi = (xi + 64) >> 7, lo = xi - 128 * hi;
                 isum += xi;
                 hw[i >> 2] |= (uint32_t)(hi & 0xff) << (8 * (i & 3));
@@ -291,40 +323,17 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB) {
         }
     }
 
-    const bool chain = tid < nt * kEG && (tid % kEG) < ne;
-    const int ct = tid / kEG, ce = tid % kEG, e = e0 + ce;
-    const bool use_fma = e < (E & ~7);
+    // one thread per (token, expert): the sequential logit chain
+    const bool chain = tid < nt * EG && (tid % EG) < ne;
+    const int ct = tid / EG, ce = tid % EG, e = e0 + ce;
     float acc = 0.0f;
-    for (int c = 0; c < nchunks; c++) {
-        if (c + 1 < nchunks) load_chunk(c + 1);
-        if (chain) {
-            const int k0 = c * kKC, kn = min(kKC, d - k0);
-            const float *xr = &s_x[ct * xstride + k0];
-            const float *wr = &s_w[(c & 1) * kEG * wstride + ce * wstride];
-            if (use_fma) {
-                for (int k = 0; k < kn; k += 4) {
-                    float4 xv = *reinterpret_cast<const float4 *>(xr + k);
-                    float4 wv = *reinterpret_cast<const float4 *>(wr + k);
-                    acc = __builtin_fmaf(xv.x, wv.x, acc);
-                    acc = __builtin_fmaf(xv.y, wv.y, acc);
-                    acc = __builtin_fmaf(xv.z, wv.z, acc);
-                    acc = __builtin_fmaf(xv.w, wv.w, acc);
-                }
-            } else {
-                for (int k = 0; k < kn; k += 4) {
-                    float4 xv = *reinterpret_cast<const float4 *>(xr + k);
-                    float4 wv = *reinterpret_cast<const float4 *>(wr + k);
-                    float p;
-                    p = xv.x * wv.x; acc = acc + p;
-                    p = xv.y * wv.y; acc = acc + p;
-                    p = xv.z * wv.z; acc = acc + p;
-                    p = xv.w * wv.w; acc = acc + p;
-                }
-            }
-        }
-        __syncthreads();
-        if (c + 1 < nchunks) store_chunk(c + 1, (c + 1) & 1);
-        __syncthreads();
+    if (chain) {
+        const float4 *xr = reinterpret_cast<const float4 *>(&s_x[ct * stride]);
+        const float4 *wr = reinterpret_cast<const float4 *>(&s_w[ce * stride]);
+        if (e < (E & ~7))
+            acc = chain16<true>(xr, wr, d / 4, acc);
+        else
+            acc = chain16<false>(xr, wr, d / 4, acc);
     }
     if (chain) a.logits[(int64_t)(t0 + ct) * E + e] = acc;
 
@@ -363,32 +372,39 @@ __global__ void k_debug_sigmoid(const float *__restrict__ x, int64_t n, float *_
     if (i < n) out[i] = sigmoid_cw(x[i]);
 }
 
-int tokens_per_group(int d) {
-    int tb = kMaxXFloats / (d + kPad);
-    return tb < 1 ? 1 : (tb > 4 ? 4 : tb);
+// tokens and experts per block so that their x rows and router rows fit in
+// 128 KB of LDS together
+void block_shape(int d, int E, int &TB, int &EG) {
+    const int row = d + kPad, budget = kLdsFloats - kSlack;
+    TB = budget / 2 / row;
+    TB = TB < 1 ? 1 : (TB > 4 ? 4 : TB);
+    EG = (budget - TB * row) / row;
+    EG = EG < 1 ? 1 : (EG > kEG ? kEG : EG);
+    if (EG > E) EG = E;
 }
 
 }  // namespace
 
 int router_token_groups(int T, int d, int E) {
-    (void)E;
-    int tb = tokens_per_group(d);
-    return (T + tb - 1) / tb;
+    int TB, EG;
+    block_shape(d, E, TB, EG);
+    return (T + TB - 1) / TB;
 }
 
 hipError_t launch_router(const RouterArgs &a, hipStream_t st) {
-    const int TB = tokens_per_group(a.d);
-    const int ntg = (a.T + TB - 1) / TB, neg = (a.E + kEG - 1) / kEG;
-    const size_t lds = sizeof(float) * ((size_t)TB * (a.d + kPad) + 2 * kEG * (kKC + kPad));
+    int TB, EG;
+    block_shape(a.d, a.E, TB, EG);
+    const int ntg = (a.T + TB - 1) / TB, neg = (a.E + EG - 1) / EG;
+    const size_t lds = sizeof(float) * ((size_t)(TB + EG) * (a.d + kPad) + kSlack);
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_router),
                                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)(sizeof(float) * (kMaxXFloats + 2 * kEG * (kKC + kPad))));
+                                           (int)(sizeof(float) * kLdsFloats));
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL(k_router, dim3(ntg, neg), dim3(kThreads), lds, st, a, TB);
+    hipLaunchKernelGGL(k_router, dim3(ntg, neg), dim3(kThreads), lds, st, a, TB, EG);
     return hipGetLastError();
 }
 

@@ -145,17 +145,21 @@ struct HOut {
     float *s, *m;   // [positions, F/32]
 };
 
-// Token rows c .. c+NT-1 of one gate/up tile: partial sums of the 4 waves
-// meet in LDS; wave t finishes token t (SwiGLU, then H out).
+constexpr int kMaxNT = 8;
+
+// Token rows c .. c+NT-1 of one gate/up tile (rows past n repeat the last
+// token and are not written): the 4 waves' partial sums meet in LDS, then
+// wave w finishes tokens w and w+4 (SwiGLU, H out).
 template <int NT>
 __device__ __forceinline__ void gateup_chunk(const uint4 *G, const uint4 *U, int kb0, int kb1,
                                              const Limbs &X, const SlotArgs &sa, int p0, int n,
                                              int c, int F, int f, const HOut &out,
-                                             float (*s_red)[2][4][64]) {
+                                             float (*s_red)[2][kMaxNT][64]) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     int row[NT];
 #pragma unroll
-    for (int t = 0; t < NT; t++) row[t] = __builtin_amdgcn_readfirstlane(slot_token(sa, p0, c + t));
+    for (int t = 0; t < NT; t++)
+        row[t] = __builtin_amdgcn_readfirstlane(slot_token(sa, p0, min(c + t, n - 1)));
     float ag[NT], au[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) ag[t] = au[t] = 0.0f;
@@ -166,8 +170,7 @@ __device__ __forceinline__ void gateup_chunk(const uint4 *G, const uint4 *U, int
         s_red[wave][1][t][lane] = au[t];
     }
     __syncthreads();
-    if (wave < NT) {
-        const int t = wave;
+    for (int t = wave; t < NT && c + t < n; t += kWaves) {
         float g = s_red[0][0][t][lane], u = s_red[0][1][t][lane];
 #pragma unroll
         for (int w = 1; w < kWaves; w++) {
@@ -205,7 +208,7 @@ __global__ __launch_bounds__(256) void k_rpl_gateup(
     e = __builtin_amdgcn_readfirstlane(e);
     p0 = __builtin_amdgcn_readfirstlane(p0);
     n = __builtin_amdgcn_readfirstlane(n);
-    __shared__ float s_red[kWaves][2][4][64];
+    __shared__ float s_red[kWaves][2][kMaxNT][64];
     // wave index made provably uniform so block indices and x addresses stay scalar
     const int NB = d >> 8, rt = blockIdx.x, lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -214,32 +217,27 @@ __global__ __launch_bounds__(256) void k_rpl_gateup(
     const uint4 *G = reinterpret_cast<const uint4 *>(gate + (int64_t)e * estride) + tile;
     const uint4 *U = reinterpret_cast<const uint4 *>(up + (int64_t)e * estride) + tile;
     const int f = rt * 64 + lane;
-    for (int c = 0; c < n;) {
+    for (int c = 0; c < n; c += kMaxNT) {
         const int left = n - c;
-        if (left >= 4) {
+        if (left > 4)
+            gateup_chunk<8>(G, U, kb0, kb1, X, sa, p0, n, c, F, f, out, s_red);
+        else if (left > 2)
             gateup_chunk<4>(G, U, kb0, kb1, X, sa, p0, n, c, F, f, out, s_red);
-            c += 4;
-        } else if (left == 3) {
-            gateup_chunk<3>(G, U, kb0, kb1, X, sa, p0, n, c, F, f, out, s_red);
-            c += 3;
-        } else if (left == 2) {
+        else if (left == 2)
             gateup_chunk<2>(G, U, kb0, kb1, X, sa, p0, n, c, F, f, out, s_red);
-            c += 2;
-        } else {
+        else
             gateup_chunk<1>(G, U, kb0, kb1, X, sa, p0, n, c, F, f, out, s_red);
-            c += 1;
-        }
     }
 }
 
 template <int NT>
 __device__ __forceinline__ void down_chunk(const uint4 *W, int kb0, int kb1, const Limbs &X,
-                                           int p0, int c, int d, int r, float *Y,
-                                           float (*s_red)[4][64]) {
+                                           int p0, int n, int c, int d, int r, float *Y,
+                                           float (*s_red)[kMaxNT][64]) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     int row[NT];
 #pragma unroll
-    for (int t = 0; t < NT; t++) row[t] = __builtin_amdgcn_readfirstlane(p0 + c + t);
+    for (int t = 0; t < NT; t++) row[t] = __builtin_amdgcn_readfirstlane(p0 + min(c + t, n - 1));
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) acc[t] = 0.0f;
@@ -247,8 +245,7 @@ __device__ __forceinline__ void down_chunk(const uint4 *W, int kb0, int kb1, con
 #pragma unroll
     for (int t = 0; t < NT; t++) s_red[wave][t][lane] = acc[t];
     __syncthreads();
-    if (wave < NT) {
-        const int t = wave;
+    for (int t = wave; t < NT && c + t < n; t += kWaves) {
         float v = s_red[0][t][lane];
 #pragma unroll
         for (int w = 1; w < kWaves; w++) v = v + s_red[w][t][lane];
@@ -270,7 +267,7 @@ __global__ __launch_bounds__(256) void k_rpl_down(
     e = __builtin_amdgcn_readfirstlane(e);
     p0 = __builtin_amdgcn_readfirstlane(p0);
     n = __builtin_amdgcn_readfirstlane(n);
-    __shared__ float s_red[kWaves][4][64];
+    __shared__ float s_red[kWaves][kMaxNT][64];
     const int NB = F >> 8, rt = blockIdx.x, lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int slices = kWaves * gridDim.z, s = blockIdx.z * kWaves + wave;
@@ -279,21 +276,16 @@ __global__ __launch_bounds__(256) void k_rpl_down(
                      (int64_t)rt * NB * 9 * 64 + lane;
     float *Yz = Y + (int64_t)blockIdx.z * split_stride;
     const int r = rt * 64 + lane;
-    for (int c = 0; c < n;) {
+    for (int c = 0; c < n; c += kMaxNT) {
         const int left = n - c;
-        if (left >= 4) {
-            down_chunk<4>(W, kb0, kb1, X, p0, c, d, r, Yz, s_red);
-            c += 4;
-        } else if (left == 3) {
-            down_chunk<3>(W, kb0, kb1, X, p0, c, d, r, Yz, s_red);
-            c += 3;
-        } else if (left == 2) {
-            down_chunk<2>(W, kb0, kb1, X, p0, c, d, r, Yz, s_red);
-            c += 2;
-        } else {
-            down_chunk<1>(W, kb0, kb1, X, p0, c, d, r, Yz, s_red);
-            c += 1;
-        }
+        if (left > 4)
+            down_chunk<8>(W, kb0, kb1, X, p0, n, c, d, r, Yz, s_red);
+        else if (left > 2)
+            down_chunk<4>(W, kb0, kb1, X, p0, n, c, d, r, Yz, s_red);
+        else if (left == 2)
+            down_chunk<2>(W, kb0, kb1, X, p0, n, c, d, r, Yz, s_red);
+        else
+            down_chunk<1>(W, kb0, kb1, X, p0, n, c, d, r, Yz, s_red);
     }
 }
 

@@ -28,20 +28,25 @@ using namespace lcmoe;
 
 namespace {
 
-enum Slot { kSlotRouter, kSlotGateUp, kSlotGateUpSh, kSlotDown, kSlotDownSh, kSlotCombine, kNumSlots };
-const char *kSlotNames[kNumSlots] = {"router", "gateup", "gateup_shared", "down", "down_shared",
-                                     "combine"};
+enum Slot { kSlotRouter, kSlotPrep, kSlotGateUp, kSlotGateUpSh, kSlotDown, kSlotDownSh,
+            kSlotCombine, kNumSlots };
+const char *kSlotNames[kNumSlots] = {"router", "act16", "gateup", "gateup_shared", "down",
+                                     "down_shared", "combine"};
 constexpr int kMaxKSplit = 4;
+// matrix-core path when an expert family averages at least this many tokens
+constexpr int kMfmaMinTokens = 6;
 
 struct ExpertSet {  // one family of experts (routed or shared)
     int n = 0, F = 0, qt_gu = 0, qt_dn = 0;
     bool rpl_gu = false, rpl_dn = false;
     uint8_t *gate = nullptr, *up = nullptr, *down = nullptr;
     int64_t sz_gu = 0, sz_dn = 0;
-    // H between the two products
+    // H between the two products: f32 (generic down), int8 limbs (row-per-lane
+    // down), f16 hi/lo halves + sub-block sums (matrix-core down)
     float *Hf = nullptr;
     int8_t *hh = nullptr, *hl = nullptr;
     float *hs = nullptr, *hm = nullptr;
+    _Float16 *h16h = nullptr, *h16l = nullptr, *h16s = nullptr;
     // down output partials [kmax][positions][d]
     float *Y = nullptr;
     int kmax = 1;
@@ -60,6 +65,7 @@ struct lcmoe_handle {
     float *x_dev = nullptr, *y_dev = nullptr, *logits = nullptr;
     int8_t *xh = nullptr, *xl = nullptr;
     float *xs = nullptr, *xm = nullptr;
+    _Float16 *x16h = nullptr, *x16l = nullptr, *x16s = nullptr;
     int32_t *topk_idx = nullptr, *counts = nullptr, *offsets = nullptr, *perm = nullptr,
             *inv = nullptr, *touched = nullptr;
     float *topk_w = nullptr;
@@ -198,6 +204,11 @@ lcmoe_status setup_set(lcmoe_handle *h, ExpertSet &s, int n, int F, int qgu, int
     } else {
         if ((st = alloc_n(h, &s.Hf, positions * F))) return st;
     }
+    if (s.rpl_gu) {
+        if ((st = alloc_n(h, &s.h16h, positions * F))) return st;
+        if ((st = alloc_n(h, &s.h16l, positions * F))) return st;
+        if ((st = alloc_n(h, &s.h16s, positions * F / 16))) return st;
+    }
     return alloc_n(h, &s.Y, (size_t)s.kmax * positions * d);
 }
 
@@ -263,6 +274,9 @@ extern "C" lcmoe_status lcmoe_create(const lcmoe_desc *desc, const lcmoe_weights
         if ((st = alloc_n(h, &h->xl, Tm * d))) return bail(st);
         if ((st = alloc_n(h, &h->xs, Tm * d / 32))) return bail(st);
         if ((st = alloc_n(h, &h->xm, Tm * d / 32))) return bail(st);
+        if ((st = alloc_n(h, &h->x16h, Tm * d))) return bail(st);
+        if ((st = alloc_n(h, &h->x16l, Tm * d))) return bail(st);
+        if ((st = alloc_n(h, &h->x16s, Tm * d / 16))) return bail(st);
     }
     if ((st = alloc_n(h, &h->topk_idx, A))) return bail(st);
     if ((st = alloc_n(h, &h->topk_w, A))) return bail(st);
@@ -281,32 +295,48 @@ extern "C" lcmoe_status lcmoe_create(const lcmoe_desc *desc, const lcmoe_weights
 
 extern "C" void lcmoe_destroy(lcmoe_handle *h) { free_handle(h); }
 
-static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const float *x, int T,
-                            hipStream_t st) {
+// Which product kernels serve an expert family this forward.
+struct Plan {
+    bool mfma;
+    int slots, ks;
+};
+
+static Plan plan_set(lcmoe_handle *h, const ExpertSet &s, bool shared, int T) {
     const lcmoe_desc &D = h->desc;
-    const int d = D.d_model, K = D.n_expert_used, E = D.n_expert;
-    const int slots = shared ? s.n : std::min(E, T * K);
-    SlotArgsHost sa{h->perm, h->counts, h->offsets, h->touched, E, K, T, shared ? 1 : 0};
-    HIP_TRY(timed(h, st, shared ? kSlotGateUpSh : kSlotGateUp, [&] {
-        if (s.rpl_gu)
-            return launch_rpl_gateup(s.gate, s.up, s.sz_gu, h->xh, h->xl, h->xs, h->xm, sa, slots,
-                                     d, s.F, s.Hf, s.hh, s.hl, s.hs, s.hm, st);
-        return launch_generic_gateup(s.qt_gu, s.gate, s.up, s.sz_gu, x, sa, slots, d, s.F, s.Hf,
-                                     nullptr, nullptr, nullptr, nullptr, st);
-    }));
-    const int ks = choose_ksplit(s, d, slots);
-    HIP_TRY(timed(h, st, shared ? kSlotDownSh : kSlotDown, [&] {
-        if (s.rpl_dn)
-            return launch_rpl_down(s.down, s.sz_dn, s.hh, s.hl, s.hs, s.hm, sa, slots, d, s.F, ks,
-                                   s.Y, s.positions * d, st);
-        return launch_generic_down(s.qt_dn, s.down, s.sz_dn, s.Hf, sa, slots, d, s.F, s.Y, st);
-    }));
-    return LCMOE_OK;
+    Plan p;
+    p.slots = shared ? s.n : std::min(D.n_expert, T * D.n_expert_used);
+    const int avg = shared ? T : (T * D.n_expert_used) / std::max(1, p.slots);
+    p.mfma = s.rpl_gu && avg >= kMfmaMinTokens;
+    p.ks = choose_ksplit(s, D.d_model, p.slots);
+    return p;
 }
 
-static int last_ksplit(lcmoe_handle *h, ExpertSet &s, bool shared, int T) {
-    const int slots = shared ? s.n : std::min(h->desc.n_expert, T * h->desc.n_expert_used);
-    return choose_ksplit(s, h->desc.d_model, slots);
+static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const float *x, int T,
+                            const Plan &pl, hipStream_t st) {
+    const lcmoe_desc &D = h->desc;
+    const int d = D.d_model, K = D.n_expert_used, E = D.n_expert;
+    SlotArgsHost sa{h->perm, h->counts, h->offsets, h->touched, E, K, T, shared ? 1 : 0};
+    HIP_TRY(timed(h, st, shared ? kSlotGateUpSh : kSlotGateUp, [&] {
+        if (pl.mfma)
+            return launch_mfma_gateup(s.gate, s.up, s.sz_gu, h->x16h, h->x16l, h->x16s, sa,
+                                      pl.slots, d, s.F, s.h16h, s.h16l, s.h16s,
+                                      s.rpl_dn ? nullptr : s.Hf, st);
+        if (s.rpl_gu)
+            return launch_rpl_gateup(s.gate, s.up, s.sz_gu, h->xh, h->xl, h->xs, h->xm, sa,
+                                     pl.slots, d, s.F, s.Hf, s.hh, s.hl, s.hs, s.hm, st);
+        return launch_generic_gateup(s.qt_gu, s.gate, s.up, s.sz_gu, x, sa, pl.slots, d, s.F,
+                                     s.Hf, nullptr, nullptr, nullptr, nullptr, st);
+    }));
+    HIP_TRY(timed(h, st, shared ? kSlotDownSh : kSlotDown, [&] {
+        if (s.rpl_dn && pl.mfma)
+            return launch_mfma_down(s.down, s.sz_dn, s.h16h, s.h16l, s.h16s, sa, pl.slots, d, s.F,
+                                    pl.ks, s.Y, s.positions * d, st);
+        if (s.rpl_dn)
+            return launch_rpl_down(s.down, s.sz_dn, s.hh, s.hl, s.hs, s.hm, sa, pl.slots, d, s.F,
+                                   pl.ks, s.Y, s.positions * d, st);
+        return launch_generic_down(s.qt_dn, s.down, s.sz_dn, s.Hf, sa, pl.slots, d, s.F, s.Y, st);
+    }));
+    return LCMOE_OK;
 }
 
 static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, float *y,
@@ -336,11 +366,16 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
     ra.touched = h->touched;
     ra.sync = h->sync;
     HIP_TRY(timed(h, st, kSlotRouter, [&] { return launch_router(ra, st); }));
+    const Plan pr = plan_set(h, h->routed, false, T);
+    const Plan ps = S > 0 ? plan_set(h, h->shared, true, T) : Plan{false, 0, 1};
+    if (pr.mfma || ps.mfma)
+        HIP_TRY(timed(h, st, kSlotPrep, [&] {
+            return launch_act16(x, T, d, h->x16h, h->x16l, h->x16s, st);
+        }));
     lcmoe_status s;
-    if ((s = run_set(h, h->routed, false, x, T, st))) return s;
-    if (S > 0 && (s = run_set(h, h->shared, true, x, T, st))) return s;
-    const int ks_r = last_ksplit(h, h->routed, false, T);
-    const int ks_s = S > 0 ? last_ksplit(h, h->shared, true, T) : 1;
+    if ((s = run_set(h, h->routed, false, x, T, pr, st))) return s;
+    if (S > 0 && (s = run_set(h, h->shared, true, x, T, ps, st))) return s;
+    const int ks_r = pr.ks, ks_s = ps.ks;
     HIP_TRY(timed(h, st, kSlotCombine, [&] {
         return launch_combine(h->routed.Y, ks_r, h->routed.positions * d, h->shared.Y, ks_s,
                               h->shared.positions * d, h->inv, h->topk_w, T, K, S, d, y, st);
