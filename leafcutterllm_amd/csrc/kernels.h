@@ -57,18 +57,17 @@ hipError_t launch_rpl_down(const uint8_t *down, int64_t estride, const int8_t *h
                            const SlotArgsHost &sa, int slots, int d, int F, int ksplit, float *Y,
                            int64_t split_stride, hipStream_t st);
 
-// Matrix-core path on the RPL64 layout: activations as permuted f16 hi/lo
-// halves plus per-sub-block sums, H out in the same format.
-hipError_t launch_act16(const float *x, int T, int d, _Float16 *xh, _Float16 *xl, _Float16 *xs,
-                        hipStream_t st);
+// Matrix-core path on the RPL64 layout: activations as f16 hi/lo pieces
+// (per token and super-block: hi[256] then lo[256]) plus per-sub-block sums,
+// H out in the same format (and/or f32).
+hipError_t launch_act16(const float *x, int T, int d, _Float16 *x16, _Float16 *xs, hipStream_t st);
 hipError_t launch_mfma_gateup(const uint8_t *gate, const uint8_t *up, int64_t estride,
-                              const _Float16 *xh, const _Float16 *xl, const _Float16 *xs,
-                              const SlotArgsHost &sa, int slots, int d, int F, _Float16 *oh,
-                              _Float16 *ol, _Float16 *os, float *of, hipStream_t st);
-hipError_t launch_mfma_down(const uint8_t *down, int64_t estride, const _Float16 *hh,
-                            const _Float16 *hl, const _Float16 *hs, const SlotArgsHost &sa,
-                            int slots, int d, int F, int ksplit, float *Y, int64_t split_stride,
-                            hipStream_t st);
+                              const _Float16 *x16, const _Float16 *xs, const SlotArgsHost &sa,
+                              int slots, int d, int F, _Float16 *h16, _Float16 *hs, float *hf,
+                              hipStream_t st);
+hipError_t launch_mfma_down(const uint8_t *down, int64_t estride, const _Float16 *h16,
+                            const _Float16 *hs, const SlotArgsHost &sa, int slots, int d, int F,
+                            int ksplit, float *Y, int64_t split_stride, hipStream_t st);
 
 // y[t] = sum_k w[t,k] * sum_s Yr[s][inv[t,k]] + sum_j sum_s Ys[s][j*T + t].
 hipError_t launch_combine(const float *Yr, int ks_r, int64_t stride_r, const float *Ys, int ks_s,

@@ -46,7 +46,7 @@ struct ExpertSet {  // one family of experts (routed or shared)
     float *Hf = nullptr;
     int8_t *hh = nullptr, *hl = nullptr;
     float *hs = nullptr, *hm = nullptr;
-    _Float16 *h16h = nullptr, *h16l = nullptr, *h16s = nullptr;
+    _Float16 *h16 = nullptr, *h16s = nullptr;  // [positions][F/256][hi 256 | lo 256], sums
     // down output partials [kmax][positions][d]
     float *Y = nullptr;
     int kmax = 1;
@@ -65,7 +65,7 @@ struct lcmoe_handle {
     float *x_dev = nullptr, *y_dev = nullptr, *logits = nullptr;
     int8_t *xh = nullptr, *xl = nullptr;
     float *xs = nullptr, *xm = nullptr;
-    _Float16 *x16h = nullptr, *x16l = nullptr, *x16s = nullptr;
+    _Float16 *x16 = nullptr, *x16s = nullptr;
     int32_t *topk_idx = nullptr, *counts = nullptr, *offsets = nullptr, *perm = nullptr,
             *inv = nullptr, *touched = nullptr;
     float *topk_w = nullptr;
@@ -180,6 +180,15 @@ int choose_ksplit(const ExpertSet &s, int d, int active) {
     return ks;
 }
 
+// Matrix-core down: 128-row blocks, two resident per CU; split K until
+// about two blocks per CU exist, keeping >= 4 super-blocks per split.
+int choose_ksplit_mfma(const ExpertSet &s, int d, int active) {
+    const int NB = s.F / 256, blocks = ((d / 32 + 3) / 4) * std::max(1, active);
+    int ks = 1;
+    while (ks < s.kmax && blocks * ks < 512 && NB >= 4 * ks * 2) ks *= 2;
+    return ks;
+}
+
 lcmoe_status setup_set(lcmoe_handle *h, ExpertSet &s, int n, int F, int qgu, int qdn,
                        const uint8_t *gate, const uint8_t *up, const uint8_t *down, int64_t positions) {
     const int64_t d = h->desc.d_model;
@@ -205,8 +214,7 @@ lcmoe_status setup_set(lcmoe_handle *h, ExpertSet &s, int n, int F, int qgu, int
         if ((st = alloc_n(h, &s.Hf, positions * F))) return st;
     }
     if (s.rpl_gu) {
-        if ((st = alloc_n(h, &s.h16h, positions * F))) return st;
-        if ((st = alloc_n(h, &s.h16l, positions * F))) return st;
+        if ((st = alloc_n(h, &s.h16, 2 * positions * F))) return st;
         if ((st = alloc_n(h, &s.h16s, positions * F / 16))) return st;
     }
     return alloc_n(h, &s.Y, (size_t)s.kmax * positions * d);
@@ -274,8 +282,7 @@ extern "C" lcmoe_status lcmoe_create(const lcmoe_desc *desc, const lcmoe_weights
         if ((st = alloc_n(h, &h->xl, Tm * d))) return bail(st);
         if ((st = alloc_n(h, &h->xs, Tm * d / 32))) return bail(st);
         if ((st = alloc_n(h, &h->xm, Tm * d / 32))) return bail(st);
-        if ((st = alloc_n(h, &h->x16h, Tm * d))) return bail(st);
-        if ((st = alloc_n(h, &h->x16l, Tm * d))) return bail(st);
+        if ((st = alloc_n(h, &h->x16, 2 * Tm * d))) return bail(st);
         if ((st = alloc_n(h, &h->x16s, Tm * d / 16))) return bail(st);
     }
     if ((st = alloc_n(h, &h->topk_idx, A))) return bail(st);
@@ -307,7 +314,8 @@ static Plan plan_set(lcmoe_handle *h, const ExpertSet &s, bool shared, int T) {
     p.slots = shared ? s.n : std::min(D.n_expert, T * D.n_expert_used);
     const int avg = shared ? T : (T * D.n_expert_used) / std::max(1, p.slots);
     p.mfma = s.rpl_gu && avg >= kMfmaMinTokens;
-    p.ks = choose_ksplit(s, D.d_model, p.slots);
+    p.ks = p.mfma && s.rpl_dn ? choose_ksplit_mfma(s, D.d_model, p.slots)
+                               : choose_ksplit(s, D.d_model, p.slots);
     return p;
 }
 
@@ -318,8 +326,8 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
     SlotArgsHost sa{h->perm, h->counts, h->offsets, h->touched, E, K, T, shared ? 1 : 0};
     HIP_TRY(timed(h, st, shared ? kSlotGateUpSh : kSlotGateUp, [&] {
         if (pl.mfma)
-            return launch_mfma_gateup(s.gate, s.up, s.sz_gu, h->x16h, h->x16l, h->x16s, sa,
-                                      pl.slots, d, s.F, s.h16h, s.h16l, s.h16s,
+            return launch_mfma_gateup(s.gate, s.up, s.sz_gu, h->x16, h->x16s, sa, pl.slots, d,
+                                      s.F, s.rpl_dn ? s.h16 : nullptr, s.h16s,
                                       s.rpl_dn ? nullptr : s.Hf, st);
         if (s.rpl_gu)
             return launch_rpl_gateup(s.gate, s.up, s.sz_gu, h->xh, h->xl, h->xs, h->xm, sa,
@@ -329,7 +337,7 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
     }));
     HIP_TRY(timed(h, st, shared ? kSlotDownSh : kSlotDown, [&] {
         if (s.rpl_dn && pl.mfma)
-            return launch_mfma_down(s.down, s.sz_dn, s.h16h, s.h16l, s.h16s, sa, pl.slots, d, s.F,
+            return launch_mfma_down(s.down, s.sz_dn, s.h16, s.h16s, sa, pl.slots, d, s.F,
                                     pl.ks, s.Y, s.positions * d, st);
         if (s.rpl_dn)
             return launch_rpl_down(s.down, s.sz_dn, s.hh, s.hl, s.hs, s.hm, sa, pl.slots, d, s.F,
@@ -370,7 +378,7 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
     const Plan ps = S > 0 ? plan_set(h, h->shared, true, T) : Plan{false, 0, 1};
     if (pr.mfma || ps.mfma)
         HIP_TRY(timed(h, st, kSlotPrep, [&] {
-            return launch_act16(x, T, d, h->x16h, h->x16l, h->x16s, st);
+            return launch_act16(x, T, d, h->x16, h->x16s, st);
         }));
     lcmoe_status s;
     if ((s = run_set(h, h->routed, false, x, T, pr, st))) return s;
