@@ -105,19 +105,52 @@ __global__ __launch_bounds__(256) void k_down(const uint8_t *__restrict__ down, 
 
 // y[t] = sum_k w[t,k] * (sum over splits Yr[s][inv[t*K+k]]) + shared terms,
 // slot order then shared order; each term rounded then added.  Grid
-// (column blocks of 1024, tokens); one float4 of columns per thread.
+// (column blocks of 1024, tokens); one float4 of columns per thread.  With
+// cr.logits the token's routing weights are first computed from the exact
+// logits and the selection (the expressions of CpuBackend::softmax,
+// rust/src/backend/cpu.rs:66-79: max, sequential sum of exp, divide) and
+// the first column block stores them to topk_w.
 __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ Yr, int ks_r,
                                                  int64_t stride_r, const float *__restrict__ Ys,
                                                  int ks_s, int64_t stride_s,
                                                  const int32_t *__restrict__ inv,
-                                                 const float *__restrict__ topk_w, int T, int K,
-                                                 int S, int d, float *__restrict__ y) {
+                                                 float *__restrict__ topk_w, int T, int K, int S,
+                                                 int d, CombineRoute cr, float *__restrict__ y) {
+    __shared__ float s_w[kMaxK];
     const int t = blockIdx.y, c4 = blockIdx.x * blockDim.x + threadIdx.x;
+    if (cr.logits) {
+        if (threadIdx.x == 0) {
+            const float *l = cr.logits + (int64_t)t * cr.E;
+            const int32_t *sel = cr.topk_idx + (int64_t)t * K;
+            float mx = -__builtin_inff(), sum = 0.0f;
+            if (cr.kind == LCMOE_ROUTE_SOFTMAX_RENORM) {  // softmax over the K selected
+                for (int k = 0; k < K; k++) {
+                    const int e = sel[k];
+                    mx = nan_max(mx, cr.bias ? l[e] + cr.bias[e] : l[e]);
+                }
+                for (int k = 0; k < K; k++) {
+                    const int e = sel[k];
+                    sum = sum + expf((cr.bias ? l[e] + cr.bias[e] : l[e]) - mx);
+                }
+            } else {  // full-E softmax probabilities of the selected experts
+                for (int e = 0; e < cr.E; e++) mx = nan_max(mx, cr.bias ? l[e] + cr.bias[e] : l[e]);
+                for (int e = 0; e < cr.E; e++)
+                    sum = sum + expf((cr.bias ? l[e] + cr.bias[e] : l[e]) - mx);
+            }
+            for (int k = 0; k < K; k++) {
+                const int e = sel[k];
+                const float w = (expf((cr.bias ? l[e] + cr.bias[e] : l[e]) - mx) / sum) * cr.scale;
+                s_w[k] = w;
+                if (blockIdx.x == 0) topk_w[(int64_t)t * K + k] = w;
+            }
+        }
+        __syncthreads();
+    }
     if (4 * c4 >= d) return;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int k = 0; k < K; k++) {
         const int pos = inv[(int64_t)t * K + k];
-        const float w = topk_w[(int64_t)t * K + k];
+        const float w = cr.logits ? s_w[k] : topk_w[(int64_t)t * K + k];
         const float4 *src = reinterpret_cast<const float4 *>(Yr + (int64_t)pos * d) + c4;
         float4 v = src[0];
         for (int s = 1; s < ks_r; s++) {
@@ -189,10 +222,10 @@ hipError_t launch_generic_down(int qt, const uint8_t *down, int64_t estride, con
 }
 
 hipError_t launch_combine(const float *Yr, int ks_r, int64_t stride_r, const float *Ys, int ks_s,
-                          int64_t stride_s, const int32_t *inv, const float *topk_w, int T, int K,
-                          int S, int d, float *y, hipStream_t st) {
+                          int64_t stride_s, const int32_t *inv, float *topk_w, int T, int K,
+                          int S, int d, const CombineRoute &cr, float *y, hipStream_t st) {
     hipLaunchKernelGGL(k_combine, dim3((d / 4 + 255) / 256, T), dim3(256), 0, st, Yr, ks_r,
-                       stride_r, Ys, ks_s, stride_s, inv, topk_w, T, K, S, d, y);
+                       stride_r, Ys, ks_s, stride_s, inv, topk_w, T, K, S, d, cr, y);
     return hipGetLastError();
 }
 

@@ -29,6 +29,40 @@ constexpr int kPad = 4;            // LDS row padding (floats) against bank conf
 constexpr int kSlack = 16;         // floats past the last LDS row (chain prefetch overrun)
 constexpr int kLdsFloats = 32768;  // dynamic LDS budget: x rows + router rows
 
+// Device-coherent (all XCDs) store and load of one int: agent-scope relaxed
+// atomics write through / read past the XCD-private L2, so a value published
+// this way needs no cache write-back fence, only the store's completion.
+__device__ __forceinline__ void store_agent(int32_t *p, int32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t load_agent(const int32_t *p) {
+    return __hip_atomic_load(const_cast<int32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Routing weights of token t from its scores s_z (sigmoid scores s_s for the
+// group router) and its selection sel[0..K), in slot order (one thread).
+__device__ void token_weights(const RouterArgs &a, int t, const float *s_z, const float *s_s,
+                              const int *sel) {
+    const int E = a.E, K = a.K;
+    const RouteParams &rp = a.rp;
+    float *ow = a.topk_w + (int64_t)t * K;
+    if (rp.kind == LCMOE_ROUTE_SIGMOID_GROUP) {
+        float sum = 0.0f;
+        for (int k = 0; k < K; k++) sum = sum + s_s[sel[k]];
+        for (int k = 0; k < K; k++) ow[k] = (s_s[sel[k]] / sum) * rp.scale;
+    } else if (rp.kind == LCMOE_ROUTE_SOFTMAX_RENORM) {  // cpu.rs:66-79 over the K
+        float mx = -__builtin_inff(), sum = 0.0f;
+        for (int k = 0; k < K; k++) mx = nan_max(mx, s_z[sel[k]]);
+        for (int k = 0; k < K; k++) sum = sum + expf(s_z[sel[k]] - mx);
+        for (int k = 0; k < K; k++) ow[k] = (expf(s_z[sel[k]] - mx) / sum) * rp.scale;
+    } else {  // full-E softmax probabilities of the selected experts
+        float mx = -__builtin_inff(), sum = 0.0f;
+        for (int e = 0; e < E; e++) mx = nan_max(mx, s_z[e]);
+        for (int e = 0; e < E; e++) sum = sum + expf(s_z[e] - mx);
+        for (int k = 0; k < K; k++) ow[k] = (expf(s_z[sel[k]] - mx) / sum) * rp.scale;
+    }
+}
+
 __device__ void select_token(const RouterArgs &a, int t, float *s_z, float *s_s, float *s_g,
                              unsigned char *s_ok, int *s_sel) {
     // one wave: lane-strided over experts; s_* are this wave's LDS rows
@@ -124,24 +158,9 @@ __device__ void select_token(const RouterArgs &a, int t, float *s_z, float *s_s,
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     if (lane == 0) {
+        token_weights(a, t, s_z, s_s, s_sel);
         int32_t *oi = a.topk_idx + (int64_t)t * K;
-        float *ow = a.topk_w + (int64_t)t * K;
-        if (rp.kind == LCMOE_ROUTE_SIGMOID_GROUP) {
-            float sum = 0.0f;
-            for (int k = 0; k < K; k++) sum = sum + s_s[s_sel[k]];
-            for (int k = 0; k < K; k++) ow[k] = (s_s[s_sel[k]] / sum) * rp.scale;
-        } else if (rp.kind == LCMOE_ROUTE_SOFTMAX_RENORM) {  // cpu.rs:66-79 over the K
-            float mx = -__builtin_inff(), sum = 0.0f;
-            for (int k = 0; k < K; k++) mx = nan_max(mx, s_z[s_sel[k]]);
-            for (int k = 0; k < K; k++) sum = sum + expf(s_z[s_sel[k]] - mx);
-            for (int k = 0; k < K; k++) ow[k] = (expf(s_z[s_sel[k]] - mx) / sum) * rp.scale;
-        } else {  // full-E softmax probabilities of the selected experts
-            float mx = -__builtin_inff(), sum = 0.0f;
-            for (int e = 0; e < E; e++) mx = nan_max(mx, s_z[e]);
-            for (int e = 0; e < E; e++) sum = sum + expf(s_z[e] - mx);
-            for (int k = 0; k < K; k++) ow[k] = (expf(s_z[s_sel[k]] - mx) / sum) * rp.scale;
-        }
-        for (int k = 0; k < K; k++) oi[k] = s_sel[k];
+        for (int k = 0; k < K; k++) store_agent(oi + k, s_sel[k]);
     }
 }
 
@@ -150,15 +169,16 @@ __device__ void select_token(const RouterArgs &a, int t, float *s_z, float *s_s,
 // per (wave, expert), prefixes over waves and experts give each wave its base
 // per expert, pass 2 ranks equal experts inside each 64-assignment group with
 // ballots (lower lane = lower a) and advances the wave's private counters.
+template <int NT>
 __device__ void dispatch_block(const RouterArgs &a, int (*s_cw)[kMaxE], int *s_off) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int A = a.T * a.K, E = a.E;
-    constexpr int W = kThreads / 64;
-    for (int i = tid; i < W * kMaxE; i += kThreads) (&s_cw[0][0])[i] = 0;
+    constexpr int W = NT / 64;
+    for (int i = tid; i < W * kMaxE; i += NT) (&s_cw[0][0])[i] = 0;
     __syncthreads();
     const int chunk = (((A + W - 1) / W) + 63) & ~63;
     const int a0 = min(A, wave * chunk), a1 = min(A, a0 + chunk);
-    for (int q = a0 + lane; q < a1; q += 64) atomicAdd(&s_cw[wave][a.topk_idx[q]], 1);
+    for (int q = a0 + lane; q < a1; q += 64) atomicAdd(&s_cw[wave][load_agent(a.topk_idx + q)], 1);
     __syncthreads();
     if (tid < E) {
         int run = 0;
@@ -188,7 +208,7 @@ __device__ void dispatch_block(const RouterArgs &a, int (*s_cw)[kMaxE], int *s_o
     for (int base = a0; base < a1; base += 64) {
         const int q = base + lane;
         const bool valid = q < a1;
-        const int e = valid ? a.topk_idx[q] : 0;
+        const int e = valid ? load_agent(a.topk_idx + q) : 0;
         uint64_t mask = __ballot(valid);
 #pragma unroll
         for (int b = 0; b < 8; b++) {
@@ -269,7 +289,12 @@ __device__ __forceinline__ float chain16(const float4 *xr, const float4 *wr, int
     return acc;
 }
 
-__global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB, int EG) {
+// mode 0: exact logits, x limbs, top-k and dispatch (the whole router).
+// mode 1: exact logits and the routing weights of an already-made selection
+// (a.topk_idx), nothing else.
+// mode 2: exact logits only; runs beside the certified fast router and the
+// expert products, and the combine turns them into routing weights.
+__global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB, int EG, int mode) {
     extern __shared__ float smem[];
     const int d = a.d, E = a.E, stride = d + kPad;
     float *s_x = smem;                // [TB][d + pad]
@@ -291,7 +316,7 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB, int E
     __syncthreads();
 
     // x limbs for the integer decode path (expert group 0 only)
-    if (eg == 0 && a.xh) {
+    if (mode == 0 && eg == 0 && a.xh) {
         const int nsb = d / 32;
         for (int q = tid; q < nt * nsb; q += kThreads) {
             int t = q / nsb, sb = q % nsb;
@@ -336,6 +361,7 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB, int E
             acc = chain16<false>(xr, wr, d / 4, acc);
     }
     if (chain) a.logits[(int64_t)(t0 + ct) * E + e] = acc;
+    if (mode == 2) return;  // logits only
 
     // ---- last expert-group block of this token group selects top-k
     const int n_eg = gridDim.y, n_tg = gridDim.x;
@@ -349,6 +375,31 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB, int E
     if (!s_flag) return;
     __threadfence();
     const int wave = tid >> 6;
+    if (mode == 1) {
+        const int lane = tid & 63;
+        for (int t = t0 + wave; t < t0 + nt; t += kThreads / 64) {
+            const float *l = a.logits + (int64_t)t * E;
+            for (int e = lane; e < E; e += 64) {
+                const float v = l[e];
+                if (a.rp.kind == LCMOE_ROUTE_SIGMOID_GROUP) {
+                    const float sg = sigmoid_cw(v);
+                    s_s[wave][e] = sg;
+                    s_z[wave][e] = a.rp.has_bias ? sg + a.bias[e] : sg;
+                } else {
+                    s_z[wave][e] = a.rp.has_bias ? v + a.bias[e] : v;
+                }
+            }
+            if (lane < a.K) s_sel[wave][lane] = a.topk_idx[(int64_t)t * a.K + lane];
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            if (lane == 0) token_weights(a, t, s_z[wave], s_s[wave], s_sel[wave]);
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        }
+        __syncthreads();
+        if (tid == 0) a.sync[tg] = 0;
+        return;
+    }
     for (int t = wave; t < nt; t += kThreads / 64)
         select_token(a, t0 + t, s_z[wave], s_s[wave], s_g[wave], s_ok[wave], s_sel[wave]);
 
@@ -363,8 +414,347 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB, int E
     __syncthreads();
     if (!s_flag) return;
     __threadfence();
-    dispatch_block(a, s_cw, s_off);
+    dispatch_block<kThreads>(a, s_cw, s_off);
     if (tid == 0) a.sync[n_tg] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// Certified fast router (softmax kinds).  One block per token.
+//
+// The reference logit is the sequential f32 chain s_k = fl(s_{k-1} + x_k w_k)
+// (one rounding per step on the FMA lanes; two on the mul+add tail lanes).
+// Its final value c differs from the exact sum S_d = sum_k x_k w_k by at most
+//   u (1 + 1.01 d u) sum_k |S_k|                      (FMA lanes)
+//   + u (1+u)(1 + 1.01 d u) sum_k |x_k w_k|           (tail lanes, extra)
+// with u = 2^-24 and S_k the exact prefix sums: each step adds at most
+// u |S_k + e_{k-1}| to the error e.  Each wave computes, for one expert, S_d
+// and sum_k |S_k| in float64 (products of two floats are exact in float64;
+// a 64-lane scan gives every lane its chunk's prefix), plus a margin for the
+// float64 roundings.  That bounds the chain's value to [S_d - B, S_d + B],
+// hence the score z = fl(c + bias) to [zlo, zhi] (rounding is monotone).
+// If the intervals order the top-k experts strictly (rank by rank, and the
+// k-th against every unselected expert), the reference chain selects exactly
+// those experts in that order, and the selection is final.  Otherwise the
+// block runs the exact chains for that token and selects from them.  The
+// routing weights need the chain values themselves; mode 1 of k_router
+// computes them beside the expert products.
+// ---------------------------------------------------------------------------
+
+// next float toward +inf / -inf (finite, non-NaN arguments)
+__device__ __forceinline__ float next_up(float f) {
+    if (f == 0.0f) return __uint_as_float(1u);
+    const uint32_t b = __float_as_uint(f);
+    return __uint_as_float(f > 0.0f ? b + 1u : b - 1u);
+}
+__device__ __forceinline__ float next_down(float f) { return -next_up(-f); }
+// smallest float >= v, largest float <= v (finite v)
+__device__ __forceinline__ float ceil_f32(double v) {
+    const float f = (float)v;
+    return (double)f < v ? next_up(f) : f;
+}
+__device__ __forceinline__ float floor_f32(double v) {
+    const float f = (float)v;
+    return (double)f > v ? next_down(f) : f;
+}
+
+constexpr int kFastThreads = 512;  // 8 waves: one expert per wave for E = 8
+
+// Activations of token t for the expert products: int8 limbs for the
+// row-per-lane kernels and f16 hi/lo pieces + sub-block sums for the
+// matrix-core kernels.  Four threads share a 32-column sub-block, eight
+// columns each, and meet through lane shuffles.
+__device__ void quantise_token(const RouterArgs &a, int t) {
+    const int d = a.d, nsb = d / 32;
+    for (int q = threadIdx.x; q < 4 * nsb; q += kFastThreads) {
+        const int sb = q >> 2, part = q & 3, col0 = 32 * sb + 8 * part;
+        const float4 *v = reinterpret_cast<const float4 *>(a.x + (int64_t)t * d + col0);
+        const float4 v0 = v[0], v1 = v[1];
+        const float f[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        if (a.xh) {
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(f[i]));
+            amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+            amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+            const float sc = amax * (1.0f / 16256.0f), inv = amax > 0.0f ? 16256.0f / amax : 0.0f;
+            int isum = 0;
+            uint32_t hw[2] = {0, 0}, lw[2] = {0, 0};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                int xi = (int)rintf(f[i] * inv);  // inv == 0 when the sub-block is all zero
+                xi = xi > 16256 ? 16256 : (xi < -16256 ? -16256 : xi);
+                const int hi = (xi + 64) >> 7, lo = xi - 128 * hi;
+                isum += xi;
+                hw[i >> 2] |= (uint32_t)(hi & 0xff) << (8 * (i & 3));
+                lw[i >> 2] |= (uint32_t)(lo & 0xff) << (8 * (i & 3));
+            }
+            isum += __shfl_xor(isum, 1, 64);
+            isum += __shfl_xor(isum, 2, 64);
+            const int64_t off = (int64_t)t * d + col0;
+            *reinterpret_cast<uint2 *>(a.xh + off) = make_uint2(hw[0], hw[1]);
+            *reinterpret_cast<uint2 *>(a.xl + off) = make_uint2(lw[0], lw[1]);
+            if (part == 0) {
+                a.xs[(int64_t)t * nsb + sb] = sc;
+                a.xm[(int64_t)t * nsb + sb] = sc * (float)isum;
+            }
+        }
+        if (a.x16) {
+            typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+            half8v hv, lv;
+            float sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const _Float16 hi = (_Float16)f[i];
+                const _Float16 lo = (_Float16)(f[i] - (float)hi);
+                hv[i] = hi;
+                lv[i] = lo;
+                sum = sum + ((float)hi + (float)lo);
+            }
+            // the sub-block sum in column order: (c0..7 + c8..15) + (c16..23 + c24..31)
+            sum = sum + __shfl_xor(sum, 1, 64);
+            sum = sum + __shfl_xor(sum, 2, 64);
+            _Float16 *piece = a.x16 + ((int64_t)t * (d >> 8) + (sb >> 3)) * 512 + 32 * (sb & 7) +
+                              8 * part;
+            *reinterpret_cast<half8v *>(piece) = hv;
+            *reinterpret_cast<half8v *>(piece + 256) = lv;
+            if (part == 0) {
+                const _Float16 shi = (_Float16)sum, slo = (_Float16)(sum - (float)shi);
+                a.x16s[((int64_t)t * nsb + sb) * 2] = shi;
+                a.x16s[((int64_t)t * nsb + sb) * 2 + 1] = slo;
+            }
+        }
+    }
+}
+
+// exact reference chain of expert e for token t (fallback path): operands in
+// batches of 32 columns, the next batch loading while this one chains
+__device__ float exact_logit(const RouterArgs &a, int t, int e) {
+    const int d = a.d, n8 = d / 32;
+    const float4 *xr = reinterpret_cast<const float4 *>(a.x + (int64_t)t * d);
+    const float4 *wr = reinterpret_cast<const float4 *>(a.wrt + (int64_t)e * d);
+    const bool fma = e < (a.E & ~7);
+    float4 xa[8], wa[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        xa[i] = xr[i];
+        wa[i] = wr[i];
+    }
+    float acc = 0.0f;
+    for (int b = 0; b < n8; b++) {
+        float4 xb[8], wb[8];
+        const int nb = min(b + 1, n8 - 1);  // the last batch re-reads itself (unused)
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            xb[i] = xr[8 * nb + i];
+            wb[i] = wr[8 * nb + i];
+        }
+        if (fma) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc = step4<true>(xa[i], wa[i], acc);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc = step4<false>(xa[i], wa[i], acc);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            xa[i] = xb[i];
+            wa[i] = wb[i];
+        }
+    }
+    return acc;
+}
+
+// float64 logit S_d and chain error bound of every expert for token t; wave
+// w takes experts w, w+8, ...; lane l holds columns [l*C, l*C + C) with
+// C = 4*NC4 in registers.  sum_k |S_k| is bounded by groups of 4 columns:
+// for k in group g, |S_k| <= |S_g| + sum_{i in g} |p_i| with S_g the prefix
+// before the group, so sum_k |S_k| <= 4 sum_g |S_g| + 4 sum_i |p_i|.
+template <int NC4>
+struct LogitRegs {
+    float4 wv[NC4];
+    const float *xs;  // this lane's token chunk in LDS
+};
+
+// this wave's first expert's router chunk, one coalesced KiB per load (the
+// lane-chunk order a.wlc)
+template <int NC4>
+__device__ __forceinline__ void load_wchunk(const RouterArgs &a, int e, float4 (&wv)[NC4]) {
+    const int lane = threadIdx.x & 63;
+    const float4 *wr = reinterpret_cast<const float4 *>(a.wlc) + (int64_t)e * NC4 * 64 + lane;
+#pragma unroll
+    for (int i = 0; i < NC4; i++) wv[i] = wr[64 * i];
+}
+
+// token row into LDS (coalesced); lane l's chunk is row l of C + 4 floats,
+// which keeps 8 consecutive lanes' b128 reads on distinct banks
+template <int NC4>
+__device__ __forceinline__ const float *stage_xrow(const RouterArgs &a, int t, float *s_x) {
+    constexpr int C = 4 * NC4;
+    const int d = a.d, lane = threadIdx.x & 63;
+    const float4 *xr = reinterpret_cast<const float4 *>(a.x + (int64_t)t * d);
+    for (int q = threadIdx.x; q < d / 4; q += kFastThreads)
+        *reinterpret_cast<float4 *>(s_x + (q / NC4) * (C + 4) + 4 * (q % NC4)) = xr[q];
+    __syncthreads();
+    return s_x + lane * (C + 4);
+}
+
+template <int NC4>
+__device__ __forceinline__ void logit_bounds(const RouterArgs &a, LogitRegs<NC4> &R, double *s_a,
+                                             double *s_b) {
+    constexpr int W = kFastThreads / 64;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int d = a.d, E = a.E, E8 = E & ~7;
+    for (int e = wave; e < E; e += W) {
+        if (e != wave) load_wchunk<NC4>(a, e, R.wv);
+        double l2[2] = {0.0, 0.0}, ab2[2] = {0.0, 0.0};
+#pragma unroll
+        for (int g = 0; g < NC4; g++) {  // products are exact in float64
+            const float4 x = *reinterpret_cast<const float4 *>(R.xs + 4 * g), w = R.wv[g];
+            const double p0 = (double)x.x * (double)w.x, p1 = (double)x.y * (double)w.y;
+            const double p2 = (double)x.z * (double)w.z, p3 = (double)x.w * (double)w.w;
+            l2[g & 1] += (p0 + p1) + (p2 + p3);
+            ab2[g & 1] += (fabs(p0) + fabs(p1)) + (fabs(p2) + fabs(p3));
+        }
+        const double loc = l2[0] + l2[1];
+        double absp = ab2[0] + ab2[1];
+        double incl = loc;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const double v = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += v;
+        }
+        double run = incl - loc, sg = 0.0;
+#pragma unroll
+        for (int g = 0; g < NC4; g++) {  // group sums again, in order
+            const float4 x = *reinterpret_cast<const float4 *>(R.xs + 4 * g), w = R.wv[g];
+            sg += fabs(run);
+            run += ((double)x.x * (double)w.x + (double)x.y * (double)w.y) +
+                   ((double)x.z * (double)w.z + (double)x.w * (double)w.w);
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            sg += __shfl_xor(sg, off, 64);
+            absp += __shfl_xor(absp, off, 64);
+        }
+        const double total = __shfl(incl, 63, 64);
+        if (lane == 0) {
+            // float64 rounding of the sums above is covered, with a wide
+            // margin, by the 2^-36 * sum|p| term
+            const double u = 0x1p-24, g = 1.0 + 1.01 * (double)d * u;
+            const double sabs = 4.0 * sg + 4.0 * absp;  // >= sum_k |S_k|
+            double B = u * g * sabs + 0x1p-36 * absp + (double)d * 0x1p-149;
+            if (e >= E8) B += u * (1.0 + u) * g * absp;
+            s_a[e] = total;
+            s_b[e] = B;
+        }
+    }
+}
+
+template <int NC4>
+__device__ __forceinline__ void logits_and_activations(const RouterArgs &a, int t, float *s_x,
+                                                       double *s_a, double *s_b) {
+    LogitRegs<NC4> R;
+    load_wchunk<NC4>(a, min((int)(threadIdx.x >> 6), a.E - 1), R.wv);
+    quantise_token(a, t);  // while the router chunks load
+    R.xs = stage_xrow<NC4>(a, t, s_x);
+    logit_bounds<NC4>(a, R, s_a, s_b);
+}
+
+__global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a) {
+    __shared__ double s_a[kMaxE], s_b[kMaxE];
+    __shared__ float s_z[kMaxE], s_zlo[kMaxE], s_zhi[kMaxE], s_s[kMaxE], s_g[kMaxE];
+    __shared__ unsigned char s_ok[kMaxE];
+    __shared__ int s_sel[kMaxK], s_rank[kMaxE];
+    __shared__ int s_cw[kFastThreads / 64][kMaxE];
+    __shared__ int s_off[kMaxE + 1];
+    __shared__ int s_flag;
+    __shared__ __attribute__((aligned(16))) float s_x[64 * (64 + 4)];  // C <= 64
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int t = blockIdx.x, d = a.d, E = a.E, K = a.K;
+
+    // bias into LDS while the logits run
+    for (int e = tid; e < E; e += kFastThreads) s_g[e] = a.rp.has_bias ? a.bias[e] : 0.0f;
+
+    // 1. activations for the expert products; float64 logit and chain error
+    //    bound per expert, one wave each
+    switch (d >> 8) {
+    case 1: logits_and_activations<1>(a, t, s_x, s_a, s_b); break;
+    case 2: logits_and_activations<2>(a, t, s_x, s_a, s_b); break;
+    case 4: logits_and_activations<4>(a, t, s_x, s_a, s_b); break;
+    case 8: logits_and_activations<8>(a, t, s_x, s_a, s_b); break;
+    default: logits_and_activations<16>(a, t, s_x, s_a, s_b); break;
+    }
+    __syncthreads();
+
+    // 2. score intervals, ranks on the float64 scores (lane = expert,
+    //    E <= 64), certification
+    if (wave == 0) {
+        const int e = lane;
+        const bool valid = e < E;
+        bool ok = true;
+        if (valid) {
+            const double lo = s_a[e] - s_b[e], hi = s_a[e] + s_b[e];
+            ok = __builtin_isfinite(lo) && __builtin_isfinite(hi);
+            const float bias = s_g[e];
+            float zlo = ceil_f32(lo), zhi = floor_f32(hi), zm = (float)s_a[e];
+            if (a.rp.has_bias) {
+                zlo = zlo + bias;
+                zhi = zhi + bias;
+                zm = zm + bias;
+            }
+            s_zlo[e] = zlo;
+            s_zhi[e] = zhi;
+            s_z[e] = zm;
+        }
+        __builtin_amdgcn_wave_barrier();
+        int rank = 0;
+        if (valid) {
+            const float k = sel_key(s_z[e]);
+            for (int f = 0; f < E; f++)
+                if (f != e && better(sel_key(s_z[f]), f, k, e)) rank++;
+            s_rank[e] = rank;
+        }
+        __builtin_amdgcn_wave_barrier();
+        // a selected expert must rank certainly before every expert ranked
+        // below it (certainly: interval ends apart, or touching with the
+        // lower index first)
+        if (valid && rank < K) {
+            const float lo_e = s_zlo[e];
+            for (int f = 0; f < E; f++) {
+                if (s_rank[f] <= rank) continue;
+                const float hi_f = s_zhi[f];
+                ok = ok && (lo_e > hi_f || (lo_e == hi_f && e < f));
+            }
+        }
+        ok = __all(ok);
+        if (lane == 0) s_flag = ok;
+        if (ok && valid && rank < K) {
+            store_agent(a.topk_idx + (int64_t)t * K + rank, e);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+    }
+    __syncthreads();
+    if (!s_flag) {  // 3. fallback: exact chains, exact selection
+        for (int e = tid; e < E; e += kFastThreads) a.logits[(int64_t)t * E + e] = exact_logit(a, t, e);
+        __threadfence_block();
+        __syncthreads();
+        if (wave == 0) {
+            select_token(a, t, s_z, s_s, s_g, s_ok, s_sel);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        __syncthreads();
+    }
+
+    // 4. the last block to finish runs the dispatch (the selections were
+    //    published with coherent stores and have completed)
+    if (tid == 0) {
+        const unsigned old = atomicAdd(&a.sync[0], 1u);
+        s_flag = (old == gridDim.x - 1);
+    }
+    __syncthreads();
+    if (!s_flag) return;
+    dispatch_block<kFastThreads>(a, s_cw, s_off);
+    if (tid == 0) a.sync[0] = 0;
 }
 
 __global__ void k_debug_sigmoid(const float *__restrict__ x, int64_t n, float *__restrict__ out) {
@@ -391,7 +781,7 @@ int router_token_groups(int T, int d, int E) {
     return (T + TB - 1) / TB;
 }
 
-hipError_t launch_router(const RouterArgs &a, hipStream_t st) {
+hipError_t launch_router(const RouterArgs &a, int mode, hipStream_t st) {
     int TB, EG;
     block_shape(a.d, a.E, TB, EG);
     const int ntg = (a.T + TB - 1) / TB, neg = (a.E + EG - 1) / EG;
@@ -404,7 +794,20 @@ hipError_t launch_router(const RouterArgs &a, hipStream_t st) {
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL(k_router, dim3(ntg, neg), dim3(kThreads), lds, st, a, TB, EG);
+    hipLaunchKernelGGL(k_router, dim3(ntg, neg), dim3(kThreads), lds, st, a, TB, EG, mode);
+    return hipGetLastError();
+}
+
+// softmax kinds, at most 64 experts, d = 64 * 4 * NC4 with NC4 in
+// {1, 2, 4, 8, 16}
+bool route_fast_ok(const RouterArgs &a) {
+    const int c4 = a.d / 256;
+    return a.rp.kind != LCMOE_ROUTE_SIGMOID_GROUP && a.wlc && a.E <= 64 && a.d % 256 == 0 &&
+           (c4 == 1 || c4 == 2 || c4 == 4 || c4 == 8 || c4 == 16);
+}
+
+hipError_t launch_route_fast(const RouterArgs &a, hipStream_t st) {
+    hipLaunchKernelGGL(k_route_fast, dim3(a.T), dim3(kFastThreads), 0, st, a);
     return hipGetLastError();
 }
 

@@ -17,6 +17,7 @@ struct RouteParams {
 struct RouterArgs {
     const float *x;    // [T, d]
     const float *wrt;  // router transposed on the device: [E, d]
+    const float *wlc;  // the same in the fast router's lane-chunk order, or null
     const float *bias; // [E] or null
     int T, d, E, K;
     RouteParams rp;
@@ -25,10 +26,17 @@ struct RouterArgs {
     float *topk_w;        // [T, K]
     int8_t *xh, *xl;      // [T, d] limbs, or null
     float *xs, *xm;       // [T, d/32] scale and quantised-sum
+    _Float16 *x16, *x16s; // f16 hi/lo pieces and sums for the matrix-core path, or null
     int32_t *counts, *offsets, *perm, *inv, *touched;
     uint32_t *sync;       // [n_token_groups + 1] zero-initialised counters
 };
-hipError_t launch_router(const RouterArgs &a, hipStream_t st);
+// mode 0: the exact router (logits, limbs, top-k, dispatch); mode 1: exact
+// logits and the weights of the selection already in topk_idx.
+hipError_t launch_router(const RouterArgs &a, int mode, hipStream_t st);
+// Certified fast router for the softmax kinds: selection, dispatch, limbs
+// and f16 pieces; weights come from launch_router mode 1.
+bool route_fast_ok(const RouterArgs &a);
+hipError_t launch_route_fast(const RouterArgs &a, hipStream_t st);
 int router_token_groups(int T, int d, int E);
 
 struct SlotArgsHost {
@@ -69,10 +77,21 @@ hipError_t launch_mfma_down(const uint8_t *down, int64_t estride, const _Float16
                             const _Float16 *hs, const SlotArgsHost &sa, int slots, int d, int F,
                             int ksplit, float *Y, int64_t split_stride, hipStream_t st);
 
+// Routing weights computed by the combine from exact logits (fast-router
+// path); logits == null: the weights are already in topk_w.
+struct CombineRoute {
+    const float *logits;     // [T, E] exact router logits, or null
+    const int32_t *topk_idx; // [T, K]
+    const float *bias;       // [E] or null
+    int kind, E;
+    float scale;
+};
+
 // y[t] = sum_k w[t,k] * sum_s Yr[s][inv[t,k]] + sum_j sum_s Ys[s][j*T + t].
+// With cr.logits, w[t,k] is computed here (and stored to topk_w).
 hipError_t launch_combine(const float *Yr, int ks_r, int64_t stride_r, const float *Ys, int ks_s,
-                          int64_t stride_s, const int32_t *inv, const float *topk_w, int T, int K,
-                          int S, int d, float *y, hipStream_t st);
+                          int64_t stride_s, const int32_t *inv, float *topk_w, int T, int K,
+                          int S, int d, const CombineRoute &cr, float *y, hipStream_t st);
 
 hipError_t launch_debug_dequant(int qt, const uint8_t *src, int64_t count, float *out,
                                 hipStream_t st);

@@ -29,9 +29,9 @@ using namespace lcmoe;
 namespace {
 
 enum Slot { kSlotRouter, kSlotPrep, kSlotGateUp, kSlotGateUpSh, kSlotDown, kSlotDownSh,
-            kSlotCombine, kNumSlots };
+            kSlotCombine, kSlotRouterExact, kNumSlots };
 const char *kSlotNames[kNumSlots] = {"router", "act16", "gateup", "gateup_shared", "down",
-                                     "down_shared", "combine"};
+                                     "down_shared", "combine", "router_exact"};
 constexpr int kMaxKSplit = 4;
 // matrix-core path when an expert family averages at least this many tokens
 constexpr int kMfmaMinTokens = 6;
@@ -59,8 +59,17 @@ struct lcmoe_handle {
     lcmoe_desc desc{};
     int device = 0;
     hipStream_t stream = nullptr;
+    // side stream for the exact router chains (routing weights) that run
+    // beside the expert products when the fast router certified the selection
+    hipStream_t side = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+    uint32_t *sync_side = nullptr;
     std::vector<void *> allocs;
     float *wrt = nullptr, *bias = nullptr;
+    // router in the fast router's lane-chunk order (null when d is not
+    // 64 * a power-of-two multiple of 4): element (e, lane*C + 4i + j) at
+    // ((e * C/4 + i) * 64 + lane) * 4 + j, C = d / 64
+    float *wlc = nullptr;
     ExpertSet routed, shared;
     float *x_dev = nullptr, *y_dev = nullptr, *logits = nullptr;
     int8_t *xh = nullptr, *xl = nullptr;
@@ -137,12 +146,16 @@ lcmoe_status upload_stack(lcmoe_handle *h, uint8_t **dst, const uint8_t *src, in
 void free_handle(lcmoe_handle *h) {
     if (!h) return;
     if (h->stream) (void)hipStreamSynchronize(h->stream);
+    if (h->side) (void)hipStreamSynchronize(h->side);
     for (auto &p : h->pending) {
         (void)hipEventDestroy(p.a);
         (void)hipEventDestroy(p.b);
     }
     for (auto ev : h->event_pool) (void)hipEventDestroy(ev);
     for (void *p : h->allocs) (void)hipFree(p);
+    if (h->ev_fork) (void)hipEventDestroy(h->ev_fork);
+    if (h->ev_join) (void)hipEventDestroy(h->ev_join);
+    if (h->side) (void)hipStreamDestroy(h->side);
     if (h->stream) (void)hipStreamDestroy(h->stream);
     delete h;
 }
@@ -248,8 +261,12 @@ extern "C" lcmoe_status lcmoe_create(const lcmoe_desc *desc, const lcmoe_weights
         return s;
     };
     if (hipGetDevice(&h->device) != hipSuccess) return bail(fail(LCMOE_ERR_HIP, "hipGetDevice failed"));
-    if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess)
+    if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&h->side, hipStreamNonBlocking) != hipSuccess)
         return bail(fail(LCMOE_ERR_HIP, "hipStreamCreate failed"));
+    if (hipEventCreateWithFlags(&h->ev_fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&h->ev_join, hipEventDisableTiming) != hipSuccess)
+        return bail(fail(LCMOE_ERR_HIP, "hipEventCreate failed"));
 
     const int64_t d = D.d_model, E = D.n_expert, K = D.n_expert_used, S = D.n_shared,
                   Tm = D.max_tokens, A = Tm * K;
@@ -261,6 +278,18 @@ extern "C" lcmoe_status lcmoe_create(const lcmoe_desc *desc, const lcmoe_weights
         if ((st = alloc_n(h, &h->wrt, wt.size()))) return bail(st);
         if (hipMemcpy(h->wrt, wt.data(), wt.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
             return bail(fail(LCMOE_ERR_HIP, "router upload failed"));
+        if (d % 256 == 0) {
+            const int64_t C = d / 64, nc4 = C / 4;
+            std::vector<float> wl((size_t)E * d);
+            for (int64_t e = 0; e < E; e++)
+                for (int64_t l = 0; l < 64; l++)
+                    for (int64_t i = 0; i < nc4; i++)
+                        for (int64_t j = 0; j < 4; j++)
+                            wl[(((e * nc4 + i) * 64 + l) * 4) + j] = wt[e * d + l * C + 4 * i + j];
+            if ((st = alloc_n(h, &h->wlc, wl.size()))) return bail(st);
+            if (hipMemcpy(h->wlc, wl.data(), wl.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+                return bail(fail(LCMOE_ERR_HIP, "router upload failed"));
+        }
     }
     if (D.has_bias) {
         if ((st = alloc_n(h, &h->bias, E))) return bail(st);
@@ -294,7 +323,9 @@ extern "C" lcmoe_status lcmoe_create(const lcmoe_desc *desc, const lcmoe_weights
     if ((st = alloc_n(h, &h->touched, E + 1))) return bail(st);
     const int nsync = router_token_groups((int)Tm, (int)d, (int)E) + 1;
     if ((st = alloc_n(h, &h->sync, nsync))) return bail(st);
-    if (hipMemset(h->sync, 0, sizeof(uint32_t) * nsync) != hipSuccess)
+    if ((st = alloc_n(h, &h->sync_side, nsync))) return bail(st);
+    if (hipMemset(h->sync, 0, sizeof(uint32_t) * nsync) != hipSuccess ||
+        hipMemset(h->sync_side, 0, sizeof(uint32_t) * nsync) != hipSuccess)
         return bail(fail(LCMOE_ERR_HIP, "workspace clear failed"));
     *out = h;
     return LCMOE_OK;
@@ -351,9 +382,15 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
                                     hipStream_t st) {
     const lcmoe_desc &D = h->desc;
     const int d = D.d_model, E = D.n_expert, K = D.n_expert_used, S = D.n_shared;
+    const Plan pr = plan_set(h, h->routed, false, T);
+    const Plan ps = S > 0 ? plan_set(h, h->shared, true, T) : Plan{false, 0, 1};
+    const bool mfma = pr.mfma || ps.mfma;
+    // int8 limbs only feed the row-per-lane kernels
+    const bool limbs = (h->routed.rpl_gu && !pr.mfma) || (S > 0 && h->shared.rpl_gu && !ps.mfma);
     RouterArgs ra{};
     ra.x = x;
     ra.wrt = h->wrt;
+    ra.wlc = h->wlc;
     ra.bias = h->bias;
     ra.T = T;
     ra.d = d;
@@ -363,30 +400,51 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
     ra.logits = h->logits;
     ra.topk_idx = h->topk_idx;
     ra.topk_w = h->topk_w;
-    ra.xh = h->xh;
+    ra.xh = limbs ? h->xh : nullptr;
     ra.xl = h->xl;
     ra.xs = h->xs;
     ra.xm = h->xm;
+    ra.x16 = nullptr;
+    ra.x16s = h->x16s;
     ra.counts = h->counts;
     ra.offsets = h->offsets;
     ra.perm = h->perm;
     ra.inv = h->inv;
     ra.touched = h->touched;
     ra.sync = h->sync;
-    HIP_TRY(timed(h, st, kSlotRouter, [&] { return launch_router(ra, st); }));
-    const Plan pr = plan_set(h, h->routed, false, T);
-    const Plan ps = S > 0 ? plan_set(h, h->shared, true, T) : Plan{false, 0, 1};
-    if (pr.mfma || ps.mfma)
-        HIP_TRY(timed(h, st, kSlotPrep, [&] {
-            return launch_act16(x, T, d, h->x16, h->x16s, st);
-        }));
+    const bool fast = route_fast_ok(ra);
+    if (fast) {
+        // the exact chains (for the routing weights only) start on the side
+        // stream at once; selection, dispatch and activations come from the
+        // certified fast router; the combine turns the chains into weights
+        HIP_TRY(hipEventRecord(h->ev_fork, st));
+        HIP_TRY(hipStreamWaitEvent(h->side, h->ev_fork, 0));
+        RouterArgs rb = ra;
+        rb.xh = nullptr;
+        rb.sync = h->sync_side;
+        HIP_TRY(timed(h, h->side, kSlotRouterExact, [&] { return launch_router(rb, 2, h->side); }));
+        HIP_TRY(hipEventRecord(h->ev_join, h->side));
+        ra.x16 = mfma ? h->x16 : nullptr;
+        HIP_TRY(timed(h, st, kSlotRouter, [&] { return launch_route_fast(ra, st); }));
+    } else {
+        HIP_TRY(timed(h, st, kSlotRouter, [&] { return launch_router(ra, 0, st); }));
+        if (mfma)
+            HIP_TRY(timed(h, st, kSlotPrep, [&] {
+                return launch_act16(x, T, d, h->x16, h->x16s, st);
+            }));
+    }
     lcmoe_status s;
     if ((s = run_set(h, h->routed, false, x, T, pr, st))) return s;
     if (S > 0 && (s = run_set(h, h->shared, true, x, T, ps, st))) return s;
+    if (fast) HIP_TRY(hipStreamWaitEvent(st, h->ev_join, 0));
     const int ks_r = pr.ks, ks_s = ps.ks;
+    CombineRoute cr{};
+    if (fast)
+        cr = CombineRoute{h->logits, h->topk_idx, D.has_bias ? h->bias : nullptr, D.route_kind,
+                          E, D.routed_scale};
     HIP_TRY(timed(h, st, kSlotCombine, [&] {
         return launch_combine(h->routed.Y, ks_r, h->routed.positions * d, h->shared.Y, ks_s,
-                              h->shared.positions * d, h->inv, h->topk_w, T, K, S, d, y, st);
+                              h->shared.positions * d, h->inv, h->topk_w, T, K, S, d, cr, y, st);
     }));
     h->last_T = T;
     h->last_stream = st;
