@@ -65,6 +65,20 @@ def cpu_baseline(cfg, layer, x, budget_s=15.0):
     }
 
 
+def copy_probe(mib: int):
+    """Three plain device-to-device copies of `mib` MiB: a known byte count to
+    scale rocprofv3's FETCH_SIZE / WRITE_SIZE counters by."""
+    from leafcutterllm_amd import hip
+    n = mib << 20
+    a, b = hip.DeviceBuffer(n), hip.DeviceBuffer(n)
+    rt = hip.rt()
+    rt.hipMemset(a.ptr, 1, n)
+    for _ in range(3):
+        rt.hipMemcpy(b.ptr, a.ptr, n, 3)  # hipMemcpyDeviceToDevice
+    rt.hipDeviceSynchronize()
+    print(json.dumps({"copy_probe_bytes": n, "copies": 3}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -75,8 +89,14 @@ def main():
     ap.add_argument("--sweep", default="1,8,64")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-events", type=int, default=1,
-                    help="record HIP events around each kernel inside the timed region")
+                    help="time each kernel with HIP events in a second timed region")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run device-to-device copies of this size (FETCH_SIZE calibration)")
     args = ap.parse_args()
+
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
 
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
@@ -123,27 +143,37 @@ def main():
             r = i % R
             moes[r].forward_dev(xbufs[(r, T)].ptr, T, ybufs[r].ptr, stream.ptr)
         stream.synchronize()
-        for m in moes:
-            m.set_timing(bool(args.kernel_events))
-            m.get_timing()  # reset
-        ev0, ev1 = hip.Event(), hip.Event()
-        stream.synchronize()
-        ev0.record(stream)
-        for i in range(args.steps):
-            r = i % R
-            moes[r].forward_dev(xbufs[(r, T)].ptr, T, ybufs[r].ptr, stream.ptr)
-        ev1.record(stream)
-        stream.synchronize()
-        ms = ev0.elapsed_ms(ev1) / args.steps
-        kern = {}
-        for m in moes:
-            for name, (kms, n) in m.get_timing().items():
-                a, b = kern.get(name, (0.0, 0))
-                kern[name] = (a + kms, b + n)
-            m.set_timing(False)
+
+        def timed_region(events: bool):
+            """K steps bracketed by HIP events on the launch stream; with
+            `events`, every launch is also bracketed (per-kernel times)."""
+            for m in moes:
+                m.set_timing(events)
+                m.get_timing()  # reset
+            ev0, ev1 = hip.Event(), hip.Event()
+            stream.synchronize()
+            ev0.record(stream)
+            for i in range(args.steps):
+                r = i % R
+                moes[r].forward_dev(xbufs[(r, T)].ptr, T, ybufs[r].ptr, stream.ptr)
+            ev1.record(stream)
+            stream.synchronize()
+            kern = {}
+            for m in moes:
+                for name, (kms, n) in m.get_timing().items():
+                    a, b = kern.get(name, (0.0, 0))
+                    kern[name] = (a + kms, b + n)
+                m.set_timing(False)
+            return ev0.elapsed_ms(ev1) / args.steps, kern
+
+        # the step time comes from a region without per-launch events (they
+        # add host and queue overhead); a second region times each kernel
+        ms, _ = timed_region(False)
+        kern = timed_region(True)[1] if args.kernel_events else {}
         bytes_per_step = sum(call_bytes[i % R] for i in range(args.steps)) / args.steps
         gu_per_launch = sum(gu_bytes[i % R] for i in range(args.steps)) / args.steps
-        gu_ms = kern["gateup"][0] / kern["gateup"][1] if kern["gateup"][1] else float("nan")
+        gu = kern.get("gateup", (0.0, 0))
+        gu_ms = gu[0] / gu[1] if gu[1] else float("nan")
         per_batch[T] = {
             "tokens_per_s": T / (ms * 1e-3),
             "ms_per_step": ms,
@@ -178,7 +208,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_gateup (fused Q4_K dequant-dot gate+up + SwiGLU)",
+            "kernel": "gate/up launch (fused Q4_K dequant + gate/up products + SwiGLU)",
             "achieved": round(head["gateup_GBps"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

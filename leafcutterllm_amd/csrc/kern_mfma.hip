@@ -35,6 +35,26 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float16v __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // native vectors: copies of HIP's
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));  // uint4 struct become memcpy
+
+// Global-memory bytes: an explicit address space keeps loads through
+// pointers rebuilt from integers as global (not flat) loads.
+typedef __attribute__((address_space(1))) const uint8_t g_u8;
+
+template <class T>
+__device__ __forceinline__ T gload(g_u8 *p) {
+    return *reinterpret_cast<const __attribute__((address_space(1))) T *>(p);
+}
+
+// p as a wave-uniform (scalar register) global pointer; p must be the same in
+// all lanes
+__device__ __forceinline__ g_u8 *uniform(const void *p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<g_u8 *>(((uint64_t)hi << 32) | lo);
+}
 
 constexpr int kWaves = 4;  // waves per block = 4 groups of 32 rows
 constexpr int kTok = 32;   // tokens per pass
@@ -50,6 +70,17 @@ __device__ __forceinline__ float16v mfma32(const half8 &a, const half8 &b, const
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// 16-token passes use v_mfma_f32_16x16x32_f16 on two 16-row tiles per wave:
+// lane l (r16 = l % 16, c4 = l / 16) holds A: token r16, columns 8*c4..+8 of
+// a 32-column sub-block; B: row r16 of the tile, the same columns; C: row
+// r16, tokens 4*c4 + i.
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4v mfma16(const half8 &a, const half8 &b, const float4v &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
 // bytes (b_i, b_j) of w -> f16 pair (1024 + b_i, 1024 + b_j); the bytes must
 // already be nibbles
 __device__ __forceinline__ half2v magic2(uint32_t w, uint32_t sel) {
@@ -62,7 +93,7 @@ constexpr uint32_t kSel11 = 0x04010401u;
 constexpr uint32_t kSel22 = 0x04020402u;
 constexpr uint32_t kSel33 = 0x04030403u;
 
-// 8 nibbles (one per byte of w0, w1, already masked) -> 8 f16 values sc*q,
+// 8 masked bytes b (one per byte of w0, w1) -> 8 f16 values (1024 + b) * sc2 + c2,
 // natural column order
 __device__ __forceinline__ half8 dec8(uint32_t w0, uint32_t w1, half2v sc2, half2v c2) {
     const half2v p0 = __builtin_elementwise_fma(magic2(w0, kSel01), sc2, c2);
@@ -83,7 +114,7 @@ struct Hdr {
 
 // get_scale_min_k4 (rust/src/kernels/mod.rs:54-63) for all 8 sub-blocks,
 // one byte per sub-block
-__device__ __forceinline__ Hdr unpack_hdr16(uint4 h) {
+__device__ __forceinline__ Hdr unpack_hdr16(u32x4 h) {
     Hdr s;
     s.sc03 = h.y & 0x3F3F3F3Fu;
     s.m03 = h.z & 0x3F3F3F3Fu;
@@ -94,16 +125,27 @@ __device__ __forceinline__ Hdr unpack_hdr16(uint4 h) {
     return s;
 }
 
-// (sc, sc) and (-1024 sc, -1024 sc) for the two sub-blocks of pair p
-__device__ __forceinline__ void pair_scales(const Hdr &s, int p, half2v &sa, half2v &ca,
-                                            half2v &sb, half2v &cb) {
+// Scales of pair p: s2 = (sc_2p, sc_2p+1 / 16) and c2 = -1024 * s2.  The
+// low-nibble sub-block 2p decodes as (1024 + q) * sc_2p - 1024 * sc_2p; the
+// high-nibble sub-block 2p+1 is decoded unshifted, from the byte 16q, as
+// (1024 + 16q) * (sc / 16) - 64 * sc.  Every step is exact in f16 (the fmas
+// round only their final, integer results <= 945).
+__device__ __forceinline__ void pair_scales(const Hdr &s, int p, half2v &s2, half2v &c2) {
     const uint32_t w = p < 2 ? s.sc03 : s.sc47;
-    const half2v k1024 = half2v{(_Float16)1024.0f, (_Float16)1024.0f};
-    const half2v km = half2v{(_Float16)-1024.0f, (_Float16)-1024.0f};
-    sa = magic2(w, (p & 1) ? kSel22 : kSel00) - k1024;
-    sb = magic2(w, (p & 1) ? kSel33 : kSel11) - k1024;
-    ca = sa * km;
-    cb = sb * km;
+    const half2v mag = magic2(w, (p & 1) ? kSel23 : kSel01);  // 1024 + sc
+    s2 = __builtin_elementwise_fma(mag, half2v{(_Float16)1.0f, (_Float16)0.0625f},
+                                   half2v{(_Float16)-1024.0f, (_Float16)-64.0f});
+    c2 = s2 * half2v{(_Float16)-1024.0f, (_Float16)-1024.0f};
+}
+
+// B operands (sc*q, 8 columns each) of pair p's two sub-blocks from one
+// lane's 8 qs bytes w0, w1
+__device__ __forceinline__ void dec_pair(const Hdr &s, int p, uint32_t w0, uint32_t w1,
+                                         half8 &blo, half8 &bhi) {
+    half2v s2, c2;
+    pair_scales(s, p, s2, c2);
+    blo = dec8(w0 & 0x0F0F0F0Fu, w1 & 0x0F0F0F0Fu, half2v{s2[0], s2[0]}, half2v{c2[0], c2[0]});
+    bhi = dec8(w0 & 0xF0F0F0F0u, w1 & 0xF0F0F0F0u, half2v{s2[1], s2[1]}, half2v{c2[1], c2[1]});
 }
 
 // B operand of the min MFMA: (m_j, m_j) for sub-blocks j = 4h .. 4h+3
@@ -125,11 +167,48 @@ __device__ __forceinline__ half8 min_operand(const Hdr &s, int h) {
 // LDS stage of one super-block for the pass's 32 tokens: token rows of 1040
 // bytes (the 1 KiB piece + 16 bytes of pad: b128 reads by 8 consecutive
 // tokens hit distinct banks), then the 32 tokens' sums (32 bytes each).
-// Two stages live in two distinct arrays so that the compiler can tell the
-// DMA into one from the reads of the other.
 constexpr int kTokBytes = 1040;
 constexpr int kSumsOff = kTok * kTokBytes;
 constexpr int kStageBytes = kSumsOff + kTok * 32;
+
+// Per-pass source addresses of the block's activation staging: wave w moves
+// the 1 KiB pieces of tokens w + 4i (i = 0..7); wave 0 also moves the 32
+// sums pieces (lane l: token l/2, half l%2).
+struct StageSrc {
+    g_u8 *tok[8];   // token row bases (wave-uniform)
+    g_u8 *sums;     // sums array base (wave-uniform)
+    uint32_t soff;  // this lane's byte offset of its sums row
+};
+
+// One super-block of activations on its way to LDS through this wave's
+// registers: loaded at the start of a step, stored to the other LDS stage at
+// its end.  Ordinary loads (not LDS DMA), so that every wait in the pipeline
+// is an in-order vmcnt wait that leaves younger weight loads in flight.
+template <int NI>
+struct StageRegs {
+    u32x4 tok[NI];
+    u32x4 sums;
+};
+
+template <int NI>
+__device__ __forceinline__ void stage_load(StageRegs<NI> &s, const StageSrc &src, int kb,
+                                           int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < NI; i++)
+        s.tok[i] = gload<u32x4>(src.tok[i] + (uint32_t)(kb * 1024 + 16 * lane));
+    // every wave loads and stores the same sums (identical bytes), which
+    // keeps the staging free of branches
+    s.sums = gload<u32x4>(src.sums + (src.soff + (uint32_t)kb * 32));
+}
+
+template <int NI>
+__device__ __forceinline__ void stage_store(uint8_t *stage, const StageRegs<NI> &s, int wave,
+                                            int lane) {
+#pragma unroll
+    for (int i = 0; i < NI; i++)
+        *reinterpret_cast<u32x4 *>(stage + (wave + 4 * i) * kTokBytes + 16 * lane) = s.tok[i];
+    *reinterpret_cast<u32x4 *>(stage + kSumsOff + 16 * lane) = s.sums;
+}
 
 __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -137,42 +216,36 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
-// Per-pass source addresses for the block's staging DMA: wave w moves the
-// 1 KiB pieces of tokens w + 4i (i = 0..7); wave 0 also moves the 32 sums
-// pieces (lane l: token l/2, half l%2).
-struct StageSrc {
-    const uint8_t *tok[8];  // token row bases (wave-uniform)
-    const uint8_t *sums;    // this lane's sums row base
-};
-
-// DMA super-block kb of the pass's activations into stage (1 KiB per token
-// per wave instruction, lane l -> bytes 16l..16l+15)
-__device__ __forceinline__ void stage_dma(uint8_t *stage, const StageSrc &src, int kb, int wave,
-                                          int lane) {
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-        __builtin_amdgcn_global_load_lds(src.tok[i] + (int64_t)kb * 1024 + 16 * lane,
-                                         (lds_void *)(stage + (wave + 4 * i) * kTokBytes), 16, 0, 0);
-    if (wave == 0)
-        __builtin_amdgcn_global_load_lds(src.sums + (int64_t)kb * 32 + 16 * (lane & 1),
-                                         (lds_void *)(stage + kSumsOff), 16, 0, 0);
+// B operand of the 16x16x16 min MFMA: (m_j, m_j) for sub-blocks 2*c4, 2*c4+1
+__device__ __forceinline__ half4 min_operand16(const Hdr &s, int c4) {
+    const uint32_t w = c4 < 2 ? s.m03 : s.m47;
+    const half2v k1024 = half2v{(_Float16)1024.0f, (_Float16)1024.0f};
+    const half2v a = magic2(w, (c4 & 1) ? kSel22 : kSel00) - k1024;
+    const half2v b = magic2(w, (c4 & 1) ? kSel33 : kSel11) - k1024;
+    return half4{a[0], a[1], b[0], b[1]};
 }
 
 // Raw weight registers of one super-block for one matrix: this lane's row
 // header and, per unit u = 2p + s, 8 bytes of chunk 1 + u.
 struct WRaw {
-    uint4 hdr;
-    uint2 q[8];
+    u32x4 hdr;
+    u32x2 q[8];
 };
 
-__device__ __forceinline__ void load_w(WRaw &w, const uint8_t *row, int kb, int h) {
-    const uint8_t *b = row + (int64_t)kb * 9 * 1024;
-    w.hdr = *reinterpret_cast<const uint4 *>(b);
+// Weight addressing: a wave-uniform base (the wave's row group, chunk 0 of
+// super-block 0) plus this lane's 32-bit row offset `lo`.
+__device__ __forceinline__ u32x4 load_hdr(g_u8 *base, uint32_t lo, int kb, int off = 0) {
+    return gload<u32x4>(base + (lo + (uint32_t)(kb * 9 * 1024 + off)));
+}
+
+__device__ __forceinline__ u32x2 load_q(g_u8 *base, uint32_t lo, int kb, int chunk, int off) {
+    return gload<u32x2>(base + (lo + (uint32_t)(kb * 9 * 1024 + chunk * 1024 + off)));
+}
+
+__device__ __forceinline__ void load_w(WRaw &w, g_u8 *base, uint32_t lo, int kb, int h) {
+    w.hdr = load_hdr(base, lo, kb);
 #pragma unroll
-    for (int u = 0; u < 8; u++)
-        w.q[u] = *reinterpret_cast<const uint2 *>(b + (1 + u) * 1024 + 8 * h);
+    for (int u = 0; u < 8; u++) w.q[u] = load_q(base, lo, kb, 1 + u, 8 * h);
 }
 
 // Activation operands of one (pair p, k-step s) unit from the LDS stage:
@@ -197,11 +270,8 @@ __device__ __forceinline__ void unit_mfma(const WRaw (&w)[MATS], const Hdr (&hd)
     const int p = u >> 1;
 #pragma unroll
     for (int m = 0; m < MATS; m++) {
-        half2v sa, ca, sb, cb;
-        pair_scales(hd[m], p, sa, ca, sb, cb);
-        const uint32_t w0 = w[m].q[u].x, w1 = w[m].q[u].y;
-        const half8 blo = dec8(w0 & 0x0F0F0F0Fu, w1 & 0x0F0F0F0Fu, sa, ca);
-        const half8 bhi = dec8((w0 >> 4) & 0x0F0F0F0Fu, (w1 >> 4) & 0x0F0F0F0Fu, sb, cb);
+        half8 blo, bhi;
+        dec_pair(hd[m], p, w[m].q[u].x, w[m].q[u].y, blo, bhi);
         S[m] = mfma32(a.h0, blo, S[m]);
         S[m] = mfma32(a.l0, blo, S[m]);
         S[m] = mfma32(a.h1, bhi, S[m]);
@@ -220,29 +290,34 @@ __device__ __forceinline__ void finish_sb(const Hdr &hd, const half8 &amin, int 
     }
 }
 
-// One super-block step: start the DMA of super-block kn into `nxt` and the
-// loads of its weights into wn, compute kb from `cur` and wc, then wait for
-// everything at the barrier.
+// Pipeline of a pass over super-blocks [kb0, kb1).  One register set of
+// weights: step k computes super-block k from it and from LDS stage k % 2,
+// and reloads each weight register with super-block k+1 right after its
+// decode has read it, so every weight load has about one step to arrive and
+// the loads stream steadily instead of in a burst per step.  The step also
+// loads super-block k+1's activations at its start and stores them to the
+// other stage at its end.  Only ordinary vector loads are used; they
+// complete in issue order, so each wait the compiler places (for the
+// activations before their store, for a weight register at its next use)
+// leaves the younger loads in flight, and no wait drains the queue at the
+// barrier.  Indices past the end are clamped to kb1 - 1 (in bounds, unused).
+
+// One step of a 32-token pass: super-block k from `cur` and w; activations
+// of super-block kn into `nxt`; w reloaded with super-block kn.
 template <int MATS>
-__device__ __forceinline__ void step(const uint8_t *const (&wr)[MATS], int kb, int kn,
+__device__ __forceinline__ void step(g_u8 *const (&wb)[MATS], uint32_t lo, int kn,
                                      const uint8_t *cur, uint8_t *nxt, const StageSrc &src,
-                                     WRaw (&wc)[MATS], WRaw (&wn)[MATS], float16v (&acc)[MATS],
-                                     int wave, int lane) {
+                                     WRaw (&w)[MATS], float16v (&acc)[MATS], int wave, int lane) {
     const int r = lane & 31, h = lane >> 5;
-    // Wait for this step's weights (loaded one step ago) before issuing the
-    // next step's loads, so that the wait cannot cover the new loads.
-#pragma unroll
-    for (int m = 0; m < MATS; m++) {
-        asm volatile("" ::"v"(wc[m].hdr.x), "v"(wc[m].hdr.y), "v"(wc[m].hdr.z), "v"(wc[m].hdr.w));
-#pragma unroll
-        for (int u = 0; u < 8; u++) asm volatile("" ::"v"(wc[m].q[u].x), "v"(wc[m].q[u].y));
-    }
-    stage_dma(nxt, src, kn, wave, lane);
-#pragma unroll
-    for (int m = 0; m < MATS; m++) load_w(wn[m], wr[m], kn, h);
+    StageRegs<8> act;
+    stage_load(act, src, kn, wave, lane);
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads first
     Hdr hd[MATS];
 #pragma unroll
-    for (int m = 0; m < MATS; m++) hd[m] = unpack_hdr16(wc[m].hdr);
+    for (int m = 0; m < MATS; m++) {
+        hd[m] = unpack_hdr16(w[m].hdr);
+        w[m].hdr = load_hdr(wb[m], lo, kn);
+    }
     float16v S[MATS];
 #pragma unroll
     for (int m = 0; m < MATS; m++) S[m] = float16v{};
@@ -251,11 +326,15 @@ __device__ __forceinline__ void step(const uint8_t *const (&wr)[MATS], int kb, i
     for (int u = 0; u < 8; u++) {
         AUnit a;
         read_a(a, tokrow, u, h);
-        unit_mfma<MATS>(wc, hd, u, a, S);
+        unit_mfma<MATS>(w, hd, u, a, S);
+#pragma unroll
+        for (int m = 0; m < MATS; m++) w[m].q[u] = load_q(wb[m], lo, kn, 1 + u, 8 * h);
+        __builtin_amdgcn_sched_barrier(0);  // bounds the live operands to one unit
     }
     const half8 amin = *reinterpret_cast<const half8 *>(cur + kSumsOff + r * 32 + 16 * h);
 #pragma unroll
     for (int m = 0; m < MATS; m++) finish_sb(hd[m], amin, h, S[m], acc[m]);
+    stage_store(nxt, act, wave, lane);
     lds_barrier();
 }
 
@@ -263,28 +342,139 @@ __shared__ __attribute__((aligned(1024))) uint8_t s_stage0[kStageBytes];
 __shared__ __attribute__((aligned(1024))) uint8_t s_stage1[kStageBytes];
 
 // One pass of the block over super-blocks [kb0, kb1) for its 32 tokens.
-// wr[m]: this lane's row of chunk 0, super-block 0 of matrix m.  Double
-// buffered: the DMA of the next super-block's activations and the loads of
-// its weights are in flight while the current one is computed.  The last
-// step re-fetches its own super-block (in bounds, unused) so that every
-// step has the same shape.
+// wb[m]: the wave's row group of matrix m (uniform); lo: this lane's row offset.
 template <int MATS>
-__device__ __forceinline__ void block_pass(const uint8_t *const (&wr)[MATS], int kb0, int kb1,
-                                           const StageSrc &src, float16v (&acc)[MATS]) {
+__device__ __forceinline__ void block_pass(g_u8 *const (&wb)[MATS], uint32_t lo, int kb0,
+                                           int kb1, const StageSrc &src, float16v (&acc)[MATS]) {
     const int lane = threadIdx.x & 63, h = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    WRaw w0[MATS], w1[MATS];
-    stage_dma(s_stage0, src, kb0, wave, lane);
+    const int last = kb1 - 1;
+    WRaw w[MATS];
+    StageRegs<8> act;
+    stage_load(act, src, kb0, wave, lane);
 #pragma unroll
-    for (int m = 0; m < MATS; m++) load_w(w0[m], wr[m], kb0, h);
+    for (int m = 0; m < MATS; m++) load_w(w[m], wb[m], lo, kb0, h);
+    stage_store(s_stage0, act, wave, lane);
     lds_barrier();
     int kb = kb0;
     for (; kb + 2 <= kb1; kb += 2) {
-        step<MATS>(wr, kb, kb + 1, s_stage0, s_stage1, src, w0, w1, acc, wave, lane);
-        step<MATS>(wr, kb + 1, min(kb + 2, kb1 - 1), s_stage1, s_stage0, src, w1, w0, acc, wave,
-                   lane);
+        step<MATS>(wb, lo, kb + 1, s_stage0, s_stage1, src, w, acc, wave, lane);
+        step<MATS>(wb, lo, min(kb + 2, last), s_stage1, s_stage0, src, w, acc, wave, lane);
     }
-    if (kb < kb1) step<MATS>(wr, kb, kb, s_stage0, s_stage1, src, w0, w1, acc, wave, lane);
+    if (kb < kb1) step<MATS>(wb, lo, kb, s_stage0, s_stage1, src, w, acc, wave, lane);
+}
+
+// ---- 16-token passes -------------------------------------------------------
+// The wave's 32 rows are two 16-row tiles t = 0, 1.  Lane l (r16 = l % 16,
+// c4 = l / 16) loads, for tile t, row 16t + r16's header and the 8 qs bytes
+// 32p + 8*c4 .. +7 of each pair p: chunk 1 + 2p + c4/2, byte 8*(c4 % 2).
+struct WRaw16 {
+    u32x4 hdr[2];
+    u32x2 q[4][2];  // [pair][tile]
+};
+
+// lo: offset of this lane's row r16 of tile 0; tile 1 is the 16 rows after
+// it, 256 bytes further in every chunk
+__device__ __forceinline__ u32x2 load_q16(g_u8 *base, uint32_t lo, int kb, int p, int t, int c4) {
+    return load_q(base, lo, kb, 1 + 2 * p + (c4 >> 1), 256 * t + 8 * (c4 & 1));
+}
+
+__device__ __forceinline__ void load_w16(WRaw16 &w, g_u8 *base, uint32_t lo, int kb, int c4) {
+#pragma unroll
+    for (int t = 0; t < 2; t++) w.hdr[t] = load_hdr(base, lo, kb, 256 * t);
+#pragma unroll
+    for (int p = 0; p < 4; p++)
+#pragma unroll
+        for (int t = 0; t < 2; t++) w.q[p][t] = load_q16(base, lo, kb, p, t, c4);
+}
+
+__device__ __forceinline__ void finish16(const Hdr &hd, const half4 &amin, int c4,
+                                         const float4v &S, float4v &acc) {
+    const float4v Smin =
+        __builtin_amdgcn_mfma_f32_16x16x16f16(amin, min_operand16(hd, c4), float4v{}, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        acc[i] = __builtin_fmaf(hd.d, S[i], acc[i]);
+        acc[i] = __builtin_fmaf(-hd.dmin, Smin[i], acc[i]);
+    }
+}
+
+// One step of a 16-token pass (same pipeline as step()).  Per pair p the
+// activations of sub-blocks 2p and 2p+1 (hi, lo) are read once and shared by
+// both tiles and all matrices.
+template <int MATS>
+__device__ __forceinline__ void step16(g_u8 *const (&wb)[MATS], uint32_t lo, int kn,
+                                       const uint8_t *cur, uint8_t *nxt, const StageSrc &src,
+                                       WRaw16 (&w)[MATS], float4v (&acc)[MATS][2], int wave,
+                                       int lane) {
+    const int r16 = lane & 15, c4 = lane >> 4;
+    StageRegs<4> act;
+    stage_load(act, src, kn, wave, lane);
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads first
+    Hdr hd[MATS][2];
+#pragma unroll
+    for (int m = 0; m < MATS; m++)
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            hd[m][t] = unpack_hdr16(w[m].hdr[t]);
+            w[m].hdr[t] = load_hdr(wb[m], lo, kn, 256 * t);
+        }
+    float4v S[MATS][2];
+#pragma unroll
+    for (int m = 0; m < MATS; m++) S[m][0] = S[m][1] = float4v{};
+    const uint8_t *tokrow = cur + r16 * kTokBytes;
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const int col = 2 * (64 * p + 8 * c4);  // bytes
+        const half8 h0 = *reinterpret_cast<const half8 *>(tokrow + col);
+        const half8 l0 = *reinterpret_cast<const half8 *>(tokrow + 512 + col);
+        const half8 h1 = *reinterpret_cast<const half8 *>(tokrow + col + 64);
+        const half8 l1 = *reinterpret_cast<const half8 *>(tokrow + 512 + col + 64);
+#pragma unroll
+        for (int m = 0; m < MATS; m++)
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                half8 blo, bhi;
+                dec_pair(hd[m][t], p, w[m].q[p][t].x, w[m].q[p][t].y, blo, bhi);
+                w[m].q[p][t] = load_q16(wb[m], lo, kn, p, t, c4);
+                S[m][t] = mfma16(h0, blo, S[m][t]);
+                S[m][t] = mfma16(l0, blo, S[m][t]);
+                S[m][t] = mfma16(h1, bhi, S[m][t]);
+                S[m][t] = mfma16(l1, bhi, S[m][t]);
+            }
+        __builtin_amdgcn_sched_barrier(0);  // bounds the live operands to one pair
+    }
+    const half4 amin = *reinterpret_cast<const half4 *>(cur + kSumsOff + r16 * 32 + 8 * c4);
+#pragma unroll
+    for (int m = 0; m < MATS; m++)
+#pragma unroll
+        for (int t = 0; t < 2; t++) finish16(hd[m][t], amin, c4, S[m][t], acc[m][t]);
+    stage_store(nxt, act, wave, lane);
+    lds_barrier();
+}
+
+// block_pass() for a pass of at most 16 tokens; lo is the offset of this
+// lane's row r16 of the wave's first tile
+template <int MATS>
+__device__ __forceinline__ void block_pass16(g_u8 *const (&wb)[MATS], uint32_t lo,
+                                             int kb0, int kb1, const StageSrc &src,
+                                             float4v (&acc)[MATS][2]) {
+    const int lane = threadIdx.x & 63, c4 = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int last = kb1 - 1;
+    WRaw16 w[MATS];
+    StageRegs<4> act;
+    stage_load(act, src, kb0, wave, lane);
+#pragma unroll
+    for (int m = 0; m < MATS; m++) load_w16(w[m], wb[m], lo, kb0, c4);
+    stage_store(s_stage0, act, wave, lane);
+    lds_barrier();
+    int kb = kb0;
+    for (; kb + 2 <= kb1; kb += 2) {
+        step16<MATS>(wb, lo, kb + 1, s_stage0, s_stage1, src, w, acc, wave, lane);
+        step16<MATS>(wb, lo, min(kb + 2, last), s_stage1, s_stage0, src, w, acc, wave, lane);
+    }
+    if (kb < kb1) step16<MATS>(wb, lo, kb, s_stage0, s_stage1, src, w, acc, wave, lane);
 }
 
 // split v into f16 hi + lo
@@ -308,9 +498,9 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
     const int ngrp = F >> 5, grp0 = blockIdx.x * kWaves + wave;
     const int grp = min(grp0, ngrp - 1);  // duplicate the last group past the end
     const int NB = d >> 8, tile = grp >> 1, nsb = d >> 5;
-    const int64_t rowoff = (int64_t)tile * NB * 9 * 1024 + (32 * (grp & 1) + r) * 16;
-    const uint8_t *const wr[2] = {gate + (int64_t)e * estride + rowoff,
-                                  up + (int64_t)e * estride + rowoff};
+    const int64_t grpoff = (int64_t)tile * NB * 9 * 1024 + 32 * (grp & 1) * 16;
+    g_u8 *const wb[2] = {uniform(gate + (int64_t)e * estride + grpoff),
+                                  uniform(up + (int64_t)e * estride + grpoff)};
     const int f = grp * 32 + r, nkb = F >> 8;
     const uint8_t *xb = reinterpret_cast<const uint8_t *>(x16);
     const uint8_t *sb = reinterpret_cast<const uint8_t *>(xs);
@@ -319,11 +509,53 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const int tok = slot_token(sa, p0, min(c + wave + 4 * i, n - 1));
-            src.tok[i] = xb + (int64_t)tok * d * 4;
+            src.tok[i] = uniform(xb + (int64_t)tok * d * 4);
         }
-        src.sums = sb + (int64_t)slot_token(sa, p0, min(c + (lane >> 1), n - 1)) * nsb * 4;
+        src.sums = uniform(sb);
+        src.soff = (uint32_t)slot_token(sa, p0, min(c + (lane >> 1), n - 1)) * nsb * 4 +
+                   16 * (lane & 1);
+        if (n - c <= 16) {
+            const int r16 = lane & 15, c4 = lane >> 4;
+            float4v acc[2][2] = {};
+            block_pass16<2>(wb, r16 * 16, 0, NB, src, acc);
+            if (grp0 >= ngrp) continue;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int q = c + 4 * c4 + i;
+                _Float16 hi[2], lo[2];
+                float v[2], part = 0.0f;
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    v[t] = silu(acc[0][t][i]) * acc[1][t][i];
+                    split16(v[t], hi[t], lo[t]);
+                    part += (float)hi[t] + (float)lo[t];
+                }
+#pragma unroll
+                for (int off = 1; off < 16; off <<= 1) part += __shfl_xor(part, off, 64);
+                if (q < n) {
+                    const int64_t p = p0 + q;
+#pragma unroll
+                    for (int t = 0; t < 2; t++) {
+                        const int ft = grp * 32 + 16 * t + r16;
+                        if (hf) hf[p * F + ft] = v[t];
+                        if (h16) {
+                            _Float16 *piece = h16 + (p * nkb + (ft >> 8)) * 512 + (ft & 255);
+                            piece[0] = hi[t];
+                            piece[256] = lo[t];
+                        }
+                    }
+                    if (h16 && r16 == 0) {
+                        _Float16 shi, slo;
+                        split16(part, shi, slo);
+                        hs[(p * (F >> 5) + grp) * 2] = shi;
+                        hs[(p * (F >> 5) + grp) * 2 + 1] = slo;
+                    }
+                }
+            }
+            continue;
+        }
         float16v acc[2] = {float16v{}, float16v{}};
-        block_pass<2>(wr, 0, NB, src, acc);
+        block_pass<2>(wb, r * 16, 0, NB, src, acc);
         if (grp0 >= ngrp) continue;
         // SwiGLU, H out (f16 hi/lo pieces and/or f32), 32-row sub-block sums
 #pragma unroll
@@ -369,8 +601,8 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down(
     const int NB = F >> 8, tile = grp >> 1, nsb = F >> 5;
     const int kb0 = (int)((int64_t)NB * blockIdx.z / gridDim.z);
     const int kb1 = (int)((int64_t)NB * (blockIdx.z + 1) / gridDim.z);
-    const int64_t rowoff = (int64_t)tile * NB * 9 * 1024 + (32 * (grp & 1) + r) * 16;
-    const uint8_t *const wr[1] = {down + (int64_t)e * estride + rowoff};
+    g_u8 *const wb[1] = {
+        uniform(down + (int64_t)e * estride + (int64_t)tile * NB * 9 * 1024 + 32 * (grp & 1) * 16)};
     float *Yz = Y + (int64_t)blockIdx.z * split_stride;
     const int row = grp * 32 + r;
     const uint8_t *hb = reinterpret_cast<const uint8_t *>(h16);
@@ -379,10 +611,27 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down(
         StageSrc src;
 #pragma unroll
         for (int i = 0; i < 8; i++)
-            src.tok[i] = hb + (int64_t)(p0 + min(c + wave + 4 * i, n - 1)) * F * 4;
-        src.sums = sb + (int64_t)(p0 + min(c + (lane >> 1), n - 1)) * nsb * 4;
+            src.tok[i] = uniform(hb + (int64_t)(p0 + min(c + wave + 4 * i, n - 1)) * F * 4);
+        src.sums = uniform(sb);
+        src.soff = (uint32_t)(p0 + min(c + (lane >> 1), n - 1)) * nsb * 4 + 16 * (lane & 1);
+        if (n - c <= 16) {
+            const int r16 = lane & 15, c4 = lane >> 4;
+            float4v acc[1][2] = {};
+            block_pass16<1>(wb, r16 * 16, kb0, kb1, src, acc);
+            if (grp0 >= ngrp) continue;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int q = c + 4 * c4 + i;
+                if (q < n) {
+#pragma unroll
+                    for (int t = 0; t < 2; t++)
+                        Yz[(int64_t)(p0 + q) * d + grp * 32 + 16 * t + r16] = acc[0][t][i];
+                }
+            }
+            continue;
+        }
         float16v acc[1] = {float16v{}};
-        block_pass<1>(wr, kb0, kb1, src, acc);
+        block_pass<1>(wb, r * 16, kb0, kb1, src, acc);
         if (grp0 >= ngrp) continue;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
