@@ -349,6 +349,9 @@ __device__ __forceinline__ void block_pass(g_u8 *const (&wb)[MATS], uint32_t lo,
     const int lane = threadIdx.x & 63, h = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int last = kb1 - 1;
+    // opaque start: keeps the prologue's loads in base + 32-bit offset form
+    // instead of per-lane 64-bit addresses folded and kept across passes
+    asm volatile("" : "+s"(kb0));
     WRaw w[MATS];
     StageRegs<8> act;
     stage_load(act, src, kb0, wave, lane);
@@ -462,6 +465,7 @@ __device__ __forceinline__ void block_pass16(g_u8 *const (&wb)[MATS], uint32_t l
     const int lane = threadIdx.x & 63, c4 = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int last = kb1 - 1;
+    asm volatile("" : "+s"(kb0));  // see block_pass()
     WRaw16 w[MATS];
     StageRegs<4> act;
     stage_load(act, src, kb0, wave, lane);
@@ -519,6 +523,10 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
             float4v acc[2][2] = {};
             block_pass16<2>(wb, r16 * 16, 0, NB, src, acc);
             if (grp0 >= ngrp) continue;
+            // output addresses are formed here from an opaque row index, so
+            // that the compiler does not keep them live across the pass
+            int fb = grp * 32 + r16;
+            asm volatile("" : "+v"(fb));
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int q = c + 4 * c4 + i;
@@ -536,7 +544,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
                     const int64_t p = p0 + q;
 #pragma unroll
                     for (int t = 0; t < 2; t++) {
-                        const int ft = grp * 32 + 16 * t + r16;
+                        const int ft = fb + 16 * t;
                         if (hf) hf[p * F + ft] = v[t];
                         if (h16) {
                             _Float16 *piece = h16 + (p * nkb + (ft >> 8)) * 512 + (ft & 255);
@@ -557,6 +565,8 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
         float16v acc[2] = {float16v{}, float16v{}};
         block_pass<2>(wb, r * 16, 0, NB, src, acc);
         if (grp0 >= ngrp) continue;
+        int fo = f;  // opaque copy: output addresses are formed here (see above)
+        asm volatile("" : "+v"(fo));
         // SwiGLU, H out (f16 hi/lo pieces and/or f32), 32-row sub-block sums
 #pragma unroll
         for (int i = 0; i < 16; i++) {
@@ -569,9 +579,9 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
             for (int off = 1; off < 32; off <<= 1) part += __shfl_xor(part, off, 64);
             if (q < n) {
                 const int64_t p = p0 + q;
-                if (hf) hf[p * F + f] = v;
+                if (hf) hf[p * F + fo] = v;
                 if (h16) {
-                    _Float16 *piece = h16 + (p * nkb + (f >> 8)) * 512 + (f & 255);
+                    _Float16 *piece = h16 + (p * nkb + (fo >> 8)) * 512 + (fo & 255);
                     piece[0] = hi;
                     piece[256] = lo;
                     if (r == 0) {
