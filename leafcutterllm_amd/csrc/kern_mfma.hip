@@ -322,14 +322,15 @@ __device__ __forceinline__ void step(g_u8 *const (&wb)[MATS], uint32_t lo, int k
 #pragma unroll
     for (int m = 0; m < MATS; m++) S[m] = float16v{};
     const uint8_t *tokrow = cur + r * kTokBytes;
+    AUnit a[2];  // unit u's operands, and unit u+1's read ahead
+    read_a(a[0], tokrow, 0, h);
 #pragma unroll
     for (int u = 0; u < 8; u++) {
-        AUnit a;
-        read_a(a, tokrow, u, h);
-        unit_mfma<MATS>(w, hd, u, a, S);
+        if (u + 1 < 8) read_a(a[(u + 1) & 1], tokrow, u + 1, h);
+        unit_mfma<MATS>(w, hd, u, a[u & 1], S);
 #pragma unroll
         for (int m = 0; m < MATS; m++) w[m].q[u] = load_q(wb[m], lo, kn, 1 + u, 8 * h);
-        __builtin_amdgcn_sched_barrier(0);  // bounds the live operands to one unit
+        __builtin_amdgcn_sched_barrier(0);  // bounds the live operands to two units
     }
     const half8 amin = *reinterpret_cast<const half8 *>(cur + kSumsOff + r * 32 + 16 * h);
 #pragma unroll
@@ -402,6 +403,16 @@ __device__ __forceinline__ void finish16(const Hdr &hd, const half4 &amin, int c
     }
 }
 
+// Activation operands of pair p for a 16-token pass: token r16, columns
+// 8*c4 .. +7 of sub-blocks 2p and 2p+1, hi and lo halves
+__device__ __forceinline__ void read_a16(AUnit &a, const uint8_t *tokrow, int p, int c4) {
+    const int col = 2 * (64 * p + 8 * c4);  // bytes
+    a.h0 = *reinterpret_cast<const half8 *>(tokrow + col);
+    a.l0 = *reinterpret_cast<const half8 *>(tokrow + 512 + col);
+    a.h1 = *reinterpret_cast<const half8 *>(tokrow + col + 64);
+    a.l1 = *reinterpret_cast<const half8 *>(tokrow + 512 + col + 64);
+}
+
 // One step of a 16-token pass (same pipeline as step()).  Per pair p the
 // activations of sub-blocks 2p and 2p+1 (hi, lo) are read once and shared by
 // both tiles and all matrices.
@@ -426,13 +437,12 @@ __device__ __forceinline__ void step16(g_u8 *const (&wb)[MATS], uint32_t lo, int
 #pragma unroll
     for (int m = 0; m < MATS; m++) S[m][0] = S[m][1] = float4v{};
     const uint8_t *tokrow = cur + r16 * kTokBytes;
+    AUnit a[2];  // pair p's operands, and pair p+1's read ahead
+    read_a16(a[0], tokrow, 0, c4);
 #pragma unroll
     for (int p = 0; p < 4; p++) {
-        const int col = 2 * (64 * p + 8 * c4);  // bytes
-        const half8 h0 = *reinterpret_cast<const half8 *>(tokrow + col);
-        const half8 l0 = *reinterpret_cast<const half8 *>(tokrow + 512 + col);
-        const half8 h1 = *reinterpret_cast<const half8 *>(tokrow + col + 64);
-        const half8 l1 = *reinterpret_cast<const half8 *>(tokrow + 512 + col + 64);
+        if (p + 1 < 4) read_a16(a[(p + 1) & 1], tokrow, p + 1, c4);
+        const half8 h0 = a[p & 1].h0, l0 = a[p & 1].l0, h1 = a[p & 1].h1, l1 = a[p & 1].l1;
 #pragma unroll
         for (int m = 0; m < MATS; m++)
 #pragma unroll
@@ -445,7 +455,7 @@ __device__ __forceinline__ void step16(g_u8 *const (&wb)[MATS], uint32_t lo, int
                 S[m][t] = mfma16(h1, bhi, S[m][t]);
                 S[m][t] = mfma16(l1, bhi, S[m][t]);
             }
-        __builtin_amdgcn_sched_barrier(0);  // bounds the live operands to one pair
+        __builtin_amdgcn_sched_barrier(0);  // bounds the live operands to two pairs
     }
     const half4 amin = *reinterpret_cast<const half4 *>(cur + kSumsOff + r16 * 32 + 8 * c4);
 #pragma unroll
@@ -596,8 +606,10 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
     }
 }
 
-// grid (d/128 row blocks, slots, ksplit); partial sums of K slice z go to
-// Y + z * split_stride
+// grid (d/256 row blocks, slots, ksplit); partial sums of K slice z go to
+// Y + z * split_stride.  A wave owns one 64-row RPL tile as two 32-row halves
+// that share every activation read (the two "matrices" of the pipeline), so
+// each LDS read feeds twice the weight bytes of a 32-row wave.
 __global__ __launch_bounds__(256, 2) void k_mfma_down(
     const uint8_t *__restrict__ down, int64_t estride, const _Float16 *__restrict__ h16,
     const _Float16 *__restrict__ hs, SlotArgs sa, int d, int F, float *__restrict__ Y,
@@ -606,15 +618,14 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down(
     if (!slot_info(sa, blockIdx.y, e, p0, n)) return;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
-    const int ngrp = d >> 5, grp0 = blockIdx.x * kWaves + wave;
-    const int grp = min(grp0, ngrp - 1);
-    const int NB = F >> 8, tile = grp >> 1, nsb = F >> 5;
+    const int ntile = d >> 6, tile0 = blockIdx.x * kWaves + wave;
+    const int tile = min(tile0, ntile - 1);  // duplicate the last tile past the end
+    const int NB = F >> 8, nsb = F >> 5;
     const int kb0 = (int)((int64_t)NB * blockIdx.z / gridDim.z);
     const int kb1 = (int)((int64_t)NB * (blockIdx.z + 1) / gridDim.z);
-    g_u8 *const wb[1] = {
-        uniform(down + (int64_t)e * estride + (int64_t)tile * NB * 9 * 1024 + 32 * (grp & 1) * 16)};
+    const uint8_t *tb = down + (int64_t)e * estride + (int64_t)tile * NB * 9 * 1024;
+    g_u8 *const wb[2] = {uniform(tb), uniform(tb + 32 * 16)};
     float *Yz = Y + (int64_t)blockIdx.z * split_stride;
-    const int row = grp * 32 + r;
     const uint8_t *hb = reinterpret_cast<const uint8_t *>(h16);
     const uint8_t *sb = reinterpret_cast<const uint8_t *>(hs);
     for (int c = 0; c < n; c += kTok) {
@@ -626,27 +637,37 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down(
         src.soff = (uint32_t)(p0 + min(c + (lane >> 1), n - 1)) * nsb * 4 + 16 * (lane & 1);
         if (n - c <= 16) {
             const int r16 = lane & 15, c4 = lane >> 4;
-            float4v acc[1][2] = {};
-            block_pass16<1>(wb, r16 * 16, kb0, kb1, src, acc);
-            if (grp0 >= ngrp) continue;
+            float4v acc[2][2] = {};
+            block_pass16<2>(wb, r16 * 16, kb0, kb1, src, acc);
+            if (tile0 >= ntile) continue;
+            int rb = tile * 64 + r16;  // opaque: output addresses are formed here
+            asm volatile("" : "+v"(rb));
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int q = c + 4 * c4 + i;
                 if (q < n) {
+                    float *yrow = Yz + (int64_t)(p0 + q) * d + rb;
 #pragma unroll
-                    for (int t = 0; t < 2; t++)
-                        Yz[(int64_t)(p0 + q) * d + grp * 32 + 16 * t + r16] = acc[0][t][i];
+                    for (int m = 0; m < 2; m++)
+#pragma unroll
+                        for (int t = 0; t < 2; t++) yrow[32 * m + 16 * t] = acc[m][t][i];
                 }
             }
             continue;
         }
-        float16v acc[1] = {float16v{}};
-        block_pass<1>(wb, r * 16, kb0, kb1, src, acc);
-        if (grp0 >= ngrp) continue;
+        float16v acc[2] = {float16v{}, float16v{}};
+        block_pass<2>(wb, r * 16, kb0, kb1, src, acc);
+        if (tile0 >= ntile) continue;
+        int rb = tile * 64 + r;  // opaque: output addresses are formed here
+        asm volatile("" : "+v"(rb));
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int q = c + c_token(i, h);
-            if (q < n) Yz[(int64_t)(p0 + q) * d + row] = acc[0][i];
+            if (q < n) {
+                float *yrow = Yz + (int64_t)(p0 + q) * d + rb;
+                yrow[0] = acc[0][i];
+                yrow[32] = acc[1][i];
+            }
         }
     }
 }
@@ -715,8 +736,8 @@ hipError_t launch_mfma_gateup(const uint8_t *gate, const uint8_t *up, int64_t es
 hipError_t launch_mfma_down(const uint8_t *down, int64_t estride, const _Float16 *h16,
                             const _Float16 *hs, const SlotArgsHost &sa, int slots, int d, int F,
                             int ksplit, float *Y, int64_t split_stride, hipStream_t st) {
-    const int groups = d / 32;
-    hipLaunchKernelGGL(k_mfma_down, dim3((groups + kWaves - 1) / kWaves, slots, ksplit), dim3(256),
+    const int tiles = d / 64;
+    hipLaunchKernelGGL(k_mfma_down, dim3((tiles + kWaves - 1) / kWaves, slots, ksplit), dim3(256),
                        0, st, down, estride, h16, hs, dev_slots(sa), d, F, Y, split_stride);
     return hipGetLastError();
 }

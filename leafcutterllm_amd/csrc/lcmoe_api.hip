@@ -193,10 +193,10 @@ int choose_ksplit(const ExpertSet &s, int d, int active) {
     return ks;
 }
 
-// Matrix-core down: 128-row blocks, two resident per CU; split K until
+// Matrix-core down: 256-row blocks, two resident per CU; split K until
 // about two blocks per CU exist, keeping >= 4 super-blocks per split.
 int choose_ksplit_mfma(const ExpertSet &s, int d, int active) {
-    const int NB = s.F / 256, blocks = ((d / 32 + 3) / 4) * std::max(1, active);
+    const int NB = s.F / 256, blocks = ((d / 64 + 3) / 4) * std::max(1, active);
     int ks = 1;
     while (ks < s.kmax && blocks * ks < 512 && NB >= 4 * ks * 2) ks *= 2;
     return ks;
