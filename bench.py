@@ -65,6 +65,21 @@ def cpu_baseline(cfg, layer, x, budget_s=15.0):
     }
 
 
+def measured_traffic(config: int, tokens: int):
+    """HBM bytes per gate/up launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes (profiles/traffic.json, calibrated by a plain copy), when
+    they were taken on this workload; None otherwise."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("workload") != f"config {config}, T={tokens}":
+        return None
+    return int(t["bytes"])
+
+
 def copy_probe(mib: int):
     """Three plain device-to-device copies of `mib` MiB: a known byte count to
     scale rocprofv3's FETCH_SIZE / WRITE_SIZE counters by."""
@@ -198,7 +213,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_k weights, f32 activations/accumulate",
+        "dtype": "f32 (f16 hi+lo activation halves x exact f16 sc*q weights on MFMA, f32 accumulate)",
         "data": "synthetic (seeded splitmix64 N(0,1) activations, N(0,0.02) weights quantised to Q4_K)",
         "config": {
             "workload": f"config {args.config}: {cfg.note}, d_model={cfg.d_model}, d_ff={cfg.d_ff}, "
@@ -213,7 +228,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(head["gateup_GBps"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(args.config, args.tokens),
+            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
+            "algorithmic_bytes": round(head["gateup_bytes"]),
         },
         "layer_roofline_frac": round(head["layer_GBps"] / HBM_PEAK_GBS, 4),
         "per_batch": {str(T): {k: (round(v, 4) if isinstance(v, float) else v)

@@ -436,8 +436,9 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB, int E
 // k-th against every unselected expert), the reference chain selects exactly
 // those experts in that order, and the selection is final.  Otherwise the
 // block runs the exact chains for that token and selects from them.  The
-// routing weights need the chain values themselves; mode 1 of k_router
-// computes them beside the expert products.
+// routing weights need the chain values themselves: mode 2 of k_router
+// computes them on a second stream beside the expert products, and the
+// combine turns them into weights.
 // ---------------------------------------------------------------------------
 
 // next float toward +inf / -inf (finite, non-NaN arguments)
