@@ -124,19 +124,40 @@ __device__ __forceinline__ void pass2(const uint4 *__restrict__ G, const uint4 *
     }
 }
 
+// this lane's 9 chunks of super-block kb
+__device__ __forceinline__ void load_chunks(uint4 (&c)[9], const uint4 *W, int kb) {
+    const uint4 *p = W + (int64_t)kb * 9 * 64;
+#pragma unroll
+    for (int i = 0; i < 9; i++) c[i] = p[i * 64];
+}
+
+template <int NT>
+__device__ __forceinline__ void dot_sb(const uint4 (&c)[9], int kb, const Limbs &X,
+                                       const int (&row)[NT], float (&acc)[NT]) {
+    const int *xh[NT], *xl[NT];
+    const float *xs[NT], *xm[NT];
+    token_ptrs<NT>(X, row, kb, xh, xl, xs, xm);
+    q4_block_dot<NT>(c, xh, xl, xs, xm, acc);
+}
+
+// Rows of this lane over super-blocks [kb0, kb1), the next super-block's
+// chunks loaded while the current one is computed (two register sets; the
+// loads complete in issue order, so waiting for the current set leaves the
+// next one in flight).
 template <int NT>
 __device__ __forceinline__ void pass1(const uint4 *__restrict__ W, int kb0, int kb1,
                                       const Limbs &X, const int (&row)[NT], float (&acc)[NT]) {
-    for (int kb = kb0; kb < kb1; kb++) {
-        uint4 cw[9];
-        const uint4 *pw = W + (int64_t)kb * 9 * 64;
-#pragma unroll
-        for (int i = 0; i < 9; i++) cw[i] = pw[i * 64];
-        const int *xh[NT], *xl[NT];
-        const float *xs[NT], *xm[NT];
-        token_ptrs<NT>(X, row, kb, xh, xl, xs, xm);
-        q4_block_dot<NT>(cw, xh, xl, xs, xm, acc);
+    if (kb0 >= kb1) return;
+    uint4 c0[9], c1[9];
+    load_chunks(c0, W, kb0);
+    int kb = kb0;
+    for (; kb + 2 <= kb1; kb += 2) {
+        load_chunks(c1, W, kb + 1);
+        dot_sb<NT>(c0, kb, X, row, acc);
+        load_chunks(c0, W, min(kb + 2, kb1 - 1));
+        dot_sb<NT>(c1, kb + 1, X, row, acc);
     }
+    if (kb < kb1) dot_sb<NT>(c0, kb, X, row, acc);
 }
 
 struct HOut {
@@ -145,11 +166,15 @@ struct HOut {
     float *s, *m;   // [positions, F/32]
 };
 
-constexpr int kMaxNT = 8;
+// Tokens per pass.  This path runs when experts average fewer than two
+// tokens (the matrix-core kernels take larger batches), so passes of at most
+// four keep the tokens' limbs within the scalar register file; an expert
+// with more tokens takes several passes.
+constexpr int kMaxNT = 4;
 
 // Token rows c .. c+NT-1 of one gate/up tile (rows past n repeat the last
 // token and are not written): the 4 waves' partial sums meet in LDS, then
-// wave w finishes tokens w and w+4 (SwiGLU, H out).
+// wave w finishes token w (SwiGLU, H out).
 template <int NT>
 __device__ __forceinline__ void gateup_chunk(const uint4 *G, const uint4 *U, int kb0, int kb1,
                                              const Limbs &X, const SlotArgs &sa, int p0, int n,
@@ -219,9 +244,7 @@ __global__ __launch_bounds__(256) void k_rpl_gateup(
     const int f = rt * 64 + lane;
     for (int c = 0; c < n; c += kMaxNT) {
         const int left = n - c;
-        if (left > 4)
-            gateup_chunk<8>(G, U, kb0, kb1, X, sa, p0, n, c, F, f, out, s_red);
-        else if (left > 2)
+        if (left > 2)
             gateup_chunk<4>(G, U, kb0, kb1, X, sa, p0, n, c, F, f, out, s_red);
         else if (left == 2)
             gateup_chunk<2>(G, U, kb0, kb1, X, sa, p0, n, c, F, f, out, s_red);
@@ -278,9 +301,7 @@ __global__ __launch_bounds__(256) void k_rpl_down(
     const int r = rt * 64 + lane;
     for (int c = 0; c < n; c += kMaxNT) {
         const int left = n - c;
-        if (left > 4)
-            down_chunk<8>(W, kb0, kb1, X, p0, n, c, d, r, Yz, s_red);
-        else if (left > 2)
+        if (left > 2)
             down_chunk<4>(W, kb0, kb1, X, p0, n, c, d, r, Yz, s_red);
         else if (left == 2)
             down_chunk<2>(W, kb0, kb1, X, p0, n, c, d, r, Yz, s_red);

@@ -34,7 +34,7 @@ const char *kSlotNames[kNumSlots] = {"router", "act16", "gateup", "gateup_shared
                                      "down_shared", "combine", "router_exact"};
 constexpr int kMaxKSplit = 4;
 // matrix-core path when an expert family averages at least this many tokens
-constexpr int kMfmaMinTokens = 6;
+constexpr int kMfmaMinTokens = 1;
 
 struct ExpertSet {  // one family of experts (routed or shared)
     int n = 0, F = 0, qt_gu = 0, qt_dn = 0;
@@ -183,13 +183,14 @@ hipError_t timed(lcmoe_handle *h, hipStream_t st, int slot, Fn fn) {
     return e;
 }
 
-// Column splits of the down product so that small batches still launch
-// enough waves: each wave keeps >= 2 super-blocks.
+// Column splits of the row-per-lane down product so that small batches
+// still launch about two blocks per CU; each wave keeps >= 2 super-blocks
+// (it loads the next while computing the current one).
 int choose_ksplit(const ExpertSet &s, int d, int active) {
     if (!s.rpl_dn) return 1;
     const int NB = s.F / 256, tiles = (d / 64) * std::max(1, active);
     int ks = 1;
-    while (ks < s.kmax && tiles * ks < 256 && NB >= 8 * ks * 2) ks *= 2;
+    while (ks < s.kmax && tiles * ks < 512 && NB >= 4 * ks * 2 * 2) ks *= 2;
     return ks;
 }
 
@@ -343,8 +344,12 @@ static Plan plan_set(lcmoe_handle *h, const ExpertSet &s, bool shared, int T) {
     const lcmoe_desc &D = h->desc;
     Plan p;
     p.slots = shared ? s.n : std::min(D.n_expert, T * D.n_expert_used);
-    const int avg = shared ? T : (T * D.n_expert_used) / std::max(1, p.slots);
-    p.mfma = s.rpl_gu && avg >= kMfmaMinTokens;
+    // tokens per expert averaged over all experts (over the touched ones it
+    // is >= 1 by construction): the matrix-core kernels decode each weight
+    // once for up to 32 tokens, the row-per-lane ones once per token pass
+    const int64_t per_expert =
+        shared ? T : (int64_t)T * D.n_expert_used / std::max(1, D.n_expert);
+    p.mfma = s.rpl_gu && per_expert >= kMfmaMinTokens;
     p.ks = p.mfma && s.rpl_dn ? choose_ksplit_mfma(s, D.d_model, p.slots)
                                : choose_ksplit(s, D.d_model, p.slots);
     return p;
