@@ -292,8 +292,6 @@ __device__ __forceinline__ float chain16(const float4 *xr, const float4 *wr, int
 // mode 0: exact logits, x limbs, top-k and dispatch (the whole router).
 // mode 1: exact logits and the routing weights of an already-made selection
 // (a.topk_idx), nothing else.
-// mode 2: exact logits only; runs beside the certified fast router and the
-// expert products, and the combine turns them into routing weights.
 __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB, int EG, int mode) {
     extern __shared__ float smem[];
     const int d = a.d, E = a.E, stride = d + kPad;
@@ -361,7 +359,6 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB, int E
             acc = chain16<false>(xr, wr, d / 4, acc);
     }
     if (chain) a.logits[(int64_t)(t0 + ct) * E + e] = acc;
-    if (mode == 2) return;  // logits only
 
     // ---- last expert-group block of this token group selects top-k
     const int n_eg = gridDim.y, n_tg = gridDim.x;
@@ -565,6 +562,77 @@ __device__ float exact_logit(const RouterArgs &a, int t, int e) {
     return acc;
 }
 
+// ---- exact chains streamed through LDS, one wave at a time ----------------
+constexpr int kCh = 256;         // columns per streamed chunk
+constexpr int kChRow = kCh + 4;  // LDS row stride (floats): rows start on different banks
+
+// LDS floats for a wave streaming NR rows: two chunk buffers, plus the 16
+// floats chain16 prefetches past a row
+constexpr int stream_floats(int NR) { return 2 * NR * kChRow + 16; }
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+// Exact reference chains (chain16's order) of up to 64 (token, expert)
+// pairs in one wave: lane l < NT*NE takes token t0 + l / NE and expert
+// e0 + l % NE (both clamped to the last valid index; callers drop those
+// lanes).  The NT x rows and NE router rows are streamed through this wave's
+// LDS region `lds` (stream_floats(NT + NE) floats) in chunks of kCh columns,
+// double-buffered: the wave loads chunk c+1 into registers while its lanes
+// run the chunk-c chains from LDS, then stores it.  LDS traffic stays inside
+// the wave, so only wave-level synchronisation is needed.
+template <int NT, int NE>
+__device__ float wave_chains(const RouterArgs &a, int t0, int e0, float *lds) {
+    constexpr int NR = NT + NE;
+    const int lane = threadIdx.x & 63, nch = a.d / kCh;
+    const int tb = min(lane / NE, NT - 1), eg = lane % NE;
+    const bool fma = min(e0 + eg, a.E - 1) < (a.E & ~7);
+    const float4 *src[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        const float *row = r < NT ? a.x + (int64_t)min(t0 + r, a.T - 1) * a.d
+                                  : a.wrt + (int64_t)min(e0 + r - NT, a.E - 1) * a.d;
+        src[r] = reinterpret_cast<const float4 *>(row) + lane;
+    }
+    float4 v[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) v[r] = src[r][0];
+#pragma unroll
+    for (int r = 0; r < NR; r++) reinterpret_cast<float4 *>(lds + r * kChRow)[lane] = v[r];
+    wave_lds_sync();
+    float acc = 0.0f;
+    for (int c = 0; c < nch; c++) {
+        const float *cur = lds + (c & 1) * NR * kChRow;
+        float *nxt = lds + ((c + 1) & 1) * NR * kChRow;
+        const bool more = c + 1 < nch;
+        if (more)
+#pragma unroll
+            for (int r = 0; r < NR; r++) v[r] = src[r][(c + 1) * (kCh / 4)];
+        const float4 *xr = reinterpret_cast<const float4 *>(cur + tb * kChRow);
+        const float4 *wr = reinterpret_cast<const float4 *>(cur + (NT + eg) * kChRow);
+        acc = fma ? chain16<true>(xr, wr, kCh / 4, acc) : chain16<false>(xr, wr, kCh / 4, acc);
+        if (more)
+#pragma unroll
+            for (int r = 0; r < NR; r++) reinterpret_cast<float4 *>(nxt + r * kChRow)[lane] = v[r];
+        wave_lds_sync();
+    }
+    return acc;
+}
+
+// The exact reference logits of all T x E (token, expert) pairs, for the
+// routing weights beside the certified fast router.  Off the critical path,
+// so it is shaped to hold few resources while the expert products run: one
+// wave per 8 tokens x 8 experts, 33 KB of LDS.
+__global__ __launch_bounds__(64) void k_exact_logits(RouterArgs a) {
+    __shared__ __attribute__((aligned(16))) float s[stream_floats(16)];
+    const int t0 = blockIdx.x * 8, e0 = blockIdx.y * 8, lane = threadIdx.x;
+    const float v = wave_chains<8, 8>(a, t0, e0, s);
+    const int t = t0 + lane / 8, e = e0 + lane % 8;
+    if (t < a.T && e < a.E) a.logits[(int64_t)t * a.E + e] = v;
+}
+
 // float64 logit S_d and chain error bound of every expert for token t; wave
 // w takes experts w, w+8, ...; lane l holds columns [l*C, l*C + C) with
 // C = 4*NC4 in registers.  sum_k |S_k| is bounded by groups of 4 columns:
@@ -669,7 +737,10 @@ __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a) {
     __shared__ int s_cw[kFastThreads / 64][kMaxE];
     __shared__ int s_off[kMaxE + 1];
     __shared__ int s_flag;
-    __shared__ __attribute__((aligned(16))) float s_x[64 * (64 + 4)];  // C <= 64
+    // x row for the logits (C <= 64 floats per lane), later the fallback's
+    // chain stream (one token, 8 experts)
+    constexpr int kXFloats = 64 * (64 + 4), kFbFloats = stream_floats(1 + 8);
+    __shared__ __attribute__((aligned(16))) float s_x[kXFloats > kFbFloats ? kXFloats : kFbFloats];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int t = blockIdx.x, d = a.d, E = a.E, K = a.K;
 
@@ -736,7 +807,11 @@ __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a) {
     }
     __syncthreads();
     if (!s_flag) {  // 3. fallback: exact chains, exact selection
-        for (int e = tid; e < E; e += kFastThreads) a.logits[(int64_t)t * E + e] = exact_logit(a, t, e);
+        if (wave == 0)
+            for (int e0 = 0; e0 < E; e0 += 8) {
+                const float v = wave_chains<1, 8>(a, t, e0, s_x);
+                if (lane < 8 && e0 + lane < E) a.logits[(int64_t)t * E + e0 + lane] = v;
+            }
         __threadfence_block();
         __syncthreads();
         if (wave == 0) {
@@ -801,6 +876,12 @@ hipError_t launch_router(const RouterArgs &a, int mode, hipStream_t st) {
 
 // softmax kinds, at most 64 experts, d = 64 * 4 * NC4 with NC4 in
 // {1, 2, 4, 8, 16}
+hipError_t launch_exact_logits(const RouterArgs &a, hipStream_t st) {
+    if (a.d % kCh) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_exact_logits, dim3((a.T + 7) / 8, (a.E + 7) / 8), dim3(64), 0, st, a);
+    return hipGetLastError();
+}
+
 bool route_fast_ok(const RouterArgs &a) {
     const int c4 = a.d / 256;
     return a.rp.kind != LCMOE_ROUTE_SIGMOID_GROUP && a.wlc && a.E <= 64 && a.d % 256 == 0 &&

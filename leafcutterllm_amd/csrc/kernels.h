@@ -34,9 +34,12 @@ struct RouterArgs {
 // logits and the weights of the selection already in topk_idx.
 hipError_t launch_router(const RouterArgs &a, int mode, hipStream_t st);
 // Certified fast router for the softmax kinds: selection, dispatch, limbs
-// and f16 pieces; weights come from launch_router mode 1.
+// and f16 pieces; the weights come from the exact logits.
 bool route_fast_ok(const RouterArgs &a);
 hipError_t launch_route_fast(const RouterArgs &a, hipStream_t st);
+// The exact reference logits of all T x E pairs into a.logits, one chain
+// per thread (reads a.x, a.wrt; nothing else).
+hipError_t launch_exact_logits(const RouterArgs &a, hipStream_t st);
 int router_token_groups(int T, int d, int E);
 
 struct SlotArgsHost {

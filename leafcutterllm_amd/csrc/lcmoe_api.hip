@@ -63,7 +63,6 @@ struct lcmoe_handle {
     // beside the expert products when the fast router certified the selection
     hipStream_t side = nullptr;
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
-    uint32_t *sync_side = nullptr;
     std::vector<void *> allocs;
     float *wrt = nullptr, *bias = nullptr;
     // router in the fast router's lane-chunk order (null when d is not
@@ -324,9 +323,7 @@ extern "C" lcmoe_status lcmoe_create(const lcmoe_desc *desc, const lcmoe_weights
     if ((st = alloc_n(h, &h->touched, E + 1))) return bail(st);
     const int nsync = router_token_groups((int)Tm, (int)d, (int)E) + 1;
     if ((st = alloc_n(h, &h->sync, nsync))) return bail(st);
-    if ((st = alloc_n(h, &h->sync_side, nsync))) return bail(st);
-    if (hipMemset(h->sync, 0, sizeof(uint32_t) * nsync) != hipSuccess ||
-        hipMemset(h->sync_side, 0, sizeof(uint32_t) * nsync) != hipSuccess)
+    if (hipMemset(h->sync, 0, sizeof(uint32_t) * nsync) != hipSuccess)
         return bail(fail(LCMOE_ERR_HIP, "workspace clear failed"));
     *out = h;
     return LCMOE_OK;
@@ -424,10 +421,7 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
         // certified fast router; the combine turns the chains into weights
         HIP_TRY(hipEventRecord(h->ev_fork, st));
         HIP_TRY(hipStreamWaitEvent(h->side, h->ev_fork, 0));
-        RouterArgs rb = ra;
-        rb.xh = nullptr;
-        rb.sync = h->sync_side;
-        HIP_TRY(timed(h, h->side, kSlotRouterExact, [&] { return launch_router(rb, 2, h->side); }));
+        HIP_TRY(timed(h, h->side, kSlotRouterExact, [&] { return launch_exact_logits(ra, h->side); }));
         HIP_TRY(hipEventRecord(h->ev_join, h->side));
         ra.x16 = mfma ? h->x16 : nullptr;
         HIP_TRY(timed(h, st, kSlotRouter, [&] { return launch_route_fast(ra, st); }));
