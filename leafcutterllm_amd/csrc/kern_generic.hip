@@ -18,13 +18,31 @@ namespace {
 constexpr int kRB = 16;  // output rows per block (4 per wave)
 constexpr int kNT = 4;   // tokens per pass
 
+// grid (F/kRB row blocks, [chain row +] slots); with ch.tiles, row y = 0 runs
+// the exact router chains (wave 0 of each block, one tile at a time)
 template <int QT>
 __global__ __launch_bounds__(256) void k_gateup(const uint8_t *__restrict__ gate,
                                                 const uint8_t *__restrict__ up, int64_t estride,
                                                 const float *__restrict__ x, SlotArgs sa, int d,
-                                                int F, float *__restrict__ H) {
+                                                int F, float *__restrict__ H, ChainArgs ch) {
+    int slot = blockIdx.y;
+    if (ch.tiles) {
+        if (slot == 0) {
+            __shared__ __attribute__((aligned(16))) float s_chain[chain_lds_floats(9, 256)];
+            static_assert(chain_lds_floats(9, 256) >= chain_lds_floats(16, 128), "chain LDS");
+            if (threadIdx.x < 64)
+                for (int tile = blockIdx.x; tile < ch.tiles; tile += gridDim.x) {
+                    if (ch.nt == 1)
+                        chain_tile<1, 256, 2>(ch, tile, s_chain);
+                    else
+                        chain_tile<8, 128, 1>(ch, tile, s_chain);
+                }
+            return;
+        }
+        slot -= 1;
+    }
     int e, p0, n;
-    if (!slot_info(sa, blockIdx.y, e, p0, n)) return;
+    if (!slot_info(sa, slot, e, p0, n)) return;
     const uint8_t *G = gate + (int64_t)e * estride, *U = up + (int64_t)e * estride;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int ng = d >> 3;
@@ -209,9 +227,15 @@ SlotArgs dev_slots(const SlotArgsHost &s) {
 
 hipError_t launch_generic_gateup(int qt, const uint8_t *gate, const uint8_t *up, int64_t estride,
                                  const float *x, const SlotArgsHost &sa, int slots, int d, int F,
-                                 float *Hf, int8_t *, int8_t *, float *, float *, hipStream_t st) {
-    return launch_typed<GateUpK>(qt, dim3((F + kRB - 1) / kRB, slots), dim3(256), st, gate, up,
-                                 estride, x, dev_slots(sa), d, F, Hf);
+                                 float *Hf, int8_t *, int8_t *, float *, float *,
+                                 const ChainArgs &ch, hipStream_t st) {
+    ChainArgs c = ch;
+    if (c.tiles) {
+        if (c.k0 % 256 || c.k1 % 256) return hipErrorInvalidValue;
+        c = with_nt(ch, ch.T == 1 ? 1 : 8);
+    }
+    return launch_typed<GateUpK>(qt, dim3((F + kRB - 1) / kRB, slots + (c.tiles ? 1 : 0)),
+                                 dim3(256), st, gate, up, estride, x, dev_slots(sa), d, F, Hf, c);
 }
 
 hipError_t launch_generic_down(int qt, const uint8_t *down, int64_t estride, const float *Hf,

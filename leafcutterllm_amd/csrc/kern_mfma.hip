@@ -500,13 +500,31 @@ __device__ __forceinline__ void split16(float v, _Float16 &hi, _Float16 &lo) {
 // token (within the pass) held in C register i by half h
 __device__ __forceinline__ int c_token(int i, int h) { return 8 * (i >> 2) + 4 * h + (i & 3); }
 
-// grid (F/128 row blocks, slots); block = 4 waves x 32 weight rows
+// Each wave of a chain block streams its chain tiles through its own half
+// of one activation stage.
+static_assert(kStageBytes / 8 >= chain_lds_floats(16, 128), "chain tile LDS");
+
+// grid (F/128 row blocks, [chain row +] slots); block = 4 waves x 32 weight
+// rows.  With ch.tiles, row y = 0 runs the exact router chains (a wave per
+// 8 x 8 tile) and slot s is row s + 1.
 __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
     const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up, int64_t estride,
     const _Float16 *__restrict__ x16, const _Float16 *__restrict__ xs, SlotArgs sa, int d, int F,
-    _Float16 *__restrict__ h16, _Float16 *__restrict__ hs, float *__restrict__ hf) {
+    _Float16 *__restrict__ h16, _Float16 *__restrict__ hs, float *__restrict__ hf, ChainArgs ch) {
+    int slot = blockIdx.y;
+    if (ch.tiles) {
+        if (slot == 0) {
+            const int cw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+            float *lds = reinterpret_cast<float *>(cw < 2 ? s_stage0 : s_stage1) +
+                         (cw & 1) * (kStageBytes / 8);
+            for (int tile = blockIdx.x * kWaves + cw; tile < ch.tiles; tile += gridDim.x * kWaves)
+                chain_tile<8, 128, 1>(ch, tile, lds);
+            return;
+        }
+        slot -= 1;
+    }
     int e, p0, n;
-    if (!slot_info(sa, blockIdx.y, e, p0, n)) return;
+    if (!slot_info(sa, slot, e, p0, n)) return;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
     const int ngrp = F >> 5, grp0 = blockIdx.x * kWaves + wave;
@@ -726,10 +744,16 @@ hipError_t launch_act16(const float *x, int T, int d, _Float16 *x16, _Float16 *x
 hipError_t launch_mfma_gateup(const uint8_t *gate, const uint8_t *up, int64_t estride,
                               const _Float16 *x16, const _Float16 *xs, const SlotArgsHost &sa,
                               int slots, int d, int F, _Float16 *h16, _Float16 *hs, float *hf,
-                              hipStream_t st) {
+                              const ChainArgs &ch, hipStream_t st) {
     const int groups = F / 32;
-    hipLaunchKernelGGL(k_mfma_gateup, dim3((groups + kWaves - 1) / kWaves, slots), dim3(256), 0,
-                       st, gate, up, estride, x16, xs, dev_slots(sa), d, F, h16, hs, hf);
+    ChainArgs c = ch;
+    if (c.tiles) {
+        if (c.k0 % 256 || c.k1 % 256) return hipErrorInvalidValue;
+        c = with_nt(ch, 8);
+    }
+    hipLaunchKernelGGL(k_mfma_gateup, dim3((groups + kWaves - 1) / kWaves, slots + (c.tiles ? 1 : 0)),
+                       dim3(256), 0, st, gate, up, estride, x16, xs, dev_slots(sa), d, F, h16, hs,
+                       hf, c);
     return hipGetLastError();
 }
 

@@ -17,6 +17,7 @@
 // Counters are reset by the blocks that consume them, so the next launch on
 // the stream starts from zero.
 
+#include "chains.h"
 #include "device_common.h"
 #include "kernels.h"
 
@@ -524,115 +525,6 @@ __device__ void quantise_token(const RouterArgs &a, int t) {
     }
 }
 
-// exact reference chain of expert e for token t (fallback path): operands in
-// batches of 32 columns, the next batch loading while this one chains
-__device__ float exact_logit(const RouterArgs &a, int t, int e) {
-    const int d = a.d, n8 = d / 32;
-    const float4 *xr = reinterpret_cast<const float4 *>(a.x + (int64_t)t * d);
-    const float4 *wr = reinterpret_cast<const float4 *>(a.wrt + (int64_t)e * d);
-    const bool fma = e < (a.E & ~7);
-    float4 xa[8], wa[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        xa[i] = xr[i];
-        wa[i] = wr[i];
-    }
-    float acc = 0.0f;
-    for (int b = 0; b < n8; b++) {
-        float4 xb[8], wb[8];
-        const int nb = min(b + 1, n8 - 1);  // the last batch re-reads itself (unused)
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            xb[i] = xr[8 * nb + i];
-            wb[i] = wr[8 * nb + i];
-        }
-        if (fma) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) acc = step4<true>(xa[i], wa[i], acc);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; i++) acc = step4<false>(xa[i], wa[i], acc);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            xa[i] = xb[i];
-            wa[i] = wb[i];
-        }
-    }
-    return acc;
-}
-
-// ---- exact chains streamed through LDS, one wave at a time ----------------
-constexpr int kCh = 256;         // columns per streamed chunk
-constexpr int kChRow = kCh + 4;  // LDS row stride (floats): rows start on different banks
-
-// LDS floats for a wave streaming NR rows: two chunk buffers, plus the 16
-// floats chain16 prefetches past a row
-constexpr int stream_floats(int NR) { return 2 * NR * kChRow + 16; }
-
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-}
-
-// Exact reference chains (chain16's order) of up to 64 (token, expert)
-// pairs in one wave: lane l < NT*NE takes token t0 + l / NE and expert
-// e0 + l % NE (both clamped to the last valid index; callers drop those
-// lanes).  The NT x rows and NE router rows are streamed through this wave's
-// LDS region `lds` (stream_floats(NT + NE) floats) in chunks of kCh columns,
-// double-buffered: the wave loads chunk c+1 into registers while its lanes
-// run the chunk-c chains from LDS, then stores it.  LDS traffic stays inside
-// the wave, so only wave-level synchronisation is needed.
-template <int NT, int NE>
-__device__ float wave_chains(const RouterArgs &a, int t0, int e0, float *lds) {
-    constexpr int NR = NT + NE;
-    const int lane = threadIdx.x & 63, nch = a.d / kCh;
-    const int tb = min(lane / NE, NT - 1), eg = lane % NE;
-    const bool fma = min(e0 + eg, a.E - 1) < (a.E & ~7);
-    const float4 *src[NR];
-#pragma unroll
-    for (int r = 0; r < NR; r++) {
-        const float *row = r < NT ? a.x + (int64_t)min(t0 + r, a.T - 1) * a.d
-                                  : a.wrt + (int64_t)min(e0 + r - NT, a.E - 1) * a.d;
-        src[r] = reinterpret_cast<const float4 *>(row) + lane;
-    }
-    float4 v[NR];
-#pragma unroll
-    for (int r = 0; r < NR; r++) v[r] = src[r][0];
-#pragma unroll
-    for (int r = 0; r < NR; r++) reinterpret_cast<float4 *>(lds + r * kChRow)[lane] = v[r];
-    wave_lds_sync();
-    float acc = 0.0f;
-    for (int c = 0; c < nch; c++) {
-        const float *cur = lds + (c & 1) * NR * kChRow;
-        float *nxt = lds + ((c + 1) & 1) * NR * kChRow;
-        const bool more = c + 1 < nch;
-        if (more)
-#pragma unroll
-            for (int r = 0; r < NR; r++) v[r] = src[r][(c + 1) * (kCh / 4)];
-        const float4 *xr = reinterpret_cast<const float4 *>(cur + tb * kChRow);
-        const float4 *wr = reinterpret_cast<const float4 *>(cur + (NT + eg) * kChRow);
-        acc = fma ? chain16<true>(xr, wr, kCh / 4, acc) : chain16<false>(xr, wr, kCh / 4, acc);
-        if (more)
-#pragma unroll
-            for (int r = 0; r < NR; r++) reinterpret_cast<float4 *>(nxt + r * kChRow)[lane] = v[r];
-        wave_lds_sync();
-    }
-    return acc;
-}
-
-// The exact reference logits of all T x E (token, expert) pairs, for the
-// routing weights beside the certified fast router.  Off the critical path,
-// so it is shaped to hold few resources while the expert products run: one
-// wave per 8 tokens x 8 experts, 33 KB of LDS.
-__global__ __launch_bounds__(64) void k_exact_logits(RouterArgs a) {
-    __shared__ __attribute__((aligned(16))) float s[stream_floats(16)];
-    const int t0 = blockIdx.x * 8, e0 = blockIdx.y * 8, lane = threadIdx.x;
-    const float v = wave_chains<8, 8>(a, t0, e0, s);
-    const int t = t0 + lane / 8, e = e0 + lane % 8;
-    if (t < a.T && e < a.E) a.logits[(int64_t)t * a.E + e] = v;
-}
-
 // float64 logit S_d and chain error bound of every expert for token t; wave
 // w takes experts w, w+8, ...; lane l holds columns [l*C, l*C + C) with
 // C = 4*NC4 in registers.  sum_k |S_k| is bounded by groups of 4 columns:
@@ -729,7 +621,10 @@ __device__ __forceinline__ void logits_and_activations(const RouterArgs &a, int 
     logit_bounds<NC4>(a, R, s_a, s_b);
 }
 
-__global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a) {
+// grid (T [+ chain blocks]): block t routes token t; with ch.tiles, the
+// blocks past T run the first column range of the exact router chains
+// (wave 0, one tile at a time)
+__global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a, ChainArgs ch) {
     __shared__ double s_a[kMaxE], s_b[kMaxE];
     __shared__ float s_z[kMaxE], s_zlo[kMaxE], s_zhi[kMaxE], s_s[kMaxE], s_g[kMaxE];
     __shared__ unsigned char s_ok[kMaxE];
@@ -739,10 +634,20 @@ __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a) {
     __shared__ int s_flag;
     // x row for the logits (C <= 64 floats per lane), later the fallback's
     // chain stream (one token, 8 experts)
-    constexpr int kXFloats = 64 * (64 + 4), kFbFloats = stream_floats(1 + 8);
+    constexpr int kXFloats = 64 * (64 + 4), kFbFloats = chain_lds_floats(1 + 8, 256);
     __shared__ __attribute__((aligned(16))) float s_x[kXFloats > kFbFloats ? kXFloats : kFbFloats];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int t = blockIdx.x, d = a.d, E = a.E, K = a.K;
+    if (t >= a.T) {
+        if (wave == 0)
+            for (int tile = t - a.T; tile < ch.tiles; tile += gridDim.x - a.T) {
+                if (ch.nt == 1)
+                    chain_tile<1, 256, 1>(ch, tile, s_x);
+                else
+                    chain_tile<8, 128, 1>(ch, tile, s_x);
+            }
+        return;
+    }
 
     // bias into LDS while the logits run
     for (int e = tid; e < E; e += kFastThreads) s_g[e] = a.rp.has_bias ? a.bias[e] : 0.0f;
@@ -807,11 +712,11 @@ __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a) {
     }
     __syncthreads();
     if (!s_flag) {  // 3. fallback: exact chains, exact selection
-        if (wave == 0)
-            for (int e0 = 0; e0 < E; e0 += 8) {
-                const float v = wave_chains<1, 8>(a, t, e0, s_x);
-                if (lane < 8 && e0 + lane < E) a.logits[(int64_t)t * E + e0 + lane] = v;
-            }
+        if (wave == 0) {
+            const ChainArgs ca = make_chains(a.x, a.wrt, a.logits, nullptr, a.T, d, E, 0, d, 1);
+            const int ne = (E + 7) / 8;
+            for (int g = 0; g < ne; g++) chain_tile<1, 256, 1>(ca, t * ne + g, s_x);
+        }
         __threadfence_block();
         __syncthreads();
         if (wave == 0) {
@@ -825,7 +730,7 @@ __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a) {
     //    published with coherent stores and have completed)
     if (tid == 0) {
         const unsigned old = atomicAdd(&a.sync[0], 1u);
-        s_flag = (old == gridDim.x - 1);
+        s_flag = (old == (unsigned)a.T - 1);
     }
     __syncthreads();
     if (!s_flag) return;
@@ -876,11 +781,6 @@ hipError_t launch_router(const RouterArgs &a, int mode, hipStream_t st) {
 
 // softmax kinds, at most 64 experts, d = 64 * 4 * NC4 with NC4 in
 // {1, 2, 4, 8, 16}
-hipError_t launch_exact_logits(const RouterArgs &a, hipStream_t st) {
-    if (a.d % kCh) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_exact_logits, dim3((a.T + 7) / 8, (a.E + 7) / 8), dim3(64), 0, st, a);
-    return hipGetLastError();
-}
 
 bool route_fast_ok(const RouterArgs &a) {
     const int c4 = a.d / 256;
@@ -888,8 +788,15 @@ bool route_fast_ok(const RouterArgs &a) {
            (c4 == 1 || c4 == 2 || c4 == 4 || c4 == 8 || c4 == 16);
 }
 
-hipError_t launch_route_fast(const RouterArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL(k_route_fast, dim3(a.T), dim3(kFastThreads), 0, st, a);
+hipError_t launch_route_fast(const RouterArgs &a, const ChainArgs &ch, hipStream_t st) {
+    ChainArgs c = ch;
+    int cb = 0;
+    if (c.tiles) {
+        if (c.k0 % 256 || c.k1 % 256) return hipErrorInvalidValue;
+        c = with_nt(ch, ch.T == 1 ? 1 : 8);
+        cb = c.tiles < 64 ? c.tiles : 64;
+    }
+    hipLaunchKernelGGL(k_route_fast, dim3(a.T + cb), dim3(kFastThreads), 0, st, a, c);
     return hipGetLastError();
 }
 

@@ -220,16 +220,39 @@ __device__ __forceinline__ void gateup_chunk(const uint4 *G, const uint4 *U, int
     __syncthreads();
 }
 
+// Chain tiles of one wave (wave 0 of each chain block): one-token tiles run
+// two chunks of loads ahead, the shortest chains (T = 1) being the ones that
+// must finish inside the shortest gate/up launch.
+__device__ __forceinline__ void run_chains(const ChainArgs &ch, float *lds) {
+    static_assert(chain_lds_floats(9, 256) >= chain_lds_floats(16, 128), "chain LDS");
+    for (int tile = blockIdx.x; tile < ch.tiles; tile += gridDim.x) {
+        if (ch.nt == 1)
+            chain_tile<1, 256, 2>(ch, tile, lds);
+        else
+            chain_tile<8, 128, 1>(ch, tile, lds);
+    }
+}
+
+// grid (F/64 row tiles, [chain row +] slots)
 __global__ __launch_bounds__(256) void k_rpl_gateup(
     const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up, int64_t estride,
     const int8_t *__restrict__ xh, const int8_t *__restrict__ xl, const float *__restrict__ xs,
     const float *__restrict__ xm, SlotArgs sa, int d, int F, float *__restrict__ hf,
     int8_t *__restrict__ hh, int8_t *__restrict__ hl, float *__restrict__ hs,
-    float *__restrict__ hm) {
+    float *__restrict__ hm, ChainArgs ch) {
+    int slot = blockIdx.y;
+    if (ch.tiles) {  // row y = 0: exact router chains, one wave per block
+        if (slot == 0) {
+            __shared__ __attribute__((aligned(16))) float s_chain[chain_lds_floats(9, 256)];
+            if (threadIdx.x < 64) run_chains(ch, s_chain);
+            return;
+        }
+        slot -= 1;
+    }
     const Limbs X{xh, xl, xs, xm, d};
     const HOut out{hf, hh, hl, hs, hm};
     int e, p0, n;
-    if (!slot_info(sa, blockIdx.y, e, p0, n)) return;
+    if (!slot_info(sa, slot, e, p0, n)) return;
     e = __builtin_amdgcn_readfirstlane(e);
     p0 = __builtin_amdgcn_readfirstlane(p0);
     n = __builtin_amdgcn_readfirstlane(n);
@@ -315,10 +338,16 @@ __global__ __launch_bounds__(256) void k_rpl_down(
 hipError_t launch_rpl_gateup(const uint8_t *gate, const uint8_t *up, int64_t estride,
                              const int8_t *xh, const int8_t *xl, const float *xs, const float *xm,
                              const SlotArgsHost &sa, int slots, int d, int F, float *Hf, int8_t *hh,
-                             int8_t *hl, float *hs, float *hm, hipStream_t st) {
+                             int8_t *hl, float *hs, float *hm, const ChainArgs &ch,
+                             hipStream_t st) {
     SlotArgs s{sa.perm, sa.counts, sa.offsets, sa.touched, sa.E, sa.K, sa.T, sa.shared};
-    hipLaunchKernelGGL(k_rpl_gateup, dim3(F / 64, slots), dim3(256), 0, st, gate, up, estride, xh,
-                       xl, xs, xm, s, d, F, Hf, hh, hl, hs, hm);
+    ChainArgs c = ch;
+    if (c.tiles) {
+        if (c.k0 % 256 || c.k1 % 256) return hipErrorInvalidValue;
+        c = with_nt(ch, ch.T == 1 ? 1 : 8);
+    }
+    hipLaunchKernelGGL(k_rpl_gateup, dim3(F / 64, slots + (c.tiles ? 1 : 0)), dim3(256), 0, st,
+                       gate, up, estride, xh, xl, xs, xm, s, d, F, Hf, hh, hl, hs, hm, c);
     return hipGetLastError();
 }
 

@@ -6,6 +6,8 @@
 
 #include <cstdint>
 
+#include "chains.h"
+
 namespace lcmoe {
 
 struct RouteParams {
@@ -34,12 +36,11 @@ struct RouterArgs {
 // logits and the weights of the selection already in topk_idx.
 hipError_t launch_router(const RouterArgs &a, int mode, hipStream_t st);
 // Certified fast router for the softmax kinds: selection, dispatch, limbs
-// and f16 pieces; the weights come from the exact logits.
+// and f16 pieces.  The weights come from the exact logits: their chains run
+// in extra blocks of this launch (columns [0, ch.k1), none if ch.tiles == 0)
+// and of the routed gate/up launch (the rest).
 bool route_fast_ok(const RouterArgs &a);
-hipError_t launch_route_fast(const RouterArgs &a, hipStream_t st);
-// The exact reference logits of all T x E pairs into a.logits, one chain
-// per thread (reads a.x, a.wrt; nothing else).
-hipError_t launch_exact_logits(const RouterArgs &a, hipStream_t st);
+hipError_t launch_route_fast(const RouterArgs &a, const ChainArgs &ch, hipStream_t st);
 int router_token_groups(int T, int d, int E);
 
 struct SlotArgsHost {
@@ -49,10 +50,13 @@ struct SlotArgsHost {
 
 // Generic decode path on GGUF-layout tensors (any supported type, any
 // shape): f32 activations in, f32 H / Y out.
+// Every gate/up launch also runs the exact router chains `ch` (ch.tiles > 0)
+// in blocks that precede the expert blocks: grid row y = 0 holds them and
+// expert slot s is row s + 1.
 hipError_t launch_generic_gateup(int qt, const uint8_t *gate, const uint8_t *up, int64_t estride,
                                  const float *x, const SlotArgsHost &sa, int slots, int d, int F,
                                  float *Hf, int8_t *hh, int8_t *hl, float *hs, float *hm,
-                                 hipStream_t st);
+                                 const ChainArgs &ch, hipStream_t st);
 hipError_t launch_generic_down(int qt, const uint8_t *down, int64_t estride, const float *Hf,
                                const SlotArgsHost &sa, int slots, int d, int F, float *Y,
                                hipStream_t st);
@@ -62,7 +66,7 @@ hipError_t launch_generic_down(int qt, const uint8_t *down, int64_t estride, con
 hipError_t launch_rpl_gateup(const uint8_t *gate, const uint8_t *up, int64_t estride,
                              const int8_t *xh, const int8_t *xl, const float *xs, const float *xm,
                              const SlotArgsHost &sa, int slots, int d, int F, float *Hf, int8_t *hh,
-                             int8_t *hl, float *hs, float *hm, hipStream_t st);
+                             int8_t *hl, float *hs, float *hm, const ChainArgs &ch, hipStream_t st);
 hipError_t launch_rpl_down(const uint8_t *down, int64_t estride, const int8_t *hh,
                            const int8_t *hl, const float *hs, const float *hm,
                            const SlotArgsHost &sa, int slots, int d, int F, int ksplit, float *Y,
@@ -75,7 +79,7 @@ hipError_t launch_act16(const float *x, int T, int d, _Float16 *x16, _Float16 *x
 hipError_t launch_mfma_gateup(const uint8_t *gate, const uint8_t *up, int64_t estride,
                               const _Float16 *x16, const _Float16 *xs, const SlotArgsHost &sa,
                               int slots, int d, int F, _Float16 *h16, _Float16 *hs, float *hf,
-                              hipStream_t st);
+                              const ChainArgs &ch, hipStream_t st);
 hipError_t launch_mfma_down(const uint8_t *down, int64_t estride, const _Float16 *h16,
                             const _Float16 *hs, const SlotArgsHost &sa, int slots, int d, int F,
                             int ksplit, float *Y, int64_t split_stride, hipStream_t st);

@@ -29,9 +29,9 @@ using namespace lcmoe;
 namespace {
 
 enum Slot { kSlotRouter, kSlotPrep, kSlotGateUp, kSlotGateUpSh, kSlotDown, kSlotDownSh,
-            kSlotCombine, kSlotRouterExact, kNumSlots };
+            kSlotCombine, kNumSlots };
 const char *kSlotNames[kNumSlots] = {"router", "act16", "gateup", "gateup_shared", "down",
-                                     "down_shared", "combine", "router_exact"};
+                                     "down_shared", "combine"};
 constexpr int kMaxKSplit = 4;
 // matrix-core path when an expert family averages at least this many tokens
 constexpr int kMfmaMinTokens = 1;
@@ -59,10 +59,6 @@ struct lcmoe_handle {
     lcmoe_desc desc{};
     int device = 0;
     hipStream_t stream = nullptr;
-    // side stream for the exact router chains (routing weights) that run
-    // beside the expert products when the fast router certified the selection
-    hipStream_t side = nullptr;
-    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     std::vector<void *> allocs;
     float *wrt = nullptr, *bias = nullptr;
     // router in the fast router's lane-chunk order (null when d is not
@@ -71,6 +67,7 @@ struct lcmoe_handle {
     float *wlc = nullptr;
     ExpertSet routed, shared;
     float *x_dev = nullptr, *y_dev = nullptr, *logits = nullptr;
+    float *chain_part = nullptr;  // [max_tokens, E] router chain running sums
     int8_t *xh = nullptr, *xl = nullptr;
     float *xs = nullptr, *xm = nullptr;
     _Float16 *x16 = nullptr, *x16s = nullptr;
@@ -145,16 +142,12 @@ lcmoe_status upload_stack(lcmoe_handle *h, uint8_t **dst, const uint8_t *src, in
 void free_handle(lcmoe_handle *h) {
     if (!h) return;
     if (h->stream) (void)hipStreamSynchronize(h->stream);
-    if (h->side) (void)hipStreamSynchronize(h->side);
     for (auto &p : h->pending) {
         (void)hipEventDestroy(p.a);
         (void)hipEventDestroy(p.b);
     }
     for (auto ev : h->event_pool) (void)hipEventDestroy(ev);
     for (void *p : h->allocs) (void)hipFree(p);
-    if (h->ev_fork) (void)hipEventDestroy(h->ev_fork);
-    if (h->ev_join) (void)hipEventDestroy(h->ev_join);
-    if (h->side) (void)hipStreamDestroy(h->side);
     if (h->stream) (void)hipStreamDestroy(h->stream);
     delete h;
 }
@@ -261,12 +254,8 @@ extern "C" lcmoe_status lcmoe_create(const lcmoe_desc *desc, const lcmoe_weights
         return s;
     };
     if (hipGetDevice(&h->device) != hipSuccess) return bail(fail(LCMOE_ERR_HIP, "hipGetDevice failed"));
-    if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess ||
-        hipStreamCreateWithFlags(&h->side, hipStreamNonBlocking) != hipSuccess)
+    if (hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess)
         return bail(fail(LCMOE_ERR_HIP, "hipStreamCreate failed"));
-    if (hipEventCreateWithFlags(&h->ev_fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&h->ev_join, hipEventDisableTiming) != hipSuccess)
-        return bail(fail(LCMOE_ERR_HIP, "hipEventCreate failed"));
 
     const int64_t d = D.d_model, E = D.n_expert, K = D.n_expert_used, S = D.n_shared,
                   Tm = D.max_tokens, A = Tm * K;
@@ -306,6 +295,7 @@ extern "C" lcmoe_status lcmoe_create(const lcmoe_desc *desc, const lcmoe_weights
     if ((st = alloc_n(h, &h->x_dev, Tm * d))) return bail(st);
     if ((st = alloc_n(h, &h->y_dev, Tm * d))) return bail(st);
     if ((st = alloc_n(h, &h->logits, Tm * E))) return bail(st);
+    if ((st = alloc_n(h, &h->chain_part, Tm * E))) return bail(st);
     if (limbs) {
         if ((st = alloc_n(h, &h->xh, Tm * d))) return bail(st);
         if ((st = alloc_n(h, &h->xl, Tm * d))) return bail(st);
@@ -353,7 +343,7 @@ static Plan plan_set(lcmoe_handle *h, const ExpertSet &s, bool shared, int T) {
 }
 
 static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const float *x, int T,
-                            const Plan &pl, hipStream_t st) {
+                            const Plan &pl, const ChainArgs &ch, hipStream_t st) {
     const lcmoe_desc &D = h->desc;
     const int d = D.d_model, K = D.n_expert_used, E = D.n_expert;
     SlotArgsHost sa{h->perm, h->counts, h->offsets, h->touched, E, K, T, shared ? 1 : 0};
@@ -361,12 +351,12 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
         if (pl.mfma)
             return launch_mfma_gateup(s.gate, s.up, s.sz_gu, h->x16, h->x16s, sa, pl.slots, d,
                                       s.F, s.rpl_dn ? s.h16 : nullptr, s.h16s,
-                                      s.rpl_dn ? nullptr : s.Hf, st);
+                                      s.rpl_dn ? nullptr : s.Hf, ch, st);
         if (s.rpl_gu)
             return launch_rpl_gateup(s.gate, s.up, s.sz_gu, h->xh, h->xl, h->xs, h->xm, sa,
-                                     pl.slots, d, s.F, s.Hf, s.hh, s.hl, s.hs, s.hm, st);
+                                     pl.slots, d, s.F, s.Hf, s.hh, s.hl, s.hs, s.hm, ch, st);
         return launch_generic_gateup(s.qt_gu, s.gate, s.up, s.sz_gu, x, sa, pl.slots, d, s.F,
-                                     s.Hf, nullptr, nullptr, nullptr, nullptr, st);
+                                     s.Hf, nullptr, nullptr, nullptr, nullptr, ch, st);
     }));
     HIP_TRY(timed(h, st, shared ? kSlotDownSh : kSlotDown, [&] {
         if (s.rpl_dn && pl.mfma)
@@ -415,16 +405,21 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
     ra.touched = h->touched;
     ra.sync = h->sync;
     const bool fast = route_fast_ok(ra);
+    // With the certified fast router, selection, dispatch and activations
+    // come from it; the exact chains of the routing weights run in extra
+    // blocks beside them, and the combine turns the chains into weights.  The
+    // chains are sequential: columns [0, kA) run in the router launch, the
+    // rest in the routed gate/up launch, which outlasts them.  The
+    // row-per-lane and generic gate/up launches of small batches are short,
+    // so the router launch takes a share of the chains; the matrix-core one
+    // takes them all.
+    ChainArgs ch_r{}, ch_g{};
     if (fast) {
-        // the exact chains (for the routing weights only) start on the side
-        // stream at once; selection, dispatch and activations come from the
-        // certified fast router; the combine turns the chains into weights
-        HIP_TRY(hipEventRecord(h->ev_fork, st));
-        HIP_TRY(hipStreamWaitEvent(h->side, h->ev_fork, 0));
-        HIP_TRY(timed(h, h->side, kSlotRouterExact, [&] { return launch_exact_logits(ra, h->side); }));
-        HIP_TRY(hipEventRecord(h->ev_join, h->side));
+        const int kA = pr.mfma ? 0 : (T == 1 ? d / 2 : d / 4) & ~255;
+        if (kA > 0) ch_r = make_chains(x, h->wrt, h->logits, h->chain_part, T, d, E, 0, kA, 8);
+        ch_g = make_chains(x, h->wrt, h->logits, h->chain_part, T, d, E, kA, d, 8);
         ra.x16 = mfma ? h->x16 : nullptr;
-        HIP_TRY(timed(h, st, kSlotRouter, [&] { return launch_route_fast(ra, st); }));
+        HIP_TRY(timed(h, st, kSlotRouter, [&] { return launch_route_fast(ra, ch_r, st); }));
     } else {
         HIP_TRY(timed(h, st, kSlotRouter, [&] { return launch_router(ra, 0, st); }));
         if (mfma)
@@ -433,9 +428,8 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
             }));
     }
     lcmoe_status s;
-    if ((s = run_set(h, h->routed, false, x, T, pr, st))) return s;
-    if (S > 0 && (s = run_set(h, h->shared, true, x, T, ps, st))) return s;
-    if (fast) HIP_TRY(hipStreamWaitEvent(st, h->ev_join, 0));
+    if ((s = run_set(h, h->routed, false, x, T, pr, ch_g, st))) return s;
+    if (S > 0 && (s = run_set(h, h->shared, true, x, T, ps, ChainArgs{}, st))) return s;
     const int ks_r = pr.ks, ks_s = ps.ks;
     CombineRoute cr{};
     if (fast)
