@@ -57,6 +57,7 @@ __device__ __forceinline__ g_u8 *uniform(const void *p) {
 }
 
 constexpr int kWaves = 4;  // waves per block = 4 groups of 32 rows
+constexpr int kXcds = 8;   // MI355X: accelerator complex dies, one L2 each
 constexpr int kTok = 32;   // tokens per pass
 constexpr uint32_t kMagic = 0x64646464u;
 
@@ -632,18 +633,33 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down(
     const uint8_t *__restrict__ down, int64_t estride, const _Float16 *__restrict__ h16,
     const _Float16 *__restrict__ hs, SlotArgs sa, int d, int F, float *__restrict__ Y,
     int64_t split_stride) {
+    // Workgroups go to the 8 XCDs round-robin in dispatch order and each XCD
+    // has its own L2.  Every (slot, split) pair reads one slice of H, shared
+    // by its row blocks: remap the grid so that each XCD runs whole pairs and
+    // keeps only its pairs' slices (identity when the grid does not divide).
+    int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+    {
+        const int nx = gridDim.x, ny = gridDim.y, total = nx * ny * gridDim.z;
+        const int id = bx + nx * (by + ny * bz), per = total / kXcds;
+        if (total % kXcds == 0 && per % nx == 0) {
+            const int q = (id % kXcds) * per + id / kXcds, pair = q / nx;
+            bx = q % nx;
+            by = pair % ny;
+            bz = pair / ny;
+        }
+    }
     int e, p0, n;
-    if (!slot_info(sa, blockIdx.y, e, p0, n)) return;
+    if (!slot_info(sa, by, e, p0, n)) return;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
-    const int ntile = d >> 6, tile0 = blockIdx.x * kWaves + wave;
+    const int ntile = d >> 6, tile0 = bx * kWaves + wave;
     const int tile = min(tile0, ntile - 1);  // duplicate the last tile past the end
     const int NB = F >> 8, nsb = F >> 5;
-    const int kb0 = (int)((int64_t)NB * blockIdx.z / gridDim.z);
-    const int kb1 = (int)((int64_t)NB * (blockIdx.z + 1) / gridDim.z);
+    const int kb0 = (int)((int64_t)NB * bz / gridDim.z);
+    const int kb1 = (int)((int64_t)NB * (bz + 1) / gridDim.z);
     const uint8_t *tb = down + (int64_t)e * estride + (int64_t)tile * NB * 9 * 1024;
     g_u8 *const wb[2] = {uniform(tb), uniform(tb + 32 * 16)};
-    float *Yz = Y + (int64_t)blockIdx.z * split_stride;
+    float *Yz = Y + (int64_t)bz * split_stride;
     const uint8_t *hb = reinterpret_cast<const uint8_t *>(h16);
     const uint8_t *sb = reinterpret_cast<const uint8_t *>(hs);
     for (int c = 0; c < n; c += kTok) {
