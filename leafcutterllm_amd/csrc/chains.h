@@ -60,8 +60,12 @@ constexpr int chain_lds_floats(int NR, int CH) { return 2 * NR * (CH + 4) + 16; 
 
 namespace chain_detail {
 
+// native vector (HIP's float4 is a struct whose copies lower to memcpy
+// through scratch memory when held in arrays)
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 template <bool FMA>
-__device__ __forceinline__ float step4(float4 x, float4 w, float acc) {
+__device__ __forceinline__ float step4(f32x4 x, f32x4 w, float acc) {
     if (FMA) {
         acc = __builtin_fmaf(x.x, w.x, acc);
         acc = __builtin_fmaf(x.y, w.y, acc);
@@ -79,8 +83,8 @@ __device__ __forceinline__ float step4(float4 x, float4 w, float acc) {
 // ascending chain over n4 float4 of LDS rows xr, wr (n4 % 8 == 0); groups of
 // 4 float4 are read one group ahead, the last read lands past the rows
 template <bool FMA>
-__device__ __forceinline__ float chain_lds(const float4 *xr, const float4 *wr, int n4, float acc) {
-    float4 xa[4], wa[4], xb[4], wb[4];
+__device__ __forceinline__ float chain_lds(const f32x4 *xr, const f32x4 *wr, int n4, float acc) {
+    f32x4 xa[4], wa[4], xb[4], wb[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         xa[i] = xr[i];
@@ -132,23 +136,23 @@ __device__ void chain_tile(const ChainArgs &a, int tile, float *lds) {
     // streaming waves that share this SIMD
     __builtin_amdgcn_s_setprio(3);
     // this lane's share of every chunk: float4 j = i * 64 + lane -> (row, col4)
-    const float4 *src[NL];
+    const f32x4 *src[NL];
     int dst[NL];
 #pragma unroll
     for (int i = 0; i < NL; i++) {
         const int j = i * 64 + lane, r = j / F4, c4 = j % F4;
         const float *row = r < NT ? a.x + (int64_t)min(t0 + r, a.T - 1) * a.d
                                   : a.wrt + (int64_t)min(e0 + r - NT, a.E - 1) * a.d;
-        src[i] = reinterpret_cast<const float4 *>(row + a.k0) + c4;
+        src[i] = reinterpret_cast<const f32x4 *>(row + a.k0) + c4;
         dst[i] = r * ROW + 4 * c4;
     }
-    float4 v[DEPTH][NL];
+    f32x4 v[DEPTH][NL];
 #pragma unroll
     for (int s = 0; s < DEPTH; s++)
 #pragma unroll
         for (int i = 0; i < NL; i++) v[s][i] = src[i][min(s, nch - 1) * F4];
 #pragma unroll
-    for (int i = 0; i < NL; i++) *reinterpret_cast<float4 *>(lds + dst[i]) = v[0][i];
+    for (int i = 0; i < NL; i++) *reinterpret_cast<f32x4 *>(lds + dst[i]) = v[0][i];
 #pragma unroll
     for (int i = 0; i < NL; i++) v[0][i] = src[i][min(DEPTH, nch - 1) * F4];
     wave_lds_sync();
@@ -167,8 +171,8 @@ __device__ void chain_tile(const ChainArgs &a, int tile, float *lds) {
             if (c < nch) {
                 const float *cur = lds + (c & 1) * NR * ROW;
                 float *nxt = lds + ((c + 1) & 1) * NR * ROW;
-                const float4 *xr = reinterpret_cast<const float4 *>(cur + xoff);
-                const float4 *wr = reinterpret_cast<const float4 *>(cur + woff);
+                const f32x4 *xr = reinterpret_cast<const f32x4 *>(cur + xoff);
+                const f32x4 *wr = reinterpret_cast<const f32x4 *>(cur + woff);
                 acc = fma ? chain_lds<true>(xr, wr, F4, acc) : chain_lds<false>(xr, wr, F4, acc);
                 // chunk c + 1 is in slot (s + 1) % DEPTH: store it, refill the
                 // slot with chunk c + 1 + DEPTH (clamped, unused past the end)
@@ -176,7 +180,7 @@ __device__ void chain_tile(const ChainArgs &a, int tile, float *lds) {
                 if (c + 1 < nch) {
 #pragma unroll
                     for (int i = 0; i < NL; i++)
-                        *reinterpret_cast<float4 *>(nxt + dst[i]) = v[slot][i];
+                        *reinterpret_cast<f32x4 *>(nxt + dst[i]) = v[slot][i];
                 }
 #pragma unroll
                 for (int i = 0; i < NL; i++) v[slot][i] = src[i][min(c + 1 + DEPTH, nch - 1) * F4];

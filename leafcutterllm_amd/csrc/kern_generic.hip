@@ -33,7 +33,7 @@ __global__ __launch_bounds__(256) void k_gateup(const uint8_t *__restrict__ gate
             if (threadIdx.x < 64)
                 for (int tile = blockIdx.x; tile < ch.tiles; tile += gridDim.x) {
                     if (ch.nt == 1)
-                        chain_tile<1, 256, 2>(ch, tile, s_chain);
+                        chain_tile<1, 256, 1>(ch, tile, s_chain);
                     else
                         chain_tile<8, 128, 1>(ch, tile, s_chain);
                 }

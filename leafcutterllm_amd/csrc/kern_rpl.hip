@@ -227,7 +227,7 @@ __device__ __forceinline__ void run_chains(const ChainArgs &ch, float *lds) {
     static_assert(chain_lds_floats(9, 256) >= chain_lds_floats(16, 128), "chain LDS");
     for (int tile = blockIdx.x; tile < ch.tiles; tile += gridDim.x) {
         if (ch.nt == 1)
-            chain_tile<1, 256, 2>(ch, tile, lds);
+            chain_tile<1, 256, 1>(ch, tile, lds);
         else
             chain_tile<8, 128, 1>(ch, tile, lds);
     }
