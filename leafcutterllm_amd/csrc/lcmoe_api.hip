@@ -415,7 +415,7 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
     // takes them all.
     ChainArgs ch_r{}, ch_g{};
     if (fast) {
-        const int kA = pr.mfma ? 0 : (T == 1 ? d / 2 : d / 4) & ~255;
+        const int kA = pr.mfma ? 0 : (d / 4) & ~255;
         if (kA > 0) ch_r = make_chains(x, h->wrt, h->logits, h->chain_part, T, d, E, 0, kA, 8);
         ch_g = make_chains(x, h->wrt, h->logits, h->chain_part, T, d, E, kA, d, 8);
         ra.x16 = mfma ? h->x16 : nullptr;
