@@ -24,6 +24,10 @@
 namespace lcmoe {
 namespace {
 
+// native 4-float vector: HIP's float4 is a struct, and arrays of it held in
+// registers lower to memcpy through scratch memory
+using chain_detail::f32x4;
+
 constexpr int kThreads = 256;
 constexpr int kEG = 8;             // max experts per block
 constexpr int kPad = 4;            // LDS row padding (floats) against bank conflicts
@@ -231,20 +235,20 @@ __device__ __forceinline__ void stage_rows(const float *__restrict__ src, float 
                                            int d, int stride, int tid) {
     const int d4 = d / 4, n = rows * d4;
     for (int base = 0; base < n; base += 8 * kThreads) {
-        float4 v[8];
+        f32x4 v[8];
 #pragma unroll
         for (int i = 0; i < 8; i++)
-            v[i] = reinterpret_cast<const float4 *>(src)[min(base + tid + i * kThreads, n - 1)];
+            v[i] = reinterpret_cast<const f32x4 *>(src)[min(base + tid + i * kThreads, n - 1)];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const int q = base + tid + i * kThreads;
-            if (q < n) *reinterpret_cast<float4 *>(&dst[(q / d4) * stride + 4 * (q % d4)]) = v[i];
+            if (q < n) *reinterpret_cast<f32x4 *>(&dst[(q / d4) * stride + 4 * (q % d4)]) = v[i];
         }
     }
 }
 
 template <bool FMA>
-__device__ __forceinline__ float step4(float4 x, float4 w, float acc) {
+__device__ __forceinline__ float step4(f32x4 x, f32x4 w, float acc) {
     if (FMA) {
         acc = __builtin_fmaf(x.x, w.x, acc);
         acc = __builtin_fmaf(x.y, w.y, acc);
@@ -262,8 +266,8 @@ __device__ __forceinline__ float step4(float4 x, float4 w, float acc) {
 // Ascending-k chain over n4 float4 steps (n4 % 8 == 0), operands fetched in
 // groups of 4 float4 (16 k) one group ahead of use.
 template <bool FMA>
-__device__ __forceinline__ float chain16(const float4 *xr, const float4 *wr, int n4, float acc) {
-    float4 xa[4], wa[4], xb[4], wb[4];
+__device__ __forceinline__ float chain16(const f32x4 *xr, const f32x4 *wr, int n4, float acc) {
+    f32x4 xa[4], wa[4], xb[4], wb[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         xa[i] = xr[i];
@@ -352,8 +356,8 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB, int E
     const int ct = tid / EG, ce = tid % EG, e = e0 + ce;
     float acc = 0.0f;
     if (chain) {
-        const float4 *xr = reinterpret_cast<const float4 *>(&s_x[ct * stride]);
-        const float4 *wr = reinterpret_cast<const float4 *>(&s_w[ce * stride]);
+        const f32x4 *xr = reinterpret_cast<const f32x4 *>(&s_x[ct * stride]);
+        const f32x4 *wr = reinterpret_cast<const f32x4 *>(&s_w[ce * stride]);
         if (e < (E & ~7))
             acc = chain16<true>(xr, wr, d / 4, acc);
         else
@@ -461,13 +465,21 @@ constexpr int kFastThreads = 512;  // 8 waves: one expert per wave for E = 8
 // Activations of token t for the expert products: int8 limbs for the
 // row-per-lane kernels and f16 hi/lo pieces + sub-block sums for the
 // matrix-core kernels.  Four threads share a 32-column sub-block, eight
-// columns each, and meet through lane shuffles.
-__device__ void quantise_token(const RouterArgs &a, int t) {
+// columns each, and meet through lane shuffles.  The same reads stage the
+// token row into LDS for the logits: lane l's chunk of C = 4*NC4 columns is
+// row l of C + 4 floats, which keeps 8 consecutive lanes' b128 reads on
+// distinct banks.
+template <int NC4>
+__device__ void quantise_token(const RouterArgs &a, int t, float *s_x) {
+    constexpr int C = 4 * NC4;
     const int d = a.d, nsb = d / 32;
     for (int q = threadIdx.x; q < 4 * nsb; q += kFastThreads) {
         const int sb = q >> 2, part = q & 3, col0 = 32 * sb + 8 * part;
-        const float4 *v = reinterpret_cast<const float4 *>(a.x + (int64_t)t * d + col0);
-        const float4 v0 = v[0], v1 = v[1];
+        const f32x4 *v = reinterpret_cast<const f32x4 *>(a.x + (int64_t)t * d + col0);
+        const f32x4 v0 = v[0], v1 = v[1];
+        const int q4 = col0 / 4;
+        *reinterpret_cast<f32x4 *>(s_x + (q4 / NC4) * (C + 4) + 4 * (q4 % NC4)) = v0;
+        *reinterpret_cast<f32x4 *>(s_x + ((q4 + 1) / NC4) * (C + 4) + 4 * ((q4 + 1) % NC4)) = v1;
         const float f[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
         if (a.xh) {
             float amax = 0.0f;
@@ -532,31 +544,18 @@ __device__ void quantise_token(const RouterArgs &a, int t) {
 // before the group, so sum_k |S_k| <= 4 sum_g |S_g| + 4 sum_i |p_i|.
 template <int NC4>
 struct LogitRegs {
-    float4 wv[NC4];
+    f32x4 wv[NC4];
     const float *xs;  // this lane's token chunk in LDS
 };
 
 // this wave's first expert's router chunk, one coalesced KiB per load (the
 // lane-chunk order a.wlc)
 template <int NC4>
-__device__ __forceinline__ void load_wchunk(const RouterArgs &a, int e, float4 (&wv)[NC4]) {
+__device__ __forceinline__ void load_wchunk(const RouterArgs &a, int e, f32x4 (&wv)[NC4]) {
     const int lane = threadIdx.x & 63;
-    const float4 *wr = reinterpret_cast<const float4 *>(a.wlc) + (int64_t)e * NC4 * 64 + lane;
+    const f32x4 *wr = reinterpret_cast<const f32x4 *>(a.wlc) + (int64_t)e * NC4 * 64 + lane;
 #pragma unroll
     for (int i = 0; i < NC4; i++) wv[i] = wr[64 * i];
-}
-
-// token row into LDS (coalesced); lane l's chunk is row l of C + 4 floats,
-// which keeps 8 consecutive lanes' b128 reads on distinct banks
-template <int NC4>
-__device__ __forceinline__ const float *stage_xrow(const RouterArgs &a, int t, float *s_x) {
-    constexpr int C = 4 * NC4;
-    const int d = a.d, lane = threadIdx.x & 63;
-    const float4 *xr = reinterpret_cast<const float4 *>(a.x + (int64_t)t * d);
-    for (int q = threadIdx.x; q < d / 4; q += kFastThreads)
-        *reinterpret_cast<float4 *>(s_x + (q / NC4) * (C + 4) + 4 * (q % NC4)) = xr[q];
-    __syncthreads();
-    return s_x + lane * (C + 4);
 }
 
 template <int NC4>
@@ -570,7 +569,7 @@ __device__ __forceinline__ void logit_bounds(const RouterArgs &a, LogitRegs<NC4>
         double l2[2] = {0.0, 0.0}, ab2[2] = {0.0, 0.0};
 #pragma unroll
         for (int g = 0; g < NC4; g++) {  // products are exact in float64
-            const float4 x = *reinterpret_cast<const float4 *>(R.xs + 4 * g), w = R.wv[g];
+            const f32x4 x = *reinterpret_cast<const f32x4 *>(R.xs + 4 * g), w = R.wv[g];
             const double p0 = (double)x.x * (double)w.x, p1 = (double)x.y * (double)w.y;
             const double p2 = (double)x.z * (double)w.z, p3 = (double)x.w * (double)w.w;
             l2[g & 1] += (p0 + p1) + (p2 + p3);
@@ -587,7 +586,7 @@ __device__ __forceinline__ void logit_bounds(const RouterArgs &a, LogitRegs<NC4>
         double run = incl - loc, sg = 0.0;
 #pragma unroll
         for (int g = 0; g < NC4; g++) {  // group sums again, in order
-            const float4 x = *reinterpret_cast<const float4 *>(R.xs + 4 * g), w = R.wv[g];
+            const f32x4 x = *reinterpret_cast<const f32x4 *>(R.xs + 4 * g), w = R.wv[g];
             sg += fabs(run);
             run += ((double)x.x * (double)w.x + (double)x.y * (double)w.y) +
                    ((double)x.z * (double)w.z + (double)x.w * (double)w.w);
@@ -616,8 +615,9 @@ __device__ __forceinline__ void logits_and_activations(const RouterArgs &a, int 
                                                        double *s_a, double *s_b) {
     LogitRegs<NC4> R;
     load_wchunk<NC4>(a, min((int)(threadIdx.x >> 6), a.E - 1), R.wv);
-    quantise_token(a, t);  // while the router chunks load
-    R.xs = stage_xrow<NC4>(a, t, s_x);
+    quantise_token<NC4>(a, t, s_x);  // while the router chunks load
+    __syncthreads();
+    R.xs = s_x + (threadIdx.x & 63) * (4 * NC4 + 4);
     logit_bounds<NC4>(a, R, s_a, s_b);
 }
 
