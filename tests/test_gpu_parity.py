@@ -133,6 +133,40 @@ def test_adversarial_router_ties():
         moe.close()
 
 
+# d = 1024: the exact router chains are split by column between the router
+# launch and the gate/up launch on the row-per-lane path (T <= 3 here) and run
+# whole in the matrix-core gate/up launch (T >= 4)
+CHAIN_CFG = small_config("chains", 1024, 512, 8, 2, L.ROUTE_SOFTMAX_RENORM, Q4, Q4)
+
+
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 16, 40])
+def test_router_chain_split_parity(T):
+    layer = L.synth_layer(CHAIN_CFG, seed=21)
+    x = L.synth_x(CHAIN_CFG, T, seed=21, index=T)
+    res = run_and_check(CHAIN_CFG, layer, x)
+    assert res["rel_l2"] < 1e-3
+
+
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 16])
+def test_router_fallback_with_chain_split(T):
+    """Experts 0 and 1 share one router row, so their scores tie exactly and
+    the certified router cannot order them: every token that ranks them near
+    the top-k boundary takes the exact fallback (ties to the lower index),
+    while the column-split chains still produce the routing weights."""
+    layer = L.synth_layer(CHAIN_CFG, seed=22)
+    r = layer["router"].copy()
+    r[:, 1] = r[:, 0]
+    layer["router"] = r
+    x = L.synth_x(CHAIN_CFG, T, seed=22, index=T)
+    res = run_and_check(CHAIN_CFG, layer, x)
+    assert res["rel_l2"] < 1e-3
+    idx = res["topk_idx"].reshape(T, 2)
+    both = np.sum((idx == 0).any(axis=1) & (idx == 1).any(axis=1))
+    if both:  # a token holding both tied experts ranks 0 before 1
+        rows = (idx == 0).any(axis=1) & (idx == 1).any(axis=1)
+        assert np.all(np.argmax(idx[rows] == 0, axis=1) < np.argmax(idx[rows] == 1, axis=1))
+
+
 def test_e1_k1_reduces_to_dense_ffn():
     """E = 1, K = 1, renormalised: weight exactly 1.0 and the layer is the
     dense SwiGLU ffn_forward (engine.rs:146-164) of the one expert."""
@@ -154,7 +188,8 @@ def test_e1_k1_reduces_to_dense_ffn():
 
 # ------------------------------------------------- full BASELINE shapes -----
 
-FULL_T = [(1, 1), (1, 16), (2, 1), (2, 8), (2, 64), (5, 1), (5, 16)]
+FULL_T = [(1, 1), (1, 16), (2, 1), (2, 2), (2, 3), (2, 4), (2, 8), (2, 17), (2, 64), (5, 1),
+          (5, 16)]
 
 
 @pytest.fixture(scope="module")
