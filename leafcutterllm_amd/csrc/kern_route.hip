@@ -294,10 +294,8 @@ __device__ __forceinline__ float chain16(const f32x4 *xr, const f32x4 *wr, int n
     return acc;
 }
 
-// mode 0: exact logits, x limbs, top-k and dispatch (the whole router).
-// mode 1: exact logits and the routing weights of an already-made selection
-// (a.topk_idx), nothing else.
-__global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB, int EG, int mode) {
+// Exact logits, x limbs, top-k and dispatch (the whole router).
+__global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB, int EG) {
     extern __shared__ float smem[];
     const int d = a.d, E = a.E, stride = d + kPad;
     float *s_x = smem;                // [TB][d + pad]
@@ -319,7 +317,7 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB, int E
     __syncthreads();
 
     // x limbs for the integer decode path (expert group 0 only)
-    if (mode == 0 && eg == 0 && a.xh) {
+    if (eg == 0 && a.xh) {
         const int nsb = d / 32;
         for (int q = tid; q < nt * nsb; q += kThreads) {
             int t = q / nsb, sb = q % nsb;
@@ -377,31 +375,6 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB, int E
     if (!s_flag) return;
     __threadfence();
     const int wave = tid >> 6;
-    if (mode == 1) {
-        const int lane = tid & 63;
-        for (int t = t0 + wave; t < t0 + nt; t += kThreads / 64) {
-            const float *l = a.logits + (int64_t)t * E;
-            for (int e = lane; e < E; e += 64) {
-                const float v = l[e];
-                if (a.rp.kind == LCMOE_ROUTE_SIGMOID_GROUP) {
-                    const float sg = sigmoid_cw(v);
-                    s_s[wave][e] = sg;
-                    s_z[wave][e] = a.rp.has_bias ? sg + a.bias[e] : sg;
-                } else {
-                    s_z[wave][e] = a.rp.has_bias ? v + a.bias[e] : v;
-                }
-            }
-            if (lane < a.K) s_sel[wave][lane] = a.topk_idx[(int64_t)t * a.K + lane];
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            if (lane == 0) token_weights(a, t, s_z[wave], s_s[wave], s_sel[wave]);
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        }
-        __syncthreads();
-        if (tid == 0) a.sync[tg] = 0;
-        return;
-    }
     for (int t = wave; t < nt; t += kThreads / 64)
         select_token(a, t0 + t, s_z[wave], s_s[wave], s_g[wave], s_ok[wave], s_sel[wave]);
 
@@ -438,8 +411,8 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB, int E
 // k-th against every unselected expert), the reference chain selects exactly
 // those experts in that order, and the selection is final.  Otherwise the
 // block runs the exact chains for that token and selects from them.  The
-// routing weights need the chain values themselves: mode 2 of k_router
-// computes them on a second stream beside the expert products, and the
+// routing weights need the chain values themselves: extra blocks of this
+// launch and of the routed gate/up launch compute them (chains.h), and the
 // combine turns them into weights.
 // ---------------------------------------------------------------------------
 
@@ -762,7 +735,7 @@ int router_token_groups(int T, int d, int E) {
     return (T + TB - 1) / TB;
 }
 
-hipError_t launch_router(const RouterArgs &a, int mode, hipStream_t st) {
+hipError_t launch_router(const RouterArgs &a, hipStream_t st) {
     int TB, EG;
     block_shape(a.d, a.E, TB, EG);
     const int ntg = (a.T + TB - 1) / TB, neg = (a.E + EG - 1) / EG;
@@ -775,7 +748,7 @@ hipError_t launch_router(const RouterArgs &a, int mode, hipStream_t st) {
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL(k_router, dim3(ntg, neg), dim3(kThreads), lds, st, a, TB, EG, mode);
+    hipLaunchKernelGGL(k_router, dim3(ntg, neg), dim3(kThreads), lds, st, a, TB, EG);
     return hipGetLastError();
 }
 

@@ -32,9 +32,8 @@ struct RouterArgs {
     int32_t *counts, *offsets, *perm, *inv, *touched;
     uint32_t *sync;       // [n_token_groups + 1] zero-initialised counters
 };
-// mode 0: the exact router (logits, limbs, top-k, dispatch); mode 1: exact
-// logits and the weights of the selection already in topk_idx.
-hipError_t launch_router(const RouterArgs &a, int mode, hipStream_t st);
+// The exact router: logits, limbs, top-k, dispatch.
+hipError_t launch_router(const RouterArgs &a, hipStream_t st);
 // Certified fast router for the softmax kinds: selection, dispatch, limbs
 // and f16 pieces.  The weights come from the exact logits: their chains run
 // in extra blocks of this launch (columns [0, ch.k1), none if ch.tiles == 0)

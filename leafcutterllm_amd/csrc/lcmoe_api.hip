@@ -421,7 +421,7 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
         ra.x16 = mfma ? h->x16 : nullptr;
         HIP_TRY(timed(h, st, kSlotRouter, [&] { return launch_route_fast(ra, ch_r, st); }));
     } else {
-        HIP_TRY(timed(h, st, kSlotRouter, [&] { return launch_router(ra, 0, st); }));
+        HIP_TRY(timed(h, st, kSlotRouter, [&] { return launch_router(ra, st); }));
         if (mfma)
             HIP_TRY(timed(h, st, kSlotPrep, [&] {
                 return launch_act16(x, T, d, h->x16, h->x16s, st);
