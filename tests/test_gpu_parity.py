@@ -147,6 +147,19 @@ def test_router_chain_split_parity(T):
     assert res["rel_l2"] < 1e-3
 
 
+# E = 12: a partial second chain tile (experts 8..11 on the mul+add tail)
+CHAIN_CFG12 = small_config("chains12", 1024, 256, 12, 3, L.ROUTE_SOFTMAX, Q4, Q4, n_shared=1,
+                           d_ff_shared=256)
+
+
+@pytest.mark.parametrize("T", [1, 2, 9, 33])
+def test_router_chain_split_partial_tiles(T):
+    layer = L.synth_layer(CHAIN_CFG12, seed=23)
+    x = L.synth_x(CHAIN_CFG12, T, seed=23, index=T)
+    res = run_and_check(CHAIN_CFG12, layer, x)
+    assert res["rel_l2"] < 1e-3
+
+
 @pytest.mark.parametrize("T", [1, 2, 3, 4, 16])
 def test_router_fallback_with_chain_split(T):
     """Experts 0 and 1 share one router row, so their scores tie exactly and
