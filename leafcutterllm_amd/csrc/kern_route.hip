@@ -230,6 +230,30 @@ __device__ void dispatch_block(const RouterArgs &a, int (*s_cw)[kMaxE], int *s_o
     }
 }
 
+// The same dispatch for one token, from its selection in LDS (one thread):
+// its K assignments a = k sorted by expert (the experts are distinct).
+__device__ void dispatch_one(const RouterArgs &a, const int *sel) {
+    const int E = a.E, K = a.K;
+    int run = 0, nt = 0;
+    for (int e = 0; e < E; e++) {
+        int c = 0;
+        for (int k = 0; k < K; k++) c += sel[k] == e;
+        a.counts[e] = c;
+        a.offsets[e] = run;
+        if (c) {
+            for (int k = 0; k < K; k++)
+                if (sel[k] == e) {
+                    a.perm[run] = k;
+                    a.inv[k] = run;
+                    run++;
+                }
+            a.touched[nt++] = e;
+        }
+    }
+    a.offsets[E] = run;
+    a.touched[E] = nt;
+}
+
 // rows x d floats from global (row-major) into LDS rows of `stride` floats
 __device__ __forceinline__ void stage_rows(const float *__restrict__ src, float *dst, int rows,
                                            int d, int stride, int tid) {
@@ -679,8 +703,9 @@ __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a, Chain
         ok = __all(ok);
         if (lane == 0) s_flag = ok;
         if (ok && valid && rank < K) {
+            s_sel[rank] = e;
             store_agent(a.topk_idx + (int64_t)t * K + rank, e);
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            if (a.T > 1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
     }
     __syncthreads();
@@ -699,8 +724,14 @@ __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a, Chain
         __syncthreads();
     }
 
-    // 4. the last block to finish runs the dispatch (the selections were
-    //    published with coherent stores and have completed)
+    // 4. one token: this block holds the whole selection and dispatches it
+    //    from LDS (no publication wait, no counter)
+    if (a.T == 1) {
+        if (tid == 0) dispatch_one(a, s_sel);
+        return;
+    }
+    // the last block to finish runs the dispatch (the selections were
+    // published with coherent stores and have completed)
     if (tid == 0) {
         const unsigned old = atomicAdd(&a.sync[0], 1u);
         s_flag = (old == (unsigned)a.T - 1);
