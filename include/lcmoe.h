@@ -36,10 +36,13 @@ typedef enum {
     LCMOE_OK = 0,
     LCMOE_ERR_INVALID_ARG = 1,    /* null pointer, bad shape or size         */
     LCMOE_ERR_UNSUPPORTED = 2,    /* quant type / router kind not supported  */
-    LCMOE_ERR_CORRUPT = 3,        /* non-finite or absurd block scale        */
+    LCMOE_ERR_CORRUPT = 3,        /* non-finite or absurd block scale,
+                                     malformed or truncated GGUF file        */
     LCMOE_ERR_HIP = 4,            /* HIP runtime error (incl. no device)     */
     LCMOE_ERR_OUT_OF_MEMORY = 5,  /* device allocation failed                */
-    LCMOE_ERR_STATE = 6           /* e.g. query before any forward           */
+    LCMOE_ERR_STATE = 6,          /* e.g. query before any forward           */
+    LCMOE_ERR_NOT_FOUND = 7,      /* GGUF tensor or metadata key absent      */
+    LCMOE_ERR_IO = 8              /* file cannot be opened or mapped         */
 } lcmoe_status;
 
 /* GGUF ggml_type codes, QuantType::code, rust/src/model/quant.rs:45-73. */
@@ -162,6 +165,63 @@ lcmoe_status lcmoe_quantize(int32_t type, const float *src, uint8_t *dst, int64_
 /* Synthetic N(0, stddev^2) data: counter-based splitmix64 + Box-Muller in
  * float64; element i depends only on (seed, stream, i). */
 void lcmoe_synth_normal(uint64_t seed, uint64_t stream, float stddev, float *out, int64_t n);
+
+/* ---- GGUF ingest (host only, no GPU needed) --------------------------- */
+
+/* A GGUF v3 file, memory-mapped read-only and parsed, as GGUFile::open does
+ * (rust/src/model/gguf.rs:76-119): header, metadata, tensor infos, data
+ * section at general.alignment (default 32).  Unlike the reference, every
+ * tensor of known type is checked to lie inside the file at open
+ * (LCMOE_ERR_CORRUPT otherwise); version != 3 is LCMOE_ERR_UNSUPPORTED, as
+ * GGUError::UnsupportedVersion.  One caller at a time per handle. */
+typedef struct lcmoe_gguf lcmoe_gguf;
+
+lcmoe_status lcmoe_gguf_open(const char *path, lcmoe_gguf **out);
+/* Unmaps the file; every pointer obtained from the handle dies with it. */
+void lcmoe_gguf_close(lcmoe_gguf *g);
+
+/* GGUFile::get_metadata_int (gguf.rs:133-157): any integer or float value
+ * (floats truncated), or a one-element U32/I32/U64/I64 array.
+ * LCMOE_ERR_NOT_FOUND if absent, LCMOE_ERR_INVALID_ARG if of another type. */
+lcmoe_status lcmoe_gguf_meta_int(const lcmoe_gguf *g, const char *key, int64_t *out);
+/* A string value (bytes as stored, NUL-terminated), NULL if absent or not a
+ * string.  Valid until lcmoe_gguf_close. */
+const char *lcmoe_gguf_meta_str(const lcmoe_gguf *g, const char *key);
+
+/* GGUFile::get_tensor_info + get_tensor_raw (gguf.rs:121-131): the first
+ * tensor of that name.  dims[4] lists ne0 (fastest) first, 1-padded; data /
+ * bytes are NULL / 0 for a GGUF type whose block size this library does not
+ * know.  Any output pointer may be NULL. */
+lcmoe_status lcmoe_gguf_tensor(const lcmoe_gguf *g, const char *name, int32_t *type,
+                               int32_t *n_dims, int64_t *dims, const uint8_t **data,
+                               uint64_t *bytes);
+
+/* <general.architecture>.block_count, else 1 + the largest N of the blk.N.*
+ * tensor names (0 if none); -1 for g == NULL. */
+int32_t lcmoe_gguf_block_count(const lcmoe_gguf *g);
+/* 1 if blk.<layer>.ffn_gate_inp.weight exists, else 0. */
+int32_t lcmoe_gguf_is_moe_layer(const lcmoe_gguf *g, int32_t layer);
+
+/* Descriptor and weights of MoE layer `layer`, ready for lcmoe_create: the
+ * MoE counterpart of load_layer (rust/src/model/loader.rs:145-168), whose
+ * architecture table maps dense FFN tensors only
+ * (rust/src/model/arch.rs:83-96).  Reads blk.<layer>.ffn_gate_inp.weight
+ * (router, F32/F16/BF16, transposed into the [d, E] form lcmoe_weights
+ * takes), the stacked ffn_{gate,up,down}_exps.weight tensors (or per-expert
+ * ffn_{gate,up,down}.<e>.weight), optional ffn_{gate,up,down}_shexp.weight
+ * (2D: one shared expert; 3D: dims[2] of them), optional exp_probs_b.bias
+ * (sigmoid gating) or ffn_gate_inp.bias (softmax gating), and the metadata
+ * <arch>.expert_used_count (required), expert_gating_func,
+ * expert_weights_norm, expert_weights_scale, expert_group_count and
+ * expert_group_used_count; shapes are cross-checked against expert_count,
+ * embedding_length and expert_feed_forward_length where present.  The
+ * descriptor is validated as lcmoe_create would.  Expert pointers point into
+ * the mapping (stacked form) or into copies the handle owns; router and bias
+ * are handle-owned f32 copies.  They stay valid until lcmoe_gguf_close or
+ * the next call for the same layer.  Unsupported layouts (a gated shared
+ * expert, ffn_gate_inp_shexp) return LCMOE_ERR_UNSUPPORTED. */
+lcmoe_status lcmoe_gguf_moe_layer(lcmoe_gguf *g, int32_t layer, int32_t max_tokens,
+                                  lcmoe_desc *desc, lcmoe_weights *w);
 
 /* ---- device self-tests (need a GPU; used by the parity tests) ---------- */
 

@@ -18,7 +18,7 @@ ROUTE_SOFTMAX_RENORM, ROUTE_SOFTMAX, ROUTE_SIGMOID_GROUP = 0, 1, 2
 STATUS = {
     0: "LCMOE_OK", 1: "LCMOE_ERR_INVALID_ARG", 2: "LCMOE_ERR_UNSUPPORTED",
     3: "LCMOE_ERR_CORRUPT", 4: "LCMOE_ERR_HIP", 5: "LCMOE_ERR_OUT_OF_MEMORY",
-    6: "LCMOE_ERR_STATE",
+    6: "LCMOE_ERR_STATE", 7: "LCMOE_ERR_NOT_FOUND", 8: "LCMOE_ERR_IO",
 }
 
 # every symbol include/lcmoe.h declares
@@ -27,6 +27,9 @@ EXPORTS = (
     "lcmoe_get_dispatch", "lcmoe_set_timing", "lcmoe_get_timing", "lcmoe_timing_name",
     "lcmoe_timing_slots", "lcmoe_last_error", "lcmoe_tensor_size", "lcmoe_scan_blocks",
     "lcmoe_quantize", "lcmoe_synth_normal", "lcmoe_debug_dequant", "lcmoe_debug_sigmoid",
+    "lcmoe_gguf_open", "lcmoe_gguf_close", "lcmoe_gguf_meta_int", "lcmoe_gguf_meta_str",
+    "lcmoe_gguf_tensor", "lcmoe_gguf_block_count", "lcmoe_gguf_is_moe_layer",
+    "lcmoe_gguf_moe_layer",
 )
 
 
@@ -93,6 +96,14 @@ def lib() -> C.CDLL:
         "lcmoe_synth_normal": (None, [u64, u64, f32, vp, i64]),
         "lcmoe_debug_dequant": (i32, [i32, vp, i64, vp]),
         "lcmoe_debug_sigmoid": (i32, [vp, i64, vp]),
+        "lcmoe_gguf_open": (i32, [C.c_char_p, P(vp)]),
+        "lcmoe_gguf_close": (None, [vp]),
+        "lcmoe_gguf_meta_int": (i32, [vp, C.c_char_p, P(i64)]),
+        "lcmoe_gguf_meta_str": (C.c_char_p, [vp, C.c_char_p]),
+        "lcmoe_gguf_tensor": (i32, [vp, C.c_char_p, P(i32), P(i32), P(i64), P(vp), P(u64)]),
+        "lcmoe_gguf_block_count": (i32, [vp]),
+        "lcmoe_gguf_is_moe_layer": (i32, [vp, i32]),
+        "lcmoe_gguf_moe_layer": (i32, [vp, i32, i32, P(Desc), P(Weights)]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)

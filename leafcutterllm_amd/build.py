@@ -1,7 +1,7 @@
 """Build recipe for the product library leafcutterllm_amd/liblcmoe.so.
 
-hipcc compiles the HIP translation unit for gfx950 only; g++ compiles the
-host-only utilities.  Every build compiles from source (no caching), so a
+hipcc compiles the HIP translation units for gfx950 only; g++ compiles the
+host-only sources (utilities and the GGUF reader).  Every build compiles from source (no caching), so a
 call always reflects the current sources.
 """
 from __future__ import annotations
@@ -46,11 +46,14 @@ def build(verbose: bool = False) -> str:
             o = os.path.join(BUILD, src[:-4] + ".o")
             _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", o], verbose)
             objs.append(o)
-    host_o = os.path.join(BUILD, "lcmoe_host.o")
-    _run(["g++", *HOST_FLAGS, "-c", os.path.join(CSRC, "lcmoe_host.cpp"), "-o", host_o], verbose)
+    for src in sorted(os.listdir(CSRC)):
+        if src.endswith(".cpp"):
+            o = os.path.join(BUILD, src[:-4] + ".o")
+            _run(["g++", *HOST_FLAGS, "-c", os.path.join(CSRC, src), "-o", o], verbose)
+            objs.append(o)
     tmp = LIB + ".tmp"
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-pthread", *objs, host_o,
-          "-o", tmp], verbose)
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-pthread", *objs, "-o", tmp],
+         verbose)
     shutil.move(tmp, LIB)
     return LIB
 

@@ -39,9 +39,30 @@ class MoeFfn:
                 a = np.ascontiguousarray(a, np.uint8)
                 keep.append(a)
             setattr(w, k, _ptr(a))
+        self._create(desc, w)
+
+    def _create(self, desc: Desc, w: Weights) -> None:
         h = C.c_void_p()
         check(lib().lcmoe_create(C.byref(desc), C.byref(w), C.byref(h)), "lcmoe_create")
         self._h = h
+
+    @classmethod
+    def from_gguf(cls, source, layer: int, max_tokens: int) -> "MoeFfn":
+        """MoE layer `layer` of a GGUF file (a path or an open GgufFile),
+        uploaded resident: GgufFile.moe_layer then lcmoe_create, which copies
+        the weights, so the file may be closed afterwards."""
+        from .gguf import GgufFile
+
+        f = source if isinstance(source, GgufFile) else GgufFile(source)
+        try:
+            desc, w = f.moe_layer(layer, max_tokens)
+            self = cls.__new__(cls)
+            self.desc = desc
+            self._create(desc, w)
+            return self
+        finally:
+            if f is not source:
+                f.close()
 
     @property
     def handle(self) -> int:
