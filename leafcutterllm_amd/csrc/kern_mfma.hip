@@ -505,9 +505,9 @@ __device__ __forceinline__ int c_token(int i, int h) { return 8 * (i >> 2) + 4 *
 // of one activation stage.
 static_assert(kStageBytes / 8 >= chain_lds_floats(16, 128), "chain tile LDS");
 
-// grid (F/128 row blocks, [chain row +] slots); block = 4 waves x 32 weight
-// rows.  With ch.tiles, row y = 0 runs the exact router chains (a wave per
-// 8 x 8 tile) and slot s is row s + 1.
+// grid (F/128 row blocks, [chain row +] slots, pass groups); block = 4 waves
+// x 32 weight rows.  With ch.tiles, row y = 0 runs the exact router chains
+// (a wave per 8 x 8 tile, blocks of z = 0) and slot s is row s + 1.
 __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
     const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up, int64_t estride,
     const _Float16 *__restrict__ x16, const _Float16 *__restrict__ xs, SlotArgs sa, int d, int F,
@@ -515,6 +515,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
     int slot = blockIdx.y;
     if (ch.tiles) {
         if (slot == 0) {
+            if (blockIdx.z) return;
             const int cw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
             float *lds = reinterpret_cast<float *>(cw < 2 ? s_stage0 : s_stage1) +
                          (cw & 1) * (kStageBytes / 8);
@@ -537,7 +538,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
     const int f = grp * 32 + r, nkb = F >> 8;
     const uint8_t *xb = reinterpret_cast<const uint8_t *>(x16);
     const uint8_t *sb = reinterpret_cast<const uint8_t *>(xs);
-    for (int c = 0; c < n; c += kTok) {
+    for (int c = blockIdx.z * kTok; c < n; c += gridDim.z * kTok) {
         StageSrc src;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -625,13 +626,14 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
     }
 }
 
-// grid (d/256 row blocks, slots, ksplit); partial sums of K slice z go to
-// Y + z * split_stride.  A wave owns one 64-row RPL tile as two 32-row halves
-// that share every activation read (the two "matrices" of the pipeline), so
-// each LDS read feeds twice the weight bytes of a 32-row wave.
+// grid (d/256 row blocks, slots, ksplit x pass groups); z = split + ksplit *
+// group.  Partial sums of K split z go to Y + z * split_stride.  A wave owns
+// one 64-row RPL tile as two 32-row halves that share every activation read
+// (the two "matrices" of the pipeline), so each LDS read feeds twice the
+// weight bytes of a 32-row wave.
 __global__ __launch_bounds__(256, 2) void k_mfma_down(
     const uint8_t *__restrict__ down, int64_t estride, const _Float16 *__restrict__ h16,
-    const _Float16 *__restrict__ hs, SlotArgs sa, int d, int F, float *__restrict__ Y,
+    const _Float16 *__restrict__ hs, SlotArgs sa, int d, int F, int ksplit, float *__restrict__ Y,
     int64_t split_stride) {
     // Workgroups go to the 8 XCDs round-robin in dispatch order and each XCD
     // has its own L2.  Every (slot, split) pair reads one slice of H, shared
@@ -648,6 +650,8 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down(
             bz = pair / ny;
         }
     }
+    const int cz = bz / ksplit, nz = gridDim.z / ksplit;  // pass group
+    bz -= cz * ksplit;                                     // K split
     int e, p0, n;
     if (!slot_info(sa, by, e, p0, n)) return;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -655,14 +659,14 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down(
     const int ntile = d >> 6, tile0 = bx * kWaves + wave;
     const int tile = min(tile0, ntile - 1);  // duplicate the last tile past the end
     const int NB = F >> 8, nsb = F >> 5;
-    const int kb0 = (int)((int64_t)NB * bz / gridDim.z);
-    const int kb1 = (int)((int64_t)NB * (bz + 1) / gridDim.z);
+    const int kb0 = (int)((int64_t)NB * bz / ksplit);
+    const int kb1 = (int)((int64_t)NB * (bz + 1) / ksplit);
     const uint8_t *tb = down + (int64_t)e * estride + (int64_t)tile * NB * 9 * 1024;
     g_u8 *const wb[2] = {uniform(tb), uniform(tb + 32 * 16)};
     float *Yz = Y + (int64_t)bz * split_stride;
     const uint8_t *hb = reinterpret_cast<const uint8_t *>(h16);
     const uint8_t *sb = reinterpret_cast<const uint8_t *>(hs);
-    for (int c = 0; c < n; c += kTok) {
+    for (int c = cz * kTok; c < n; c += nz * kTok) {
         StageSrc src;
 #pragma unroll
         for (int i = 0; i < 8; i++)
@@ -759,26 +763,31 @@ hipError_t launch_act16(const float *x, int T, int d, _Float16 *x16, _Float16 *x
 
 hipError_t launch_mfma_gateup(const uint8_t *gate, const uint8_t *up, int64_t estride,
                               const _Float16 *x16, const _Float16 *xs, const SlotArgsHost &sa,
-                              int slots, int d, int F, _Float16 *h16, _Float16 *hs, float *hf,
-                              const ChainArgs &ch, hipStream_t st) {
+                              int slots, int chunks, int d, int F, _Float16 *h16, _Float16 *hs,
+                              float *hf, const ChainArgs &ch, hipStream_t st) {
     const int groups = F / 32;
     ChainArgs c = ch;
     if (c.tiles) {
         if (c.k0 % 256 || c.k1 % 256) return hipErrorInvalidValue;
         c = with_nt(ch, 8);
     }
-    hipLaunchKernelGGL(k_mfma_gateup, dim3((groups + kWaves - 1) / kWaves, slots + (c.tiles ? 1 : 0)),
+    if (chunks < 1 || chunks > 65535) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_mfma_gateup,
+                       dim3((groups + kWaves - 1) / kWaves, slots + (c.tiles ? 1 : 0), chunks),
                        dim3(256), 0, st, gate, up, estride, x16, xs, dev_slots(sa), d, F, h16, hs,
                        hf, c);
     return hipGetLastError();
 }
 
 hipError_t launch_mfma_down(const uint8_t *down, int64_t estride, const _Float16 *h16,
-                            const _Float16 *hs, const SlotArgsHost &sa, int slots, int d, int F,
-                            int ksplit, float *Y, int64_t split_stride, hipStream_t st) {
+                            const _Float16 *hs, const SlotArgsHost &sa, int slots, int chunks,
+                            int d, int F, int ksplit, float *Y, int64_t split_stride,
+                            hipStream_t st) {
     const int tiles = d / 64;
-    hipLaunchKernelGGL(k_mfma_down, dim3((tiles + kWaves - 1) / kWaves, slots, ksplit), dim3(256),
-                       0, st, down, estride, h16, hs, dev_slots(sa), d, F, Y, split_stride);
+    if (chunks < 1 || ksplit < 1 || (int64_t)chunks * ksplit > 65535) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_mfma_down, dim3((tiles + kWaves - 1) / kWaves, slots, ksplit * chunks),
+                       dim3(256), 0, st, down, estride, h16, hs, dev_slots(sa), d, F, ksplit, Y,
+                       split_stride);
     return hipGetLastError();
 }
 

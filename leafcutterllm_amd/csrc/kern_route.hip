@@ -169,11 +169,45 @@ __device__ void select_token(const RouterArgs &a, int t, float *s_z, float *s_s,
     }
 }
 
+// Exclusive scan of s_off[0..E) (per-expert counts) into offsets by one
+// wave, writing offsets[0..E], touched[] and s_off[E] = total.
+__device__ void scan_experts(const RouterArgs &a, int *s_off) {
+    const int lane = threadIdx.x & 63, E = a.E;
+    int run = 0, nt = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+        const int e = e0 + lane;
+        const int c = e < E ? s_off[e] : 0;
+        int incl = c;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int v = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += v;
+        }
+        const uint64_t m = __ballot(c > 0);
+        if (e < E) {
+            s_off[e] = run + incl - c;
+            a.offsets[e] = run + incl - c;
+        }
+        if (c > 0) a.touched[nt + __popcll(m & ((1ull << lane) - 1ull))] = e;
+        run += __shfl(incl, 63, 64);
+        nt += __popcll(m);
+    }
+    if (lane == 0) {
+        s_off[E] = run;
+        a.offsets[E] = run;
+        a.touched[E] = nt;
+    }
+}
+
 // Stable counting sort of the A = T*K assignments a = t*K + k by expert, by
-// the 4 waves of one block.  Each wave owns a contiguous chunk: pass 1 counts
-// per (wave, expert), prefixes over waves and experts give each wave its base
-// per expert, pass 2 ranks equal experts inside each 64-assignment group with
-// ballots (lower lane = lower a) and advances the wave's private counters.
+// the NT/64 waves of one block.  Each wave owns a contiguous chunk: pass 1
+// counts per (wave, expert), prefixes over waves and experts give each wave
+// its base per expert, pass 2 ranks equal experts inside each 64-assignment
+// group with ballots (lower lane = lower a) and advances the wave's private
+// counters.  The selections are read with device-coherent loads, kDispBatch
+// groups in flight per lane.
+constexpr int kDispBatch = 8;
+
 template <int NT>
 __device__ void dispatch_block(const RouterArgs &a, int (*s_cw)[kMaxE], int *s_off) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -183,7 +217,17 @@ __device__ void dispatch_block(const RouterArgs &a, int (*s_cw)[kMaxE], int *s_o
     __syncthreads();
     const int chunk = (((A + W - 1) / W) + 63) & ~63;
     const int a0 = min(A, wave * chunk), a1 = min(A, a0 + chunk);
-    for (int q = a0 + lane; q < a1; q += 64) atomicAdd(&s_cw[wave][load_agent(a.topk_idx + q)], 1);
+    for (int base = a0; base < a1; base += 64 * kDispBatch) {
+        int ev[kDispBatch];
+#pragma unroll
+        for (int j = 0; j < kDispBatch; j++) {
+            const int q = base + 64 * j + lane;
+            ev[j] = q < a1 ? load_agent(a.topk_idx + q) : -1;
+        }
+#pragma unroll
+        for (int j = 0; j < kDispBatch; j++)
+            if (ev[j] >= 0) atomicAdd(&s_cw[wave][ev[j]], 1);
+    }
     __syncthreads();
     if (tid < E) {
         int run = 0;
@@ -196,62 +240,69 @@ __device__ void dispatch_block(const RouterArgs &a, int (*s_cw)[kMaxE], int *s_o
         s_off[tid] = run;
     }
     __syncthreads();
-    if (tid == 0) {
-        int run = 0, nt = 0;
-        for (int e = 0; e < E; e++) {
-            int c = s_off[e];
-            s_off[e] = run;
-            a.offsets[e] = run;
-            run += c;
-            if (c) a.touched[nt++] = e;
-        }
-        s_off[E] = run;
-        a.offsets[E] = run;
-        a.touched[E] = nt;
-    }
+    if (wave == 0) scan_experts(a, s_off);
     __syncthreads();
-    for (int base = a0; base < a1; base += 64) {
-        const int q = base + lane;
-        const bool valid = q < a1;
-        const int e = valid ? load_agent(a.topk_idx + q) : 0;
-        uint64_t mask = __ballot(valid);
+    for (int base = a0; base < a1; base += 64 * kDispBatch) {
+        int ev[kDispBatch];
 #pragma unroll
-        for (int b = 0; b < 8; b++) {
-            uint64_t bb = __ballot(valid && ((e >> b) & 1));
-            mask &= ((e >> b) & 1) ? bb : ~bb;
+        for (int j = 0; j < kDispBatch; j++) {
+            const int q = base + 64 * j + lane;
+            ev[j] = q < a1 ? load_agent(a.topk_idx + q) : 0;
         }
-        if (valid) {
-            const int rank = __popcll(mask & ((1ull << lane) - 1ull));
-            const int pos = s_off[e] + s_cw[wave][e] + rank;
-            a.perm[pos] = q;
-            a.inv[q] = pos;
-            if (rank == 0) s_cw[wave][e] += __popcll(mask);
+#pragma unroll
+        for (int j = 0; j < kDispBatch; j++) {
+            const int q = base + 64 * j + lane;
+            const bool valid = q < a1;
+            const int e = ev[j];
+            uint64_t mask = __ballot(valid);
+#pragma unroll
+            for (int b = 0; b < 8; b++) {
+                uint64_t bb = __ballot(valid && ((e >> b) & 1));
+                mask &= ((e >> b) & 1) ? bb : ~bb;
+            }
+            if (valid) {
+                const int rank = __popcll(mask & ((1ull << lane) - 1ull));
+                const int pos = s_off[e] + s_cw[wave][e] + rank;
+                a.perm[pos] = q;
+                a.inv[q] = pos;
+                if (rank == 0) s_cw[wave][e] += __popcll(mask);
+            }
         }
     }
 }
 
-// The same dispatch for one token, from its selection in LDS (one thread):
-// its K assignments a = k sorted by expert (the experts are distinct).
+// The same dispatch for one token, by one wave, from its selection sel[0..K)
+// in LDS: its K assignments a = k sorted by expert (the experts are distinct).
 __device__ void dispatch_one(const RouterArgs &a, const int *sel) {
-    const int E = a.E, K = a.K;
-    int run = 0, nt = 0;
-    for (int e = 0; e < E; e++) {
-        int c = 0;
-        for (int k = 0; k < K; k++) c += sel[k] == e;
-        a.counts[e] = c;
-        a.offsets[e] = run;
-        if (c) {
-            for (int k = 0; k < K; k++)
-                if (sel[k] == e) {
-                    a.perm[run] = k;
-                    a.inv[k] = run;
-                    run++;
-                }
-            a.touched[nt++] = e;
+    const int lane = threadIdx.x & 63, E = a.E, K = a.K;
+    int sk[kMaxK];
+#pragma unroll
+    for (int k = 0; k < kMaxK; k++) sk[k] = k < K ? sel[k] : -1;
+    int run = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+        const int e = e0 + lane;
+        int kpos = -1;
+#pragma unroll
+        for (int k = 0; k < kMaxK; k++)
+            if (sk[k] == e) kpos = k;
+        const bool hit = kpos >= 0 && e < E;
+        const uint64_t m = __ballot(hit);
+        const int pos = run + __popcll(m & ((1ull << lane) - 1ull));
+        if (e < E) {
+            a.counts[e] = hit ? 1 : 0;
+            a.offsets[e] = pos;
         }
+        if (hit) {
+            a.perm[pos] = kpos;
+            a.inv[kpos] = pos;
+            a.touched[pos] = e;
+        }
+        run += __popcll(m);
     }
-    a.offsets[E] = run;
-    a.touched[E] = nt;
+    if (lane == 0) {
+        a.offsets[E] = run;
+        a.touched[E] = run;
+    }
 }
 
 // rows x d floats from global (row-major) into LDS rows of `stride` floats
@@ -462,21 +513,24 @@ constexpr int kFastThreads = 512;  // 8 waves: one expert per wave for E = 8
 // Activations of token t for the expert products: int8 limbs for the
 // row-per-lane kernels and f16 hi/lo pieces + sub-block sums for the
 // matrix-core kernels.  Four threads share a 32-column sub-block, eight
-// columns each, and meet through lane shuffles.  The same reads stage the
-// token row into LDS for the logits: lane l's chunk of C = 4*NC4 columns is
-// row l of C + 4 floats, which keeps 8 consecutive lanes' b128 reads on
-// distinct banks.
-template <int NC4>
+// columns each, and meet through lane shuffles (NTHR threads, a multiple
+// of 64).  With s_x, the same reads stage the token row into LDS for the
+// logits: lane l's chunk of C = 4*NC4 columns is row l of C + 4 floats,
+// which keeps 8 consecutive lanes' b128 reads on distinct banks.
+template <int NC4, int NTHR = kFastThreads>
 __device__ void quantise_token(const RouterArgs &a, int t, float *s_x) {
     constexpr int C = 4 * NC4;
     const int d = a.d, nsb = d / 32;
-    for (int q = threadIdx.x; q < 4 * nsb; q += kFastThreads) {
+    for (int q = threadIdx.x; q < 4 * nsb; q += NTHR) {
         const int sb = q >> 2, part = q & 3, col0 = 32 * sb + 8 * part;
         const f32x4 *v = reinterpret_cast<const f32x4 *>(a.x + (int64_t)t * d + col0);
         const f32x4 v0 = v[0], v1 = v[1];
-        const int q4 = col0 / 4;
-        *reinterpret_cast<f32x4 *>(s_x + (q4 / NC4) * (C + 4) + 4 * (q4 % NC4)) = v0;
-        *reinterpret_cast<f32x4 *>(s_x + ((q4 + 1) / NC4) * (C + 4) + 4 * ((q4 + 1) % NC4)) = v1;
+        if (s_x) {
+            const int q4 = col0 / 4;
+            *reinterpret_cast<f32x4 *>(s_x + (q4 / NC4) * (C + 4) + 4 * (q4 % NC4)) = v0;
+            *reinterpret_cast<f32x4 *>(s_x + ((q4 + 1) / NC4) * (C + 4) + 4 * ((q4 + 1) % NC4)) =
+                v1;
+        }
         const float f[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
         if (a.xh) {
             float amax = 0.0f;
@@ -727,7 +781,7 @@ __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a, Chain
     // 4. one token: this block holds the whole selection and dispatches it
     //    from LDS (no publication wait, no counter)
     if (a.T == 1) {
-        if (tid == 0) dispatch_one(a, s_sel);
+        if (wave == 0) dispatch_one(a, s_sel);
         return;
     }
     // the last block to finish runs the dispatch (the selections were
@@ -739,6 +793,61 @@ __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a, Chain
     __syncthreads();
     if (!s_flag) return;
     dispatch_block<kFastThreads>(a, s_cw, s_off);
+    if (tid == 0) a.sync[0] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// Chain router: exact logits for every (token, expert) as chain tiles
+// (chains.h), spread over the whole chip, then selection and dispatch.  It
+// serves the sigmoid-group kind, more than 64 experts, and batches whose
+// T*E*d makes the per-token fast router re-read the router matrix too often.
+//
+// Launch 1, grid (chain blocks + activation blocks): wave w of chain block b
+// runs tile 4b + w (8 tokens x 8 experts over all d columns); activation
+// block T0 + t prepares token t's limbs and/or f16 pieces.
+// Launch 2, grid (ceil(T / 8)): wave w selects token 8b + w from its logits
+// (select_token); the last block to finish dispatches (one token: the
+// selecting wave dispatches from LDS).
+// ---------------------------------------------------------------------------
+
+constexpr int kChainWaves = 4;
+constexpr int kChainLds = chain_lds_floats(16, 128);
+constexpr int kSelWaves = 8;
+
+__global__ __launch_bounds__(64 * kChainWaves) void k_route_chains(RouterArgs a, ChainArgs ch,
+                                                                   int chain_blocks) {
+    __shared__ __attribute__((aligned(16))) float s_lds[kChainWaves][kChainLds];
+    if ((int)blockIdx.x < chain_blocks) {
+        const int wave = threadIdx.x >> 6, tile = blockIdx.x * kChainWaves + wave;
+        if (tile < ch.tiles) chain_tile<8, 128, 4>(ch, tile, s_lds[wave]);
+        return;
+    }
+    quantise_token<1, 64 * kChainWaves>(a, blockIdx.x - chain_blocks, nullptr);
+}
+
+__global__ __launch_bounds__(64 * kSelWaves) void k_route_select(RouterArgs a) {
+    __shared__ float s_z[kSelWaves][kMaxE], s_s[kSelWaves][kMaxE], s_g[kSelWaves][kMaxE];
+    __shared__ unsigned char s_ok[kSelWaves][kMaxE];
+    __shared__ int s_sel[kSelWaves][kMaxK];
+    __shared__ int s_cw[kSelWaves][kMaxE];
+    __shared__ int s_off[kMaxE + 1];
+    __shared__ int s_flag;
+    const int tid = threadIdx.x, wave = tid >> 6, t = blockIdx.x * kSelWaves + wave;
+    if (t < a.T) select_token(a, t, s_z[wave], s_s[wave], s_g[wave], s_ok[wave], s_sel[wave]);
+    if (a.T == 1) {
+        if (wave == 0) dispatch_one(a, s_sel[0]);
+        return;
+    }
+    __threadfence();  // every selection released at device scope before the count
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned old = atomicAdd(&a.sync[0], 1u);
+        s_flag = (old == gridDim.x - 1);
+    }
+    __syncthreads();
+    if (!s_flag) return;
+    __threadfence();
+    dispatch_block<64 * kSelWaves>(a, s_cw, s_off);
     if (tid == 0) a.sync[0] = 0;
 }
 
@@ -780,6 +889,20 @@ hipError_t launch_router(const RouterArgs &a, hipStream_t st) {
         attr_set = true;
     }
     hipLaunchKernelGGL(k_router, dim3(ntg, neg), dim3(kThreads), lds, st, a, TB, EG);
+    return hipGetLastError();
+}
+
+bool route_chains_ok(const RouterArgs &a) { return a.d % 128 == 0; }
+
+hipError_t launch_route_chains(const RouterArgs &a, hipStream_t st) {
+    const ChainArgs ch = make_chains(a.x, a.wrt, a.logits, nullptr, a.T, a.d, a.E, 0, a.d, 8);
+    const int cb = (ch.tiles + kChainWaves - 1) / kChainWaves;
+    const int ab = (a.xh || a.x16) ? a.T : 0;
+    hipLaunchKernelGGL(k_route_chains, dim3(cb + ab), dim3(64 * kChainWaves), 0, st, a, ch, cb);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_route_select, dim3((a.T + kSelWaves - 1) / kSelWaves),
+                       dim3(64 * kSelWaves), 0, st, a);
     return hipGetLastError();
 }
 

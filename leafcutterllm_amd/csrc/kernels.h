@@ -34,6 +34,11 @@ struct RouterArgs {
 };
 // The exact router: logits, limbs, top-k, dispatch.
 hipError_t launch_router(const RouterArgs &a, hipStream_t st);
+// The exact router as chain tiles over the whole chip, then selection and
+// dispatch (two launches; d % 128 == 0).  Also writes the limbs (a.xh) and
+// the f16 pieces (a.x16) when those are set.
+bool route_chains_ok(const RouterArgs &a);
+hipError_t launch_route_chains(const RouterArgs &a, hipStream_t st);
 // Certified fast router for the softmax kinds: selection, dispatch, limbs
 // and f16 pieces.  The weights come from the exact logits: their chains run
 // in extra blocks of this launch (columns [0, ch.k1), none if ch.tiles == 0)
@@ -75,13 +80,16 @@ hipError_t launch_rpl_down(const uint8_t *down, int64_t estride, const int8_t *h
 // (per token and super-block: hi[256] then lo[256]) plus per-sub-block sums,
 // H out in the same format (and/or f32).
 hipError_t launch_act16(const float *x, int T, int d, _Float16 *x16, _Float16 *xs, hipStream_t st);
+// `chunks` blocks share each slot's 32-token passes (block z takes passes
+// z, z + chunks, ...), so experts with many tokens spread over the chip.
 hipError_t launch_mfma_gateup(const uint8_t *gate, const uint8_t *up, int64_t estride,
                               const _Float16 *x16, const _Float16 *xs, const SlotArgsHost &sa,
-                              int slots, int d, int F, _Float16 *h16, _Float16 *hs, float *hf,
-                              const ChainArgs &ch, hipStream_t st);
+                              int slots, int chunks, int d, int F, _Float16 *h16, _Float16 *hs,
+                              float *hf, const ChainArgs &ch, hipStream_t st);
 hipError_t launch_mfma_down(const uint8_t *down, int64_t estride, const _Float16 *h16,
-                            const _Float16 *hs, const SlotArgsHost &sa, int slots, int d, int F,
-                            int ksplit, float *Y, int64_t split_stride, hipStream_t st);
+                            const _Float16 *hs, const SlotArgsHost &sa, int slots, int chunks,
+                            int d, int F, int ksplit, float *Y, int64_t split_stride,
+                            hipStream_t st);
 
 // Routing weights computed by the combine from exact logits (fast-router
 // path); logits == null: the weights are already in topk_w.

@@ -35,6 +35,8 @@ const char *kSlotNames[kNumSlots] = {"router", "act16", "gateup", "gateup_shared
 constexpr int kMaxKSplit = 4;
 // matrix-core path when an expert family averages at least this many tokens
 constexpr int kMfmaMinTokens = 1;
+// largest T * E * d served by the certified per-token router
+constexpr int64_t kFastRouterElems = (int64_t)1 << 24;
 
 struct ExpertSet {  // one family of experts (routed or shared)
     int n = 0, F = 0, qt_gu = 0, qt_dn = 0;
@@ -326,6 +328,7 @@ extern "C" void lcmoe_destroy(lcmoe_handle *h) { free_handle(h); }
 struct Plan {
     bool mfma;
     int slots, ks;
+    int chunks;  // blocks sharing one matrix-core slot's 32-token passes
 };
 
 static Plan plan_set(lcmoe_handle *h, const ExpertSet &s, bool shared, int T) {
@@ -338,7 +341,12 @@ static Plan plan_set(lcmoe_handle *h, const ExpertSet &s, bool shared, int T) {
     const int64_t per_expert =
         shared ? T : (int64_t)T * D.n_expert_used / std::max(1, D.n_expert);
     p.mfma = s.rpl_gu && per_expert >= kMfmaMinTokens;
-    p.ks = p.mfma && s.rpl_dn ? choose_ksplit_mfma(s, D.d_model, p.slots)
+    // passes per slot: all T tokens for a shared expert, the average over
+    // the touched experts for the routed ones (busier experts run several
+    // passes per block)
+    const int64_t per_slot = shared ? T : ((int64_t)T * D.n_expert_used + p.slots - 1) / p.slots;
+    p.chunks = p.mfma ? (int)std::min<int64_t>(64, std::max<int64_t>(1, (per_slot + 31) / 32)) : 1;
+    p.ks = p.mfma && s.rpl_dn ? choose_ksplit_mfma(s, D.d_model, p.slots * p.chunks)
                                : choose_ksplit(s, D.d_model, p.slots);
     return p;
 }
@@ -350,8 +358,8 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
     SlotArgsHost sa{h->perm, h->counts, h->offsets, h->touched, E, K, T, shared ? 1 : 0};
     HIP_TRY(timed(h, st, shared ? kSlotGateUpSh : kSlotGateUp, [&] {
         if (pl.mfma)
-            return launch_mfma_gateup(s.gate, s.up, s.sz_gu, h->x16, h->x16s, sa, pl.slots, d,
-                                      s.F, s.rpl_dn ? s.h16 : nullptr, s.h16s,
+            return launch_mfma_gateup(s.gate, s.up, s.sz_gu, h->x16, h->x16s, sa, pl.slots,
+                                      pl.chunks, d, s.F, s.rpl_dn ? s.h16 : nullptr, s.h16s,
                                       s.rpl_dn ? nullptr : s.Hf, ch, st);
         if (s.rpl_gu)
             return launch_rpl_gateup(s.gate, s.up, s.sz_gu, h->xh, h->xl, h->xs, h->xm, sa,
@@ -361,8 +369,8 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
     }));
     HIP_TRY(timed(h, st, shared ? kSlotDownSh : kSlotDown, [&] {
         if (s.rpl_dn && pl.mfma)
-            return launch_mfma_down(s.down, s.sz_dn, s.h16, s.h16s, sa, pl.slots, d, s.F,
-                                    pl.ks, s.Y, s.positions * d, st);
+            return launch_mfma_down(s.down, s.sz_dn, s.h16, s.h16s, sa, pl.slots, pl.chunks, d,
+                                    s.F, pl.ks, s.Y, s.positions * d, st);
         if (s.rpl_dn)
             return launch_rpl_down(s.down, s.sz_dn, s.hh, s.hl, s.hs, s.hm, sa, pl.slots, d, s.F,
                                    pl.ks, s.Y, s.positions * d, st);
@@ -376,7 +384,7 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
     const lcmoe_desc &D = h->desc;
     const int d = D.d_model, E = D.n_expert, K = D.n_expert_used, S = D.n_shared;
     const Plan pr = plan_set(h, h->routed, false, T);
-    const Plan ps = S > 0 ? plan_set(h, h->shared, true, T) : Plan{false, 0, 1};
+    const Plan ps = S > 0 ? plan_set(h, h->shared, true, T) : Plan{false, 0, 1, 1};
     const bool mfma = pr.mfma || ps.mfma;
     // int8 limbs only feed the row-per-lane kernels
     const bool limbs = (h->routed.rpl_gu && !pr.mfma) || (S > 0 && h->shared.rpl_gu && !ps.mfma);
@@ -405,7 +413,10 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
     ra.inv = h->inv;
     ra.touched = h->touched;
     ra.sync = h->sync;
-    const bool fast = route_fast_ok(ra);
+    // the fast router reads the whole router matrix once per token: past
+    // kFastRouterElems multiply-adds per forward the chain router, which
+    // reads each router row once per 8 tokens, is the faster one
+    const bool fast = route_fast_ok(ra) && (int64_t)T * E * d <= kFastRouterElems;
     // With the certified fast router, selection, dispatch and activations
     // come from it; the exact chains of the routing weights run in extra
     // blocks beside them, and the combine turns the chains into weights.  The
@@ -421,6 +432,9 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
         ch_g = make_chains(x, h->wrt, h->logits, h->chain_part, T, d, E, kA, d, 8);
         ra.x16 = mfma ? h->x16 : nullptr;
         HIP_TRY(timed(h, st, kSlotRouter, [&] { return launch_route_fast(ra, ch_r, st); }));
+    } else if (route_chains_ok(ra)) {
+        ra.x16 = mfma ? h->x16 : nullptr;
+        HIP_TRY(timed(h, st, kSlotRouter, [&] { return launch_route_chains(ra, st); }));
     } else {
         HIP_TRY(timed(h, st, kSlotRouter, [&] { return launch_router(ra, st); }));
         if (mfma)
