@@ -710,6 +710,249 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down(
     }
 }
 
+// ---- Q6_K down ------------------------------------------------------------
+// Weights in the RPL64 Q6_K layout (lcmoe_host.cpp): per 64-row tile and
+// super-block, thirteen 1 KiB chunks (chunk c = bytes 16c .. 16c+15 of every
+// row's 210-byte block: ql in 0-7, qh in 8-11, the 16 int8 scales in 12) and
+// then the 64 rows' f16 d.
+//
+// Element 128n + 32j + l of a block (half n, group j, l < 32) has the 6-bit
+// code q = (4 bits of ql) | (2 bits of qh) << 4 (dequantize_q6_k,
+// rust/src/kernels/mod.rs:145-180):
+//   j = 0: ql[64n + l] low,  qh[32n + l] bits 0-1    j = 1: ql[64n+32+l] low,  bits 2-3
+//   j = 2: ql[64n + l] high, qh[32n + l] bits 4-5    j = 3: ql[64n+32+l] high, bits 6-7
+// and the value d * sc[8n + 2j + l/16] * (q - 32).  A 16-column K-step is
+// one scale group.  sc * (q - 32) reaches 4096, past the integers f16 holds
+// exactly, so the scale is split as sc = 16 sh + sl (sh = sc >> 4 in
+// [-8, 7], sl = sc & 15): B1 = sh (q - 32) and B2 = sl (q - 32) are exact
+// f16 values, and S = 16 S1 + S2 with S1 = A B1, S2 = A B2 (four MFMAs per
+// K-step with the activations' hi/lo halves).  Lane (r, h) of a 32-row half
+// takes, per unit v = 2n + i, the 8 bytes at 8h of ql chunks 4n+i and
+// 4n+2+i and of qh chunk 8+2n+i: columns 128n + 32j + 16i + 8h .. +7 of the
+// four groups j.
+constexpr int kQ6Chunks = 13;
+constexpr int kQ6Stride = kQ6Chunks * 1024 + 128;
+
+struct W6 {
+    u32x4 sc;        // the row's 16 scales
+    uint32_t d;      // the row's d (f16 bits)
+    u32x2 q[4][3];   // per unit: ql (groups 0, 2), ql (groups 1, 3), qh
+};
+
+__device__ __forceinline__ u32x2 load_q6(g_u8 *base, uint32_t lo, int kb, int chunk) {
+    return gload<u32x2>(base + (lo + (uint32_t)(kb * kQ6Stride + chunk * 1024)));
+}
+
+// lo: this lane's row offset (row * 16) plus 8h; dlo: the row's d offset
+__device__ __forceinline__ void load_w6_unit(W6 &w, g_u8 *base, uint32_t lo, int kb, int v) {
+    const int n = v >> 1, i = v & 1;
+    w.q[v][0] = load_q6(base, lo, kb, 4 * n + i);
+    w.q[v][1] = load_q6(base, lo, kb, 4 * n + 2 + i);
+    w.q[v][2] = load_q6(base, lo, kb, 8 + 2 * n + i);
+}
+
+__device__ __forceinline__ void load_w6_head(W6 &w, g_u8 *base, uint32_t rlo, uint32_t dlo,
+                                             int kb) {
+    w.sc = gload<u32x4>(base + (rlo + (uint32_t)(kb * kQ6Stride + 12 * 1024)));
+    w.d = gload<uint16_t>(base + (dlo + (uint32_t)(kb * kQ6Stride + kQ6Chunks * 1024)));
+}
+
+// 6-bit codes of group j from one unit's words (one code per byte)
+__device__ __forceinline__ uint32_t q6_group(uint32_t qa, uint32_t qb, uint32_t qh, int j) {
+    switch (j) {
+    case 0: return (qa & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u);
+    case 1: return (qb & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u);
+    case 2: return ((qa >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u);
+    default: return ((qb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u);
+    }
+}
+
+// byte b of w twice, as the f16 pair (1024 + byte, 1024 + byte)
+__device__ __forceinline__ half2v magic_bb(uint32_t w, int b) {
+    const uint32_t sel = 0x04000400u | ((uint32_t)b << 16) | (uint32_t)b;
+    return magic2(w, sel);
+}
+
+// B1 = sh (q - 32), B2 = sl (q - 32) for 8 codes (bytes of g0, g1):
+// (1024 + q) s - 1056 s, one rounding of an exact integer result
+__device__ __forceinline__ void dec6(uint32_t g0, uint32_t g1, half2v sh2, half2v c1, half2v sl2,
+                                     half2v c2, half8 &b1, half8 &b2) {
+    const half2v m[4] = {magic2(g0, kSel01), magic2(g0, kSel23), magic2(g1, kSel01),
+                         magic2(g1, kSel23)};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const half2v x = __builtin_elementwise_fma(m[k], sh2, c1);
+        const half2v y = __builtin_elementwise_fma(m[k], sl2, c2);
+        b1[2 * k] = x[0];
+        b1[2 * k + 1] = x[1];
+        b2[2 * k] = y[0];
+        b2[2 * k + 1] = y[1];
+    }
+}
+
+// One step of a 32-token pass over Q6_K: super-block k of both 32-row halves
+// from `cur` and w; activations of super-block kn into `nxt`; w reloaded
+// with kn unit by unit after each unit's decode.
+__device__ __forceinline__ void step_q6(g_u8 *wb, const uint32_t (&lo)[2], const uint32_t (&rlo)[2],
+                                        const uint32_t (&dlo)[2], int kn, const uint8_t *cur,
+                                        uint8_t *nxt, const StageSrc &src, W6 (&w)[2],
+                                        float16v (&acc)[2], int wave, int lane) {
+    const int r = lane & 31, h = lane >> 5;
+    StageRegs<8> act;
+    stage_load(act, src, kn, wave, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 sc[2];
+    float dd[2];
+#pragma unroll
+    for (int m = 0; m < 2; m++) {
+        sc[m] = w[m].sc;
+        dd[m] = dh2f(w[m].d & 0xffff);
+        load_w6_head(w[m], wb, rlo[m], dlo[m], kn);
+    }
+    float16v S1[2], S2[2];
+#pragma unroll
+    for (int m = 0; m < 2; m++) S1[m] = S2[m] = float16v{};
+    const uint8_t *tokrow = cur + r * kTokBytes;
+    const half2v k1024 = half2v{(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const half2v k1032 = half2v{(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const half2v k1056 = half2v{(_Float16)-1056.0f, (_Float16)-1056.0f};
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const int n = v >> 1, i = v & 1;
+        // scale nibbles of this unit's four groups: bytes i, i + 2 of words
+        // 2n (groups 0, 1) and 2n + 1 (groups 2, 3)
+        uint32_t sl_w[2][2], sh_w[2][2];
+#pragma unroll
+        for (int m = 0; m < 2; m++)
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const uint32_t wv = sc[m][2 * n + k];
+                sl_w[m][k] = wv & 0x0F0F0F0Fu;
+                sh_w[m][k] = ((wv >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;  // sh + 8
+            }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int col = 2 * (128 * n + 32 * j + 16 * i + 8 * h);  // bytes
+            const half8 ah = *reinterpret_cast<const half8 *>(tokrow + col);
+            const half8 al = *reinterpret_cast<const half8 *>(tokrow + 512 + col);
+#pragma unroll
+            for (int m = 0; m < 2; m++) {
+                const int b = i + 2 * (j & 1);
+                const half2v sl2 = magic_bb(sl_w[m][j >> 1], b) + k1024;
+                const half2v sh2 = magic_bb(sh_w[m][j >> 1], b) + k1032;
+                const half2v c1 = sh2 * k1056, c2 = sl2 * k1056;
+                const uint32_t g0 = q6_group(w[m].q[v][0].x, w[m].q[v][1].x, w[m].q[v][2].x, j);
+                const uint32_t g1 = q6_group(w[m].q[v][0].y, w[m].q[v][1].y, w[m].q[v][2].y, j);
+                half8 b1, b2;
+                dec6(g0, g1, sh2, c1, sl2, c2, b1, b2);
+                S1[m] = mfma32(ah, b1, S1[m]);
+                S1[m] = mfma32(al, b1, S1[m]);
+                S2[m] = mfma32(ah, b2, S2[m]);
+                S2[m] = mfma32(al, b2, S2[m]);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < 2; m++) load_w6_unit(w[m], wb, lo[m], kn, v);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int m = 0; m < 2; m++) {
+        const float d16 = 16.0f * dd[m];
+#pragma unroll
+        for (int t = 0; t < 16; t++) {
+            acc[m][t] = __builtin_fmaf(d16, S1[m][t], acc[m][t]);
+            acc[m][t] = __builtin_fmaf(dd[m], S2[m][t], acc[m][t]);
+        }
+    }
+    stage_store(nxt, act, wave, lane);
+    lds_barrier();
+}
+
+__device__ __forceinline__ void block_pass_q6(g_u8 *wb, const uint32_t (&lo)[2],
+                                              const uint32_t (&rlo)[2], const uint32_t (&dlo)[2],
+                                              int kb0, int kb1, const StageSrc &src,
+                                              float16v (&acc)[2]) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int last = kb1 - 1;
+    asm volatile("" : "+s"(kb0));  // see block_pass()
+    W6 w[2];
+    StageRegs<8> act;
+    stage_load(act, src, kb0, wave, lane);
+#pragma unroll
+    for (int m = 0; m < 2; m++) {
+        load_w6_head(w[m], wb, rlo[m], dlo[m], kb0);
+#pragma unroll
+        for (int v = 0; v < 4; v++) load_w6_unit(w[m], wb, lo[m], kb0, v);
+    }
+    stage_store(s_stage0, act, wave, lane);
+    lds_barrier();
+    int kb = kb0;
+    for (; kb + 2 <= kb1; kb += 2) {
+        step_q6(wb, lo, rlo, dlo, kb + 1, s_stage0, s_stage1, src, w, acc, wave, lane);
+        step_q6(wb, lo, rlo, dlo, min(kb + 2, last), s_stage1, s_stage0, src, w, acc, wave, lane);
+    }
+    if (kb < kb1) step_q6(wb, lo, rlo, dlo, kb, s_stage0, s_stage1, src, w, acc, wave, lane);
+}
+
+// grid (d/256 row blocks, slots, ksplit x pass groups), as k_mfma_down; every
+// pass takes 32 tokens.
+__global__ __launch_bounds__(256, 2) void k_mfma_down_q6(
+    const uint8_t *__restrict__ down, int64_t estride, const _Float16 *__restrict__ h16,
+    SlotArgs sa, int d, int F, int ksplit, float *__restrict__ Y, int64_t split_stride) {
+    int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+    {
+        const int nx = gridDim.x, ny = gridDim.y, total = nx * ny * gridDim.z;
+        const int id = bx + nx * (by + ny * bz), per = total / kXcds;
+        if (total % kXcds == 0 && per % nx == 0) {
+            const int q = (id % kXcds) * per + id / kXcds, pair = q / nx;
+            bx = q % nx;
+            by = pair % ny;
+            bz = pair / ny;
+        }
+    }
+    const int cz = bz / ksplit, nz = gridDim.z / ksplit;
+    bz -= cz * ksplit;
+    int e, p0, n;
+    if (!slot_info(sa, by, e, p0, n)) return;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
+    const int ntile = d >> 6, tile0 = bx * kWaves + wave;
+    const int tile = min(tile0, ntile - 1);  // duplicate the last tile past the end
+    const int NB = F >> 8;
+    const int kb0 = (int)((int64_t)NB * bz / ksplit);
+    const int kb1 = (int)((int64_t)NB * (bz + 1) / ksplit);
+    g_u8 *const wb = uniform(down + (int64_t)e * estride + (int64_t)tile * NB * kQ6Stride);
+    const uint32_t rlo[2] = {(uint32_t)r * 16, (uint32_t)(32 + r) * 16};
+    const uint32_t lo[2] = {rlo[0] + 8 * h, rlo[1] + 8 * h};
+    const uint32_t dlo[2] = {(uint32_t)r * 2, (uint32_t)(32 + r) * 2};
+    float *Yz = Y + (int64_t)bz * split_stride;
+    const uint8_t *hb = reinterpret_cast<const uint8_t *>(h16);
+    for (int c = cz * kTok; c < n; c += nz * kTok) {
+        StageSrc src;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            src.tok[i] = uniform(hb + (int64_t)(p0 + min(c + wave + 4 * i, n - 1)) * F * 4);
+        // the sums are not used (Q6_K has no mins): stage a valid row
+        src.sums = uniform(hb);
+        src.soff = 16 * (uint32_t)lane;
+        float16v acc[2] = {float16v{}, float16v{}};
+        block_pass_q6(wb, lo, rlo, dlo, kb0, kb1, src, acc);
+        if (tile0 >= ntile) continue;
+        int rb = tile * 64 + r;  // opaque: output addresses are formed here
+        asm volatile("" : "+v"(rb));
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int q = c + c_token(i, h);
+            if (q < n) {
+                float *yrow = Yz + (int64_t)(p0 + q) * d + rb;
+                yrow[0] = acc[0][i];
+                yrow[32] = acc[1][i];
+            }
+        }
+    }
+}
+
 // x rows -> f16 hi/lo pieces (per super-block: hi[256] then lo[256]) and
 // per-sub-block sums (hi, lo); one thread per 32-column sub-block
 __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int T, int d,
@@ -752,6 +995,17 @@ SlotArgs dev_slots(const SlotArgsHost &s) {
 }
 
 }  // namespace
+
+hipError_t launch_mfma_down_q6(const uint8_t *down, int64_t estride, const _Float16 *h16,
+                               const SlotArgsHost &sa, int slots, int chunks, int d, int F,
+                               int ksplit, float *Y, int64_t split_stride, hipStream_t st) {
+    const int tiles = d / 64;
+    if (chunks < 1 || ksplit < 1 || (int64_t)chunks * ksplit > 65535) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_mfma_down_q6, dim3((tiles + kWaves - 1) / kWaves, slots, ksplit * chunks),
+                       dim3(256), 0, st, down, estride, h16, dev_slots(sa), d, F, ksplit, Y,
+                       split_stride);
+    return hipGetLastError();
+}
 
 hipError_t launch_act16(const float *x, int T, int d, _Float16 *x16, _Float16 *xs,
                         hipStream_t st) {

@@ -164,6 +164,9 @@ struct HOut {
     float *f;       // H f32 [positions, F] or null
     int8_t *h, *l;  // H limbs [positions, F] or null
     float *s, *m;   // [positions, F/32]
+    // H as f16 hi/lo pieces [positions][F/256][hi 256 | lo 256] and 32-row
+    // sums (hi, lo) [positions][F/32][2] for the matrix-core down, or null
+    _Float16 *h16, *hs16;
 };
 
 // Tokens per pass.  This path runs when experts average fewer than two
@@ -216,6 +219,20 @@ __device__ __forceinline__ void gateup_chunk(const uint4 *G, const uint4 *U, int
                 out.m[p * (F >> 5) + (f >> 5)] = sum;
             }
         }
+        if (out.h16) {
+            const _Float16 hi = (_Float16)h, lo = (_Float16)(h - (float)hi);
+            float part = (float)hi + (float)lo;
+#pragma unroll
+            for (int off = 1; off < 32; off <<= 1) part += __shfl_xor(part, off, 64);
+            _Float16 *piece = out.h16 + (p * (F >> 8) + (f >> 8)) * 512 + (f & 255);
+            piece[0] = hi;
+            piece[256] = lo;
+            if ((lane & 31) == 0) {
+                const _Float16 shi = (_Float16)part, slo = (_Float16)(part - (float)shi);
+                out.hs16[(p * (F >> 5) + (f >> 5)) * 2] = shi;
+                out.hs16[(p * (F >> 5) + (f >> 5)) * 2 + 1] = slo;
+            }
+        }
     }
     __syncthreads();
 }
@@ -239,7 +256,8 @@ __global__ __launch_bounds__(256) void k_rpl_gateup(
     const int8_t *__restrict__ xh, const int8_t *__restrict__ xl, const float *__restrict__ xs,
     const float *__restrict__ xm, SlotArgs sa, int d, int F, float *__restrict__ hf,
     int8_t *__restrict__ hh, int8_t *__restrict__ hl, float *__restrict__ hs,
-    float *__restrict__ hm, ChainArgs ch) {
+    float *__restrict__ hm, _Float16 *__restrict__ h16, _Float16 *__restrict__ hs16,
+    ChainArgs ch) {
     int slot = blockIdx.y;
     if (ch.tiles) {  // row y = 0: exact router chains, one wave per block
         if (slot == 0) {
@@ -250,7 +268,7 @@ __global__ __launch_bounds__(256) void k_rpl_gateup(
         slot -= 1;
     }
     const Limbs X{xh, xl, xs, xm, d};
-    const HOut out{hf, hh, hl, hs, hm};
+    const HOut out{hf, hh, hl, hs, hm, h16, hs16};
     int e, p0, n;
     if (!slot_info(sa, slot, e, p0, n)) return;
     e = __builtin_amdgcn_readfirstlane(e);
@@ -338,8 +356,8 @@ __global__ __launch_bounds__(256) void k_rpl_down(
 hipError_t launch_rpl_gateup(const uint8_t *gate, const uint8_t *up, int64_t estride,
                              const int8_t *xh, const int8_t *xl, const float *xs, const float *xm,
                              const SlotArgsHost &sa, int slots, int d, int F, float *Hf, int8_t *hh,
-                             int8_t *hl, float *hs, float *hm, const ChainArgs &ch,
-                             hipStream_t st) {
+                             int8_t *hl, float *hs, float *hm, _Float16 *h16, _Float16 *hs16,
+                             const ChainArgs &ch, hipStream_t st) {
     SlotArgs s{sa.perm, sa.counts, sa.offsets, sa.touched, sa.E, sa.K, sa.T, sa.shared};
     ChainArgs c = ch;
     if (c.tiles) {
@@ -347,7 +365,8 @@ hipError_t launch_rpl_gateup(const uint8_t *gate, const uint8_t *up, int64_t est
         c = with_nt(ch, ch.T == 1 ? 1 : 8);
     }
     hipLaunchKernelGGL(k_rpl_gateup, dim3(F / 64, slots + (c.tiles ? 1 : 0)), dim3(256), 0, st,
-                       gate, up, estride, xh, xl, xs, xm, s, d, F, Hf, hh, hl, hs, hm, c);
+                       gate, up, estride, xh, xl, xs, xm, s, d, F, Hf, hh, hl, hs, hm, h16, hs16,
+                       c);
     return hipGetLastError();
 }
 

@@ -67,10 +67,13 @@ hipError_t launch_generic_down(int qt, const uint8_t *down, int64_t estride, con
 
 // Row-per-lane Q4_K decode path on the RPL64 layout: int8-limb activations,
 // exact integer dot products.
+// H goes out as f32 (Hf), int8 limbs (hh, hl, hs, hm) and/or f16 pieces
+// with 32-row sums (h16, hs16) for the matrix-core down; null skips a form.
 hipError_t launch_rpl_gateup(const uint8_t *gate, const uint8_t *up, int64_t estride,
                              const int8_t *xh, const int8_t *xl, const float *xs, const float *xm,
                              const SlotArgsHost &sa, int slots, int d, int F, float *Hf, int8_t *hh,
-                             int8_t *hl, float *hs, float *hm, const ChainArgs &ch, hipStream_t st);
+                             int8_t *hl, float *hs, float *hm, _Float16 *h16, _Float16 *hs16,
+                             const ChainArgs &ch, hipStream_t st);
 hipError_t launch_rpl_down(const uint8_t *down, int64_t estride, const int8_t *hh,
                            const int8_t *hl, const float *hs, const float *hm,
                            const SlotArgsHost &sa, int slots, int d, int F, int ksplit, float *Y,
@@ -90,6 +93,11 @@ hipError_t launch_mfma_down(const uint8_t *down, int64_t estride, const _Float16
                             const _Float16 *hs, const SlotArgsHost &sa, int slots, int chunks,
                             int d, int F, int ksplit, float *Y, int64_t split_stride,
                             hipStream_t st);
+// The same down product for Q6_K weights in the RPL64 Q6_K layout (32-token
+// passes; H as f16 pieces, no sums needed).
+hipError_t launch_mfma_down_q6(const uint8_t *down, int64_t estride, const _Float16 *h16,
+                               const SlotArgsHost &sa, int slots, int chunks, int d, int F,
+                               int ksplit, float *Y, int64_t split_stride, hipStream_t st);
 
 // Routing weights computed by the combine from exact logits (fast-router
 // path); logits == null: the weights are already in topk_w.
@@ -114,6 +122,10 @@ hipError_t launch_debug_sigmoid(const float *x, int64_t n, float *out, hipStream
 // RPL64 eligibility: Q4_K, rows tile by 64, columns are whole super-blocks.
 inline bool rpl64_ok(int qt, int64_t rows, int64_t cols) {
     return qt == 12 && rows % 64 == 0 && cols % 256 == 0;
+}
+// Q6_K matrices the matrix-core down serves (RPL64 Q6_K layout)
+inline bool rpl64_q6_ok(int qt, int64_t rows, int64_t cols) {
+    return qt == 14 && rows % 64 == 0 && cols % 256 == 0;
 }
 
 }  // namespace lcmoe

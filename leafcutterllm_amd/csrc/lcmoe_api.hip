@@ -40,7 +40,9 @@ constexpr int64_t kFastRouterElems = (int64_t)1 << 24;
 
 struct ExpertSet {  // one family of experts (routed or shared)
     int n = 0, F = 0, qt_gu = 0, qt_dn = 0;
-    bool rpl_gu = false, rpl_dn = false;
+    // RPL64 Q4_K gate/up; RPL64 Q4_K down (row-per-lane and matrix-core);
+    // RPL64 Q6_K down (matrix-core only)
+    bool rpl_gu = false, rpl_dn = false, q6_dn = false;
     uint8_t *gate = nullptr, *up = nullptr, *down = nullptr;
     int64_t sz_gu = 0, sz_dn = 0;
     // H between the two products: f32 (generic down), int8 limbs (row-per-lane
@@ -111,7 +113,8 @@ lcmoe_status alloc_n(lcmoe_handle *h, T **dst, size_t n) {
 }
 
 // Uploads n stacked expert matrices [rows, cols] of type qt, repacking each
-// to RPL64 when `rpl` (one expert at a time through a host staging buffer).
+// to RPL64 (Q4_K or Q6_K, by qt) when `rpl` (one expert at a time through a
+// host staging buffer).
 lcmoe_status upload_stack(lcmoe_handle *h, uint8_t **dst, const uint8_t *src, int n, int qt,
                           int64_t rows, int64_t cols, bool rpl, int64_t *sz_out) {
     const int64_t sz = (int64_t)lcmoe_tensor_size(qt, rows * cols);
@@ -131,9 +134,15 @@ lcmoe_status upload_stack(lcmoe_handle *h, uint8_t **dst, const uint8_t *src, in
         std::vector<std::thread> th;
         for (unsigned t = 0; t < nth; t++)
             th.emplace_back([&, t] {
-                const int64_t NB = cols / 256, tb = (int64_t)NB * 9 * 1024;
-                for (int64_t rt = t; rt < tiles; rt += nth)
-                    repack_rpl64_q4k(s + rt * 64 * NB * 144, buf.data() + rt * tb, 64, cols);
+                const int64_t NB = cols / 256;
+                const bool q6 = qt == LCMOE_TYPE_Q6_K;
+                const int64_t tb = NB * (q6 ? 13 * 1024 + 128 : 9 * 1024), bb = q6 ? 210 : 144;
+                for (int64_t rt = t; rt < tiles; rt += nth) {
+                    if (q6)
+                        repack_rpl64_q6k(s + rt * 64 * NB * bb, buf.data() + rt * tb, 64, cols);
+                    else
+                        repack_rpl64_q4k(s + rt * 64 * NB * bb, buf.data() + rt * tb, 64, cols);
+                }
             });
         for (auto &x : th) x.join();
         HIP_TRY(hipMemcpy(*dst + (size_t)e * sz, buf.data(), (size_t)sz, hipMemcpyHostToDevice));
@@ -192,6 +201,7 @@ int choose_ksplit(const ExpertSet &s, int d, int active) {
 // Matrix-core down: 256-row blocks, two resident per CU; split K until
 // about two blocks per CU exist, keeping >= 4 super-blocks per split.
 int choose_ksplit_mfma(const ExpertSet &s, int d, int active) {
+    if (!s.rpl_dn && !s.q6_dn) return 1;
     const int NB = s.F / 256, blocks = ((d / 64 + 3) / 4) * std::max(1, active);
     int ks = 1;
     while (ks < s.kmax && blocks * ks < 512 && NB >= 4 * ks * 2) ks *= 2;
@@ -208,18 +218,20 @@ lcmoe_status setup_set(lcmoe_handle *h, ExpertSet &s, int n, int F, int qgu, int
     s.positions = positions;
     s.rpl_gu = rpl64_ok(qgu, F, d);
     s.rpl_dn = s.rpl_gu && rpl64_ok(qdn, d, F);
-    s.kmax = s.rpl_dn ? kMaxKSplit : 1;
+    s.q6_dn = s.rpl_gu && rpl64_q6_ok(qdn, d, F);
+    s.kmax = s.rpl_dn || s.q6_dn ? kMaxKSplit : 1;
     int64_t szu = 0;
     lcmoe_status st;
     if ((st = upload_stack(h, &s.gate, gate, n, qgu, F, d, s.rpl_gu, &s.sz_gu))) return st;
     if ((st = upload_stack(h, &s.up, up, n, qgu, F, d, s.rpl_gu, &szu))) return st;
-    if ((st = upload_stack(h, &s.down, down, n, qdn, d, F, s.rpl_dn, &s.sz_dn))) return st;
+    if ((st = upload_stack(h, &s.down, down, n, qdn, d, F, s.rpl_dn || s.q6_dn, &s.sz_dn)))
+        return st;
     if (s.rpl_dn) {
         if ((st = alloc_n(h, &s.hh, positions * F))) return st;
         if ((st = alloc_n(h, &s.hl, positions * F))) return st;
         if ((st = alloc_n(h, &s.hs, positions * F / 32))) return st;
         if ((st = alloc_n(h, &s.hm, positions * F / 32))) return st;
-    } else {
+    } else if (!s.q6_dn) {
         if ((st = alloc_n(h, &s.Hf, positions * F))) return st;
     }
     if (s.rpl_gu) {
@@ -346,8 +358,8 @@ static Plan plan_set(lcmoe_handle *h, const ExpertSet &s, bool shared, int T) {
     // passes per block)
     const int64_t per_slot = shared ? T : ((int64_t)T * D.n_expert_used + p.slots - 1) / p.slots;
     p.chunks = p.mfma ? (int)std::min<int64_t>(64, std::max<int64_t>(1, (per_slot + 31) / 32)) : 1;
-    p.ks = p.mfma && s.rpl_dn ? choose_ksplit_mfma(s, D.d_model, p.slots * p.chunks)
-                               : choose_ksplit(s, D.d_model, p.slots);
+    p.ks = (p.mfma && s.rpl_dn) || s.q6_dn ? choose_ksplit_mfma(s, D.d_model, p.slots * p.chunks)
+                                            : choose_ksplit(s, D.d_model, p.slots);
     return p;
 }
 
@@ -356,18 +368,24 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
     const lcmoe_desc &D = h->desc;
     const int d = D.d_model, K = D.n_expert_used, E = D.n_expert;
     SlotArgsHost sa{h->perm, h->counts, h->offsets, h->touched, E, K, T, shared ? 1 : 0};
+    // H between the products in the form the down kernel reads
+    const bool h16_out = (pl.mfma && s.rpl_dn) || s.q6_dn;
     HIP_TRY(timed(h, st, shared ? kSlotGateUpSh : kSlotGateUp, [&] {
         if (pl.mfma)
             return launch_mfma_gateup(s.gate, s.up, s.sz_gu, h->x16, h->x16s, sa, pl.slots,
-                                      pl.chunks, d, s.F, s.rpl_dn ? s.h16 : nullptr, s.h16s,
-                                      s.rpl_dn ? nullptr : s.Hf, ch, st);
+                                      pl.chunks, d, s.F, h16_out ? s.h16 : nullptr, s.h16s,
+                                      h16_out ? nullptr : s.Hf, ch, st);
         if (s.rpl_gu)
             return launch_rpl_gateup(s.gate, s.up, s.sz_gu, h->xh, h->xl, h->xs, h->xm, sa,
-                                     pl.slots, d, s.F, s.Hf, s.hh, s.hl, s.hs, s.hm, ch, st);
+                                     pl.slots, d, s.F, s.Hf, s.rpl_dn ? s.hh : nullptr, s.hl,
+                                     s.hs, s.hm, s.q6_dn ? s.h16 : nullptr, s.h16s, ch, st);
         return launch_generic_gateup(s.qt_gu, s.gate, s.up, s.sz_gu, x, sa, pl.slots, d, s.F,
                                      s.Hf, nullptr, nullptr, nullptr, nullptr, ch, st);
     }));
     HIP_TRY(timed(h, st, shared ? kSlotDownSh : kSlotDown, [&] {
+        if (s.q6_dn)
+            return launch_mfma_down_q6(s.down, s.sz_dn, s.h16, sa, pl.slots, pl.chunks, d, s.F,
+                                       pl.ks, s.Y, s.positions * d, st);
         if (s.rpl_dn && pl.mfma)
             return launch_mfma_down(s.down, s.sz_dn, s.h16, s.h16s, sa, pl.slots, pl.chunks, d,
                                     s.F, pl.ks, s.Y, s.positions * d, st);

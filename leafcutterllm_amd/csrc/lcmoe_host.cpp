@@ -307,6 +307,24 @@ void repack_rpl64_q4k(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t co
             }
 }
 
+// RPL64 repack of a GGUF Q6_K [rows, cols] matrix (rows % 64 == 0,
+// cols % 256 == 0): per 64-row tile and super-block, the 210-byte blocks of
+// the 64 rows are cut into thirteen 16-byte chunks (ql: 0-7, qh: 8-11,
+// scales: 12) stored chunk by chunk as for Q4_K, followed by the 64 rows'
+// 2-byte d: 13,440 bytes per tile and super-block.  Same bytes, new order.
+void repack_rpl64_q6k(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t cols) {
+    const int64_t NB = cols / 256, row_bytes = NB * 210, tb = 13 * 1024 + 128;
+    for (int64_t rt = 0; rt < rows / 64; rt++)
+        for (int64_t kb = 0; kb < NB; kb++) {
+            uint8_t *o = dst + (rt * NB + kb) * tb;
+            for (int r = 0; r < 64; r++) {
+                const uint8_t *blk = src + (rt * 64 + r) * row_bytes + kb * 210;
+                for (int c = 0; c < 13; c++) std::memcpy(o + c * 1024 + r * 16, blk + c * 16, 16);
+                std::memcpy(o + 13 * 1024 + r * 2, blk + 208, 2);
+            }
+        }
+}
+
 }  // namespace lcmoe
 
 extern "C" lcmoe_status lcmoe_quantize(int32_t type, const float *src, uint8_t *dst, int64_t count) {

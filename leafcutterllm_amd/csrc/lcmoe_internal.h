@@ -86,5 +86,7 @@ lcmoe_status validate_desc(const lcmoe_desc *d);
 lcmoe_status scan_weights(const lcmoe_desc *d, const lcmoe_weights *w);
 // RPL64 repack (defined in lcmoe_host.cpp, layout documented there).
 void repack_rpl64_q4k(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t cols);
+// RPL64 repack of Q6_K (defined in lcmoe_host.cpp, layout documented there).
+void repack_rpl64_q6k(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t cols);
 
 }  // namespace lcmoe

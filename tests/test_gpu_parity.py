@@ -230,6 +230,17 @@ def test_full_config_parity(full_layers, c, T):
     print(f"config {c} T={T}: rel_l2={res['rel_l2']:.2e} touched={int((res['counts'] > 0).sum())}")
 
 
+@pytest.mark.parametrize("T", [1, 32, 256])
+def test_full_config4_parity(full_layers, T):
+    """DeepSeek-V3 shape: sigmoid-group router over 256 experts, Q6_K down
+    (matrix-core Q6_K path), one shared expert."""
+    cfg, layer, moe = full_layers(4)
+    x = L.synth_x(cfg, T, seed=0, index=T)
+    subset = None if T == 1 else [0, T // 2, T - 1]
+    res = run_and_check(cfg, layer, x, moe=moe, y_subset=subset)
+    print(f"config 4 T={T}: rel_l2={res['rel_l2']:.2e} touched={int((res['counts'] > 0).sum())}")
+
+
 def test_full_config3_prefill_parity(full_layers):
     cfg, layer, moe = full_layers(3)
     x = L.synth_x(cfg, 2048, seed=0, index=2048)
