@@ -107,10 +107,11 @@ __device__ __forceinline__ half8 dec8(uint32_t w0, uint32_t w1, half2v sc2, half
     return r;
 }
 
-// Per-row super-block header (d, dmin, 12 packed scale bytes) unpacked.
+// Per-row super-block header (d, dmin, 12 packed scale bytes) unpacked;
+// d2, dmin2: the scales of sub-blocks 4-7 in the split layout.
 struct Hdr {
     uint32_t sc03, sc47, m03, m47;
-    float d, dmin;
+    float d, dmin, d2, dmin2;
 };
 
 // get_scale_min_k4 (rust/src/kernels/mod.rs:54-63) for all 8 sub-blocks,
@@ -123,6 +124,15 @@ __device__ __forceinline__ Hdr unpack_hdr16(u32x4 h) {
     s.m47 = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
     s.d = dh2f(h.x & 0xffff);
     s.dmin = dh2f(h.x >> 16);
+    s.d2 = s.d;
+    s.dmin2 = s.dmin;
+    return s;
+}
+
+__device__ __forceinline__ Hdr unpack_hdr_split(u32x4 h, uint32_t db) {
+    Hdr s = unpack_hdr16(h);
+    s.d2 = dh2f(db & 0xffff);
+    s.dmin2 = dh2f(db >> 16);
     return s;
 }
 
@@ -230,23 +240,43 @@ __device__ __forceinline__ half4 min_operand16(const Hdr &s, int c4) {
 // header and, per unit u = 2p + s, 8 bytes of chunk 1 + u.
 struct WRaw {
     u32x4 hdr;
+    uint32_t db;  // split layout: the second (d, dmin)
     u32x2 q[8];
 };
 
+// Bytes per 64-row tile and super-block: nine 1 KiB chunks; the split
+// layout (rows whose length is an odd multiple of 128 columns, lcmoe_host.cpp)
+// adds the 64 rows' second (d, dmin) pair, 4 bytes each.
+template <bool SPLIT>
+constexpr int kTileSB = SPLIT ? 9 * 1024 + 256 : 9 * 1024;
+
 // Weight addressing: a wave-uniform base (the wave's row group, chunk 0 of
 // super-block 0) plus this lane's 32-bit row offset `lo`.
+template <bool SPLIT = false>
 __device__ __forceinline__ u32x4 load_hdr(g_u8 *base, uint32_t lo, int kb, int off = 0) {
-    return gload<u32x4>(base + (lo + (uint32_t)(kb * 9 * 1024 + off)));
+    return gload<u32x4>(base + (lo + (uint32_t)(kb * kTileSB<SPLIT> + off)));
 }
 
+template <bool SPLIT = false>
 __device__ __forceinline__ u32x2 load_q(g_u8 *base, uint32_t lo, int kb, int chunk, int off) {
-    return gload<u32x2>(base + (lo + (uint32_t)(kb * 9 * 1024 + chunk * 1024 + off)));
+    return gload<u32x2>(base + (lo + (uint32_t)(kb * kTileSB<SPLIT> + chunk * 1024 + off)));
 }
 
-__device__ __forceinline__ void load_w(WRaw &w, g_u8 *base, uint32_t lo, int kb, int h) {
-    w.hdr = load_hdr(base, lo, kb);
+// the second (d, dmin) of a split-layout row; dbo: the row's offset from
+// `base` into the pair area
+template <bool SPLIT>
+__device__ __forceinline__ uint32_t load_db(g_u8 *base, uint32_t dbo, int kb) {
+    if (!SPLIT) return 0;
+    return gload<uint32_t>(base + (dbo + (uint32_t)(kb * kTileSB<SPLIT>)));
+}
+
+template <bool SPLIT = false>
+__device__ __forceinline__ void load_w(WRaw &w, g_u8 *base, uint32_t lo, uint32_t dbo, int kb,
+                                       int h) {
+    w.hdr = load_hdr<SPLIT>(base, lo, kb);
+    w.db = load_db<SPLIT>(base, dbo, kb);
 #pragma unroll
-    for (int u = 0; u < 8; u++) w.q[u] = load_q(base, lo, kb, 1 + u, 8 * h);
+    for (int u = 0; u < 8; u++) w.q[u] = load_q<SPLIT>(base, lo, kb, 1 + u, 8 * h);
 }
 
 // Activation operands of one (pair p, k-step s) unit from the LDS stage:
@@ -291,6 +321,32 @@ __device__ __forceinline__ void finish_sb(const Hdr &hd, const half8 &amin, int 
     }
 }
 
+// The split layout's finish (sub-blocks 0-3 scaled by d, dmin; 4-7 by d2,
+// dmin2).  Mid-step, after sub-blocks 0-3: acc += d * S.  At the end:
+// acc += d2 * S and the min terms -dmin * SA - dmin2 * SB, computed as
+// (dmin2 - dmin) * SA - dmin2 * (SA + SB): SA from an MFMA whose lanes of
+// sub-blocks 4-7 supply zero mins, SA + SB from the unmasked MFMA, one
+// result live at a time.
+__device__ __forceinline__ void finish_first(const Hdr &hd, const float16v &S, float16v &acc) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[i] = __builtin_fmaf(hd.d, S[i], acc[i]);
+}
+
+__device__ __forceinline__ void finish_split(const Hdr &hd, const half8 &amin, int h,
+                                             const float16v &S, float16v &acc) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[i] = __builtin_fmaf(hd.d2, S[i], acc[i]);
+    const half8 mo = min_operand(hd, h);
+    const _Float16 k0 = h == 0 ? (_Float16)1.0f : (_Float16)0.0f;
+    const float16v SA = mfma32(amin, mo * k0, float16v{});
+    const float ddm = hd.dmin2 - hd.dmin;  // exact: two f16 values
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[i] = __builtin_fmaf(ddm, SA[i], acc[i]);
+    const float16v ST = mfma32(amin, mo, float16v{});
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[i] = __builtin_fmaf(-hd.dmin2, ST[i], acc[i]);
+}
+
 // Pipeline of a pass over super-blocks [kb0, kb1).  One register set of
 // weights: step k computes super-block k from it and from LDS stage k % 2,
 // and reloads each weight register with super-block k+1 right after its
@@ -305,10 +361,11 @@ __device__ __forceinline__ void finish_sb(const Hdr &hd, const half8 &amin, int 
 
 // One step of a 32-token pass: super-block k from `cur` and w; activations
 // of super-block kn into `nxt`; w reloaded with super-block kn.
-template <int MATS>
-__device__ __forceinline__ void step(g_u8 *const (&wb)[MATS], uint32_t lo, int kn,
-                                     const uint8_t *cur, uint8_t *nxt, const StageSrc &src,
-                                     WRaw (&w)[MATS], float16v (&acc)[MATS], int wave, int lane) {
+template <int MATS, bool SPLIT = false>
+__device__ __forceinline__ void step(g_u8 *const (&wb)[MATS], uint32_t lo,
+                                     const uint32_t (&dbo)[MATS], int kn, const uint8_t *cur,
+                                     uint8_t *nxt, const StageSrc &src, WRaw (&w)[MATS],
+                                     float16v (&acc)[MATS], int wave, int lane) {
     const int r = lane & 31, h = lane >> 5;
     StageRegs<8> act;
     stage_load(act, src, kn, wave, lane);
@@ -316,13 +373,15 @@ __device__ __forceinline__ void step(g_u8 *const (&wb)[MATS], uint32_t lo, int k
     Hdr hd[MATS];
 #pragma unroll
     for (int m = 0; m < MATS; m++) {
-        hd[m] = unpack_hdr16(w[m].hdr);
-        w[m].hdr = load_hdr(wb[m], lo, kn);
+        hd[m] = SPLIT ? unpack_hdr_split(w[m].hdr, w[m].db) : unpack_hdr16(w[m].hdr);
+        w[m].hdr = load_hdr<SPLIT>(wb[m], lo, kn);
+        w[m].db = load_db<SPLIT>(wb[m], dbo[m], kn);
     }
     float16v S[MATS];
 #pragma unroll
     for (int m = 0; m < MATS; m++) S[m] = float16v{};
     const uint8_t *tokrow = cur + r * kTokBytes;
+    const half8 *aminp = reinterpret_cast<const half8 *>(cur + kSumsOff + r * 32 + 16 * h);
     AUnit a[2];  // unit u's operands, and unit u+1's read ahead
     read_a(a[0], tokrow, 0, h);
 #pragma unroll
@@ -330,12 +389,24 @@ __device__ __forceinline__ void step(g_u8 *const (&wb)[MATS], uint32_t lo, int k
         if (u + 1 < 8) read_a(a[(u + 1) & 1], tokrow, u + 1, h);
         unit_mfma<MATS>(w, hd, u, a[u & 1], S);
 #pragma unroll
-        for (int m = 0; m < MATS; m++) w[m].q[u] = load_q(wb[m], lo, kn, 1 + u, 8 * h);
+        for (int m = 0; m < MATS; m++) w[m].q[u] = load_q<SPLIT>(wb[m], lo, kn, 1 + u, 8 * h);
+        if (SPLIT && u == 3) {  // sub-blocks 0-3 done: their own d
+#pragma unroll
+            for (int m = 0; m < MATS; m++) {
+                finish_first(hd[m], S[m], acc[m]);
+                S[m] = float16v{};
+            }
+        }
         __builtin_amdgcn_sched_barrier(0);  // bounds the live operands to two units
     }
-    const half8 amin = *reinterpret_cast<const half8 *>(cur + kSumsOff + r * 32 + 16 * h);
+    const half8 amin = *aminp;
 #pragma unroll
-    for (int m = 0; m < MATS; m++) finish_sb(hd[m], amin, h, S[m], acc[m]);
+    for (int m = 0; m < MATS; m++) {
+        if (SPLIT)
+            finish_split(hd[m], amin, h, S[m], acc[m]);
+        else
+            finish_sb(hd[m], amin, h, S[m], acc[m]);
+    }
     stage_store(nxt, act, wave, lane);
     lds_barrier();
 }
@@ -345,9 +416,10 @@ __shared__ __attribute__((aligned(1024))) uint8_t s_stage1[kStageBytes];
 
 // One pass of the block over super-blocks [kb0, kb1) for its 32 tokens.
 // wb[m]: the wave's row group of matrix m (uniform); lo: this lane's row offset.
-template <int MATS>
-__device__ __forceinline__ void block_pass(g_u8 *const (&wb)[MATS], uint32_t lo, int kb0,
-                                           int kb1, const StageSrc &src, float16v (&acc)[MATS]) {
+template <int MATS, bool SPLIT = false>
+__device__ __forceinline__ void block_pass(g_u8 *const (&wb)[MATS], uint32_t lo,
+                                           const uint32_t (&dbo)[MATS], int kb0, int kb1,
+                                           const StageSrc &src, float16v (&acc)[MATS]) {
     const int lane = threadIdx.x & 63, h = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int last = kb1 - 1;
@@ -358,15 +430,16 @@ __device__ __forceinline__ void block_pass(g_u8 *const (&wb)[MATS], uint32_t lo,
     StageRegs<8> act;
     stage_load(act, src, kb0, wave, lane);
 #pragma unroll
-    for (int m = 0; m < MATS; m++) load_w(w[m], wb[m], lo, kb0, h);
+    for (int m = 0; m < MATS; m++) load_w<SPLIT>(w[m], wb[m], lo, dbo[m], kb0, h);
     stage_store(s_stage0, act, wave, lane);
     lds_barrier();
     int kb = kb0;
     for (; kb + 2 <= kb1; kb += 2) {
-        step<MATS>(wb, lo, kb + 1, s_stage0, s_stage1, src, w, acc, wave, lane);
-        step<MATS>(wb, lo, min(kb + 2, last), s_stage1, s_stage0, src, w, acc, wave, lane);
+        step<MATS, SPLIT>(wb, lo, dbo, kb + 1, s_stage0, s_stage1, src, w, acc, wave, lane);
+        step<MATS, SPLIT>(wb, lo, dbo, min(kb + 2, last), s_stage1, s_stage0, src, w, acc, wave,
+                          lane);
     }
-    if (kb < kb1) step<MATS>(wb, lo, kb, s_stage0, s_stage1, src, w, acc, wave, lane);
+    if (kb < kb1) step<MATS, SPLIT>(wb, lo, dbo, kb, s_stage0, s_stage1, src, w, acc, wave, lane);
 }
 
 // ---- 16-token passes -------------------------------------------------------
@@ -375,22 +448,29 @@ __device__ __forceinline__ void block_pass(g_u8 *const (&wb)[MATS], uint32_t lo,
 // 32p + 8*c4 .. +7 of each pair p: chunk 1 + 2p + c4/2, byte 8*(c4 % 2).
 struct WRaw16 {
     u32x4 hdr[2];
-    u32x2 q[4][2];  // [pair][tile]
+    uint32_t db[2];  // split layout: the second (d, dmin) per tile
+    u32x2 q[4][2];   // [pair][tile]
 };
 
 // lo: offset of this lane's row r16 of tile 0; tile 1 is the 16 rows after
-// it, 256 bytes further in every chunk
+// it, 256 bytes further in every chunk (64 bytes further in the pair area)
+template <bool SPLIT = false>
 __device__ __forceinline__ u32x2 load_q16(g_u8 *base, uint32_t lo, int kb, int p, int t, int c4) {
-    return load_q(base, lo, kb, 1 + 2 * p + (c4 >> 1), 256 * t + 8 * (c4 & 1));
+    return load_q<SPLIT>(base, lo, kb, 1 + 2 * p + (c4 >> 1), 256 * t + 8 * (c4 & 1));
 }
 
-__device__ __forceinline__ void load_w16(WRaw16 &w, g_u8 *base, uint32_t lo, int kb, int c4) {
+template <bool SPLIT = false>
+__device__ __forceinline__ void load_w16(WRaw16 &w, g_u8 *base, uint32_t lo, uint32_t dbo, int kb,
+                                         int c4) {
 #pragma unroll
-    for (int t = 0; t < 2; t++) w.hdr[t] = load_hdr(base, lo, kb, 256 * t);
+    for (int t = 0; t < 2; t++) {
+        w.hdr[t] = load_hdr<SPLIT>(base, lo, kb, 256 * t);
+        w.db[t] = load_db<SPLIT>(base, dbo + 64 * t, kb);
+    }
 #pragma unroll
     for (int p = 0; p < 4; p++)
 #pragma unroll
-        for (int t = 0; t < 2; t++) w.q[p][t] = load_q16(base, lo, kb, p, t, c4);
+        for (int t = 0; t < 2; t++) w.q[p][t] = load_q16<SPLIT>(base, lo, kb, p, t, c4);
 }
 
 __device__ __forceinline__ void finish16(const Hdr &hd, const half4 &amin, int c4,
@@ -401,6 +481,20 @@ __device__ __forceinline__ void finish16(const Hdr &hd, const half4 &amin, int c
     for (int i = 0; i < 4; i++) {
         acc[i] = __builtin_fmaf(hd.d, S[i], acc[i]);
         acc[i] = __builtin_fmaf(-hd.dmin, Smin[i], acc[i]);
+    }
+}
+
+// finish16 for one half of a split-layout super-block: lanes c4 = 2 part,
+// 2 part + 1 hold that half's mins
+__device__ __forceinline__ void finish16_part(const Hdr &hd, const half4 &amin, int c4, int part,
+                                              const float4v &S, float4v &acc) {
+    const half4 mop = (c4 >> 1) == part ? min_operand16(hd, c4) : half4{};
+    const float4v Smin = __builtin_amdgcn_mfma_f32_16x16x16f16(amin, mop, float4v{}, 0, 0, 0);
+    const float dd = part ? hd.d2 : hd.d, dm = part ? hd.dmin2 : hd.dmin;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        acc[i] = __builtin_fmaf(dd, S[i], acc[i]);
+        acc[i] = __builtin_fmaf(-dm, Smin[i], acc[i]);
     }
 }
 
@@ -417,11 +511,11 @@ __device__ __forceinline__ void read_a16(AUnit &a, const uint8_t *tokrow, int p,
 // One step of a 16-token pass (same pipeline as step()).  Per pair p the
 // activations of sub-blocks 2p and 2p+1 (hi, lo) are read once and shared by
 // both tiles and all matrices.
-template <int MATS>
-__device__ __forceinline__ void step16(g_u8 *const (&wb)[MATS], uint32_t lo, int kn,
-                                       const uint8_t *cur, uint8_t *nxt, const StageSrc &src,
-                                       WRaw16 (&w)[MATS], float4v (&acc)[MATS][2], int wave,
-                                       int lane) {
+template <int MATS, bool SPLIT = false>
+__device__ __forceinline__ void step16(g_u8 *const (&wb)[MATS], uint32_t lo,
+                                       const uint32_t (&dbo)[MATS], int kn, const uint8_t *cur,
+                                       uint8_t *nxt, const StageSrc &src, WRaw16 (&w)[MATS],
+                                       float4v (&acc)[MATS][2], int wave, int lane) {
     const int r16 = lane & 15, c4 = lane >> 4;
     StageRegs<4> act;
     stage_load(act, src, kn, wave, lane);
@@ -431,13 +525,15 @@ __device__ __forceinline__ void step16(g_u8 *const (&wb)[MATS], uint32_t lo, int
     for (int m = 0; m < MATS; m++)
 #pragma unroll
         for (int t = 0; t < 2; t++) {
-            hd[m][t] = unpack_hdr16(w[m].hdr[t]);
-            w[m].hdr[t] = load_hdr(wb[m], lo, kn, 256 * t);
+            hd[m][t] = SPLIT ? unpack_hdr_split(w[m].hdr[t], w[m].db[t]) : unpack_hdr16(w[m].hdr[t]);
+            w[m].hdr[t] = load_hdr<SPLIT>(wb[m], lo, kn, 256 * t);
+            w[m].db[t] = load_db<SPLIT>(wb[m], dbo[m] + 64 * t, kn);
         }
     float4v S[MATS][2];
 #pragma unroll
     for (int m = 0; m < MATS; m++) S[m][0] = S[m][1] = float4v{};
     const uint8_t *tokrow = cur + r16 * kTokBytes;
+    const half4 *aminp = reinterpret_cast<const half4 *>(cur + kSumsOff + r16 * 32 + 8 * c4);
     AUnit a[2];  // pair p's operands, and pair p+1's read ahead
     read_a16(a[0], tokrow, 0, c4);
 #pragma unroll
@@ -450,29 +546,44 @@ __device__ __forceinline__ void step16(g_u8 *const (&wb)[MATS], uint32_t lo, int
             for (int t = 0; t < 2; t++) {
                 half8 blo, bhi;
                 dec_pair(hd[m][t], p, w[m].q[p][t].x, w[m].q[p][t].y, blo, bhi);
-                w[m].q[p][t] = load_q16(wb[m], lo, kn, p, t, c4);
+                w[m].q[p][t] = load_q16<SPLIT>(wb[m], lo, kn, p, t, c4);
                 S[m][t] = mfma16(h0, blo, S[m][t]);
                 S[m][t] = mfma16(l0, blo, S[m][t]);
                 S[m][t] = mfma16(h1, bhi, S[m][t]);
                 S[m][t] = mfma16(l1, bhi, S[m][t]);
             }
+        if (SPLIT && p == 1) {  // sub-blocks 0-3 done: their own d, dmin
+            const half4 amin = *aminp;
+#pragma unroll
+            for (int m = 0; m < MATS; m++)
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    finish16_part(hd[m][t], amin, c4, 0, S[m][t], acc[m][t]);
+                    S[m][t] = float4v{};
+                }
+        }
         __builtin_amdgcn_sched_barrier(0);  // bounds the live operands to two pairs
     }
-    const half4 amin = *reinterpret_cast<const half4 *>(cur + kSumsOff + r16 * 32 + 8 * c4);
+    const half4 amin = *aminp;
 #pragma unroll
     for (int m = 0; m < MATS; m++)
 #pragma unroll
-        for (int t = 0; t < 2; t++) finish16(hd[m][t], amin, c4, S[m][t], acc[m][t]);
+        for (int t = 0; t < 2; t++) {
+            if (SPLIT)
+                finish16_part(hd[m][t], amin, c4, 1, S[m][t], acc[m][t]);
+            else
+                finish16(hd[m][t], amin, c4, S[m][t], acc[m][t]);
+        }
     stage_store(nxt, act, wave, lane);
     lds_barrier();
 }
 
 // block_pass() for a pass of at most 16 tokens; lo is the offset of this
 // lane's row r16 of the wave's first tile
-template <int MATS>
+template <int MATS, bool SPLIT = false>
 __device__ __forceinline__ void block_pass16(g_u8 *const (&wb)[MATS], uint32_t lo,
-                                             int kb0, int kb1, const StageSrc &src,
-                                             float4v (&acc)[MATS][2]) {
+                                             const uint32_t (&dbo)[MATS], int kb0, int kb1,
+                                             const StageSrc &src, float4v (&acc)[MATS][2]) {
     const int lane = threadIdx.x & 63, c4 = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int last = kb1 - 1;
@@ -481,15 +592,17 @@ __device__ __forceinline__ void block_pass16(g_u8 *const (&wb)[MATS], uint32_t l
     StageRegs<4> act;
     stage_load(act, src, kb0, wave, lane);
 #pragma unroll
-    for (int m = 0; m < MATS; m++) load_w16(w[m], wb[m], lo, kb0, c4);
+    for (int m = 0; m < MATS; m++) load_w16<SPLIT>(w[m], wb[m], lo, dbo[m], kb0, c4);
     stage_store(s_stage0, act, wave, lane);
     lds_barrier();
     int kb = kb0;
     for (; kb + 2 <= kb1; kb += 2) {
-        step16<MATS>(wb, lo, kb + 1, s_stage0, s_stage1, src, w, acc, wave, lane);
-        step16<MATS>(wb, lo, min(kb + 2, last), s_stage1, s_stage0, src, w, acc, wave, lane);
+        step16<MATS, SPLIT>(wb, lo, dbo, kb + 1, s_stage0, s_stage1, src, w, acc, wave, lane);
+        step16<MATS, SPLIT>(wb, lo, dbo, min(kb + 2, last), s_stage1, s_stage0, src, w, acc, wave,
+                            lane);
     }
-    if (kb < kb1) step16<MATS>(wb, lo, kb, s_stage0, s_stage1, src, w, acc, wave, lane);
+    if (kb < kb1)
+        step16<MATS, SPLIT>(wb, lo, dbo, kb, s_stage0, s_stage1, src, w, acc, wave, lane);
 }
 
 // split v into f16 hi + lo
@@ -535,7 +648,9 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
     const int64_t grpoff = (int64_t)tile * NB * 9 * 1024 + 32 * (grp & 1) * 16;
     g_u8 *const wb[2] = {uniform(gate + (int64_t)e * estride + grpoff),
                                   uniform(up + (int64_t)e * estride + grpoff)};
-    const int f = grp * 32 + r, nkb = F >> 8;
+    // H rows: ceil(F / 256) pieces and 8 sums per piece (zero past F)
+    const int f = grp * 32 + r, nkb = (F + 255) >> 8, hsr = nkb * 8;
+    const uint32_t nodb[2] = {0, 0};
     const uint8_t *xb = reinterpret_cast<const uint8_t *>(x16);
     const uint8_t *sb = reinterpret_cast<const uint8_t *>(xs);
     for (int c = blockIdx.z * kTok; c < n; c += gridDim.z * kTok) {
@@ -551,7 +666,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
         if (n - c <= 16) {
             const int r16 = lane & 15, c4 = lane >> 4;
             float4v acc[2][2] = {};
-            block_pass16<2>(wb, r16 * 16, 0, NB, src, acc);
+            block_pass16<2>(wb, r16 * 16, nodb, 0, NB, src, acc);
             if (grp0 >= ngrp) continue;
             // output addresses are formed here from an opaque row index, so
             // that the compiler does not keep them live across the pass
@@ -585,15 +700,15 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
                     if (h16 && r16 == 0) {
                         _Float16 shi, slo;
                         split16(part, shi, slo);
-                        hs[(p * (F >> 5) + grp) * 2] = shi;
-                        hs[(p * (F >> 5) + grp) * 2 + 1] = slo;
+                        hs[(p * hsr + grp) * 2] = shi;
+                        hs[(p * hsr + grp) * 2 + 1] = slo;
                     }
                 }
             }
             continue;
         }
         float16v acc[2] = {float16v{}, float16v{}};
-        block_pass<2>(wb, r * 16, 0, NB, src, acc);
+        block_pass<2>(wb, r * 16, nodb, 0, NB, src, acc);
         if (grp0 >= ngrp) continue;
         int fo = f;  // opaque copy: output addresses are formed here (see above)
         asm volatile("" : "+v"(fo));
@@ -617,8 +732,8 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
                     if (r == 0) {
                         _Float16 shi, slo;
                         split16(part, shi, slo);
-                        hs[(p * (F >> 5) + grp) * 2] = shi;
-                        hs[(p * (F >> 5) + grp) * 2 + 1] = slo;
+                        hs[(p * hsr + grp) * 2] = shi;
+                        hs[(p * hsr + grp) * 2 + 1] = slo;
                     }
                 }
             }
@@ -630,7 +745,9 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
 // group.  Partial sums of K split z go to Y + z * split_stride.  A wave owns
 // one 64-row RPL tile as two 32-row halves that share every activation read
 // (the two "matrices" of the pipeline), so each LDS read feeds twice the
-// weight bytes of a 32-row wave.
+// weight bytes of a 32-row wave.  SPLIT: F is an odd multiple of 128 and the
+// weights are in the split layout (ceil(F / 256) super-blocks per row).
+template <bool SPLIT>
 __global__ __launch_bounds__(256, 2) void k_mfma_down(
     const uint8_t *__restrict__ down, int64_t estride, const _Float16 *__restrict__ h16,
     const _Float16 *__restrict__ hs, SlotArgs sa, int d, int F, int ksplit, float *__restrict__ Y,
@@ -658,10 +775,10 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down(
     const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
     const int ntile = d >> 6, tile0 = bx * kWaves + wave;
     const int tile = min(tile0, ntile - 1);  // duplicate the last tile past the end
-    const int NB = F >> 8, nsb = F >> 5;
+    const int NB = (F + 255) >> 8, nsb = NB * 8;
     const int kb0 = (int)((int64_t)NB * bz / ksplit);
     const int kb1 = (int)((int64_t)NB * (bz + 1) / ksplit);
-    const uint8_t *tb = down + (int64_t)e * estride + (int64_t)tile * NB * 9 * 1024;
+    const uint8_t *tb = down + (int64_t)e * estride + (int64_t)tile * NB * kTileSB<SPLIT>;
     g_u8 *const wb[2] = {uniform(tb), uniform(tb + 32 * 16)};
     float *Yz = Y + (int64_t)bz * split_stride;
     const uint8_t *hb = reinterpret_cast<const uint8_t *>(h16);
@@ -670,13 +787,17 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down(
         StageSrc src;
 #pragma unroll
         for (int i = 0; i < 8; i++)
-            src.tok[i] = uniform(hb + (int64_t)(p0 + min(c + wave + 4 * i, n - 1)) * F * 4);
+            src.tok[i] = uniform(hb + (int64_t)(p0 + min(c + wave + 4 * i, n - 1)) * NB * 1024);
         src.sums = uniform(sb);
         src.soff = (uint32_t)(p0 + min(c + (lane >> 1), n - 1)) * nsb * 4 + 16 * (lane & 1);
         if (n - c <= 16) {
             const int r16 = lane & 15, c4 = lane >> 4;
+            // pair-area offsets of rows r16 (half 0) and 32 + r16 (half 1),
+            // from each half's base
+            const uint32_t dbo[2] = {9 * 1024 + 4 * (uint32_t)r16,
+                                     9 * 1024 + 4 * (32 + (uint32_t)r16) - 32 * 16};
             float4v acc[2][2] = {};
-            block_pass16<2>(wb, r16 * 16, kb0, kb1, src, acc);
+            block_pass16<2, SPLIT>(wb, r16 * 16, dbo, kb0, kb1, src, acc);
             if (tile0 >= ntile) continue;
             int rb = tile * 64 + r16;  // opaque: output addresses are formed here
             asm volatile("" : "+v"(rb));
@@ -693,8 +814,10 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down(
             }
             continue;
         }
+        const uint32_t dbo[2] = {9 * 1024 + 4 * (uint32_t)r,
+                                 9 * 1024 + 4 * (32 + (uint32_t)r) - 32 * 16};
         float16v acc[2] = {float16v{}, float16v{}};
-        block_pass<2>(wb, r * 16, kb0, kb1, src, acc);
+        block_pass<2, SPLIT>(wb, r * 16, dbo, kb0, kb1, src, acc);
         if (tile0 >= ntile) continue;
         int rb = tile * 64 + r;  // opaque: output addresses are formed here
         asm volatile("" : "+v"(rb));
@@ -1039,9 +1162,14 @@ hipError_t launch_mfma_down(const uint8_t *down, int64_t estride, const _Float16
                             hipStream_t st) {
     const int tiles = d / 64;
     if (chunks < 1 || ksplit < 1 || (int64_t)chunks * ksplit > 65535) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_mfma_down, dim3((tiles + kWaves - 1) / kWaves, slots, ksplit * chunks),
-                       dim3(256), 0, st, down, estride, h16, hs, dev_slots(sa), d, F, ksplit, Y,
-                       split_stride);
+    if (F % 128) return hipErrorInvalidValue;
+    const dim3 grid((tiles + kWaves - 1) / kWaves, slots, ksplit * chunks);
+    if (F % 256)
+        hipLaunchKernelGGL(k_mfma_down<true>, grid, dim3(256), 0, st, down, estride, h16, hs,
+                           dev_slots(sa), d, F, ksplit, Y, split_stride);
+    else
+        hipLaunchKernelGGL(k_mfma_down<false>, grid, dim3(256), 0, st, down, estride, h16, hs,
+                           dev_slots(sa), d, F, ksplit, Y, split_stride);
     return hipGetLastError();
 }
 

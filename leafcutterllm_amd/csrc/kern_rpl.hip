@@ -219,18 +219,19 @@ __device__ __forceinline__ void gateup_chunk(const uint4 *G, const uint4 *U, int
                 out.m[p * (F >> 5) + (f >> 5)] = sum;
             }
         }
-        if (out.h16) {
+        if (out.h16) {  // rows of ceil(F / 256) pieces, 8 sums per piece
+            const int nkb = (F + 255) >> 8;
             const _Float16 hi = (_Float16)h, lo = (_Float16)(h - (float)hi);
             float part = (float)hi + (float)lo;
 #pragma unroll
             for (int off = 1; off < 32; off <<= 1) part += __shfl_xor(part, off, 64);
-            _Float16 *piece = out.h16 + (p * (F >> 8) + (f >> 8)) * 512 + (f & 255);
+            _Float16 *piece = out.h16 + (p * nkb + (f >> 8)) * 512 + (f & 255);
             piece[0] = hi;
             piece[256] = lo;
             if ((lane & 31) == 0) {
                 const _Float16 shi = (_Float16)part, slo = (_Float16)(part - (float)shi);
-                out.hs16[(p * (F >> 5) + (f >> 5)) * 2] = shi;
-                out.hs16[(p * (F >> 5) + (f >> 5)) * 2 + 1] = slo;
+                out.hs16[(p * nkb * 8 + (f >> 5)) * 2] = shi;
+                out.hs16[(p * nkb * 8 + (f >> 5)) * 2 + 1] = slo;
             }
         }
     }

@@ -41,8 +41,9 @@ constexpr int64_t kFastRouterElems = (int64_t)1 << 24;
 struct ExpertSet {  // one family of experts (routed or shared)
     int n = 0, F = 0, qt_gu = 0, qt_dn = 0;
     // RPL64 Q4_K gate/up; RPL64 Q4_K down (row-per-lane and matrix-core);
-    // RPL64 Q6_K down (matrix-core only)
-    bool rpl_gu = false, rpl_dn = false, q6_dn = false;
+    // RPL64 Q6_K down and split-layout Q4_K down (F an odd multiple of 128),
+    // both matrix-core only
+    bool rpl_gu = false, rpl_dn = false, q6_dn = false, split_dn = false;
     uint8_t *gate = nullptr, *up = nullptr, *down = nullptr;
     int64_t sz_gu = 0, sz_dn = 0;
     // H between the two products: f32 (generic down), int8 limbs (row-per-lane
@@ -113,21 +114,30 @@ lcmoe_status alloc_n(lcmoe_handle *h, T **dst, size_t n) {
 }
 
 // Uploads n stacked expert matrices [rows, cols] of type qt, repacking each
-// to RPL64 (Q4_K or Q6_K, by qt) when `rpl` (one expert at a time through a
-// host staging buffer).
+// to RPL64 (Q4_K or Q6_K, by qt) when `rpl`, or to the split Q4_K layout
+// when `split` (one expert at a time through a host staging buffer).
+// *sz_out: device bytes per expert.
 lcmoe_status upload_stack(lcmoe_handle *h, uint8_t **dst, const uint8_t *src, int n, int qt,
-                          int64_t rows, int64_t cols, bool rpl, int64_t *sz_out) {
+                          int64_t rows, int64_t cols, bool rpl, int64_t *sz_out,
+                          bool split = false) {
     const int64_t sz = (int64_t)lcmoe_tensor_size(qt, rows * cols);
-    *sz_out = sz;
-    lcmoe_status st = alloc_n(h, dst, (size_t)sz * n);
+    const int64_t dsz = split ? rows / 64 * ((cols + 255) / 256) * (9 * 1024 + 256) : sz;
+    *sz_out = dsz;
+    lcmoe_status st = alloc_n(h, dst, (size_t)dsz * n);
     if (st) return st;
-    if (!rpl) {
+    if (!rpl && !split) {
         HIP_TRY(hipMemcpy(*dst, src, (size_t)sz * n, hipMemcpyHostToDevice));
         return LCMOE_OK;
     }
-    std::vector<uint8_t> buf((size_t)sz);
+    std::vector<uint8_t> buf((size_t)dsz);
     for (int e = 0; e < n; e++) {
         const uint8_t *s = src + (size_t)e * sz;
+        if (split) {  // straddling blocks: one thread (the layout reads across rows)
+            repack_rpl64_q4k_split(s, buf.data(), rows, cols);
+            HIP_TRY(hipMemcpy(*dst + (size_t)e * dsz, buf.data(), (size_t)dsz,
+                              hipMemcpyHostToDevice));
+            continue;
+        }
         // repack 64-row tiles in parallel
         const int64_t tiles = rows / 64;
         unsigned nth = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
@@ -201,8 +211,8 @@ int choose_ksplit(const ExpertSet &s, int d, int active) {
 // Matrix-core down: 256-row blocks, two resident per CU; split K until
 // about two blocks per CU exist, keeping >= 4 super-blocks per split.
 int choose_ksplit_mfma(const ExpertSet &s, int d, int active) {
-    if (!s.rpl_dn && !s.q6_dn) return 1;
-    const int NB = s.F / 256, blocks = ((d / 64 + 3) / 4) * std::max(1, active);
+    if (!s.rpl_dn && !s.q6_dn && !s.split_dn) return 1;
+    const int NB = (s.F + 255) / 256, blocks = ((d / 64 + 3) / 4) * std::max(1, active);
     int ks = 1;
     while (ks < s.kmax && blocks * ks < 512 && NB >= 4 * ks * 2) ks *= 2;
     return ks;
@@ -219,24 +229,31 @@ lcmoe_status setup_set(lcmoe_handle *h, ExpertSet &s, int n, int F, int qgu, int
     s.rpl_gu = rpl64_ok(qgu, F, d);
     s.rpl_dn = s.rpl_gu && rpl64_ok(qdn, d, F);
     s.q6_dn = s.rpl_gu && rpl64_q6_ok(qdn, d, F);
-    s.kmax = s.rpl_dn || s.q6_dn ? kMaxKSplit : 1;
+    s.split_dn = s.rpl_gu && qdn == LCMOE_TYPE_Q4_K && d % 64 == 0 && F % 256 == 128;
+    s.kmax = s.rpl_dn || s.q6_dn || s.split_dn ? kMaxKSplit : 1;
     int64_t szu = 0;
     lcmoe_status st;
     if ((st = upload_stack(h, &s.gate, gate, n, qgu, F, d, s.rpl_gu, &s.sz_gu))) return st;
     if ((st = upload_stack(h, &s.up, up, n, qgu, F, d, s.rpl_gu, &szu))) return st;
-    if ((st = upload_stack(h, &s.down, down, n, qdn, d, F, s.rpl_dn || s.q6_dn, &s.sz_dn)))
+    if ((st = upload_stack(h, &s.down, down, n, qdn, d, F, s.rpl_dn || s.q6_dn, &s.sz_dn,
+                           s.split_dn)))
         return st;
     if (s.rpl_dn) {
         if ((st = alloc_n(h, &s.hh, positions * F))) return st;
         if ((st = alloc_n(h, &s.hl, positions * F))) return st;
         if ((st = alloc_n(h, &s.hs, positions * F / 32))) return st;
         if ((st = alloc_n(h, &s.hm, positions * F / 32))) return st;
-    } else if (!s.q6_dn) {
+    } else if (!s.q6_dn && !s.split_dn) {
         if ((st = alloc_n(h, &s.Hf, positions * F))) return st;
     }
     if (s.rpl_gu) {
-        if ((st = alloc_n(h, &s.h16, 2 * positions * F))) return st;
-        if ((st = alloc_n(h, &s.h16s, positions * F / 16))) return st;
+        // ceil(F / 256) pieces of 512 halves and 8 sum pairs per piece per
+        // position; the part past F is never written and stays zero
+        const int64_t nkb = (F + 255) / 256;
+        if ((st = alloc_n(h, &s.h16, positions * nkb * 512))) return st;
+        if ((st = alloc_n(h, &s.h16s, positions * nkb * 16))) return st;
+        HIP_TRY(hipMemset(s.h16, 0, sizeof(_Float16) * positions * nkb * 512));
+        HIP_TRY(hipMemset(s.h16s, 0, sizeof(_Float16) * positions * nkb * 16));
     }
     return alloc_n(h, &s.Y, (size_t)s.kmax * positions * d);
 }
@@ -358,8 +375,9 @@ static Plan plan_set(lcmoe_handle *h, const ExpertSet &s, bool shared, int T) {
     // passes per block)
     const int64_t per_slot = shared ? T : ((int64_t)T * D.n_expert_used + p.slots - 1) / p.slots;
     p.chunks = p.mfma ? (int)std::min<int64_t>(64, std::max<int64_t>(1, (per_slot + 31) / 32)) : 1;
-    p.ks = (p.mfma && s.rpl_dn) || s.q6_dn ? choose_ksplit_mfma(s, D.d_model, p.slots * p.chunks)
-                                            : choose_ksplit(s, D.d_model, p.slots);
+    p.ks = (p.mfma && s.rpl_dn) || s.q6_dn || s.split_dn
+               ? choose_ksplit_mfma(s, D.d_model, p.slots * p.chunks)
+               : choose_ksplit(s, D.d_model, p.slots);
     return p;
 }
 
@@ -369,7 +387,8 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
     const int d = D.d_model, K = D.n_expert_used, E = D.n_expert;
     SlotArgsHost sa{h->perm, h->counts, h->offsets, h->touched, E, K, T, shared ? 1 : 0};
     // H between the products in the form the down kernel reads
-    const bool h16_out = (pl.mfma && s.rpl_dn) || s.q6_dn;
+    const bool mfma_dn_only = s.q6_dn || s.split_dn;
+    const bool h16_out = (pl.mfma && s.rpl_dn) || mfma_dn_only;
     HIP_TRY(timed(h, st, shared ? kSlotGateUpSh : kSlotGateUp, [&] {
         if (pl.mfma)
             return launch_mfma_gateup(s.gate, s.up, s.sz_gu, h->x16, h->x16s, sa, pl.slots,
@@ -378,7 +397,7 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
         if (s.rpl_gu)
             return launch_rpl_gateup(s.gate, s.up, s.sz_gu, h->xh, h->xl, h->xs, h->xm, sa,
                                      pl.slots, d, s.F, s.Hf, s.rpl_dn ? s.hh : nullptr, s.hl,
-                                     s.hs, s.hm, s.q6_dn ? s.h16 : nullptr, s.h16s, ch, st);
+                                     s.hs, s.hm, mfma_dn_only ? s.h16 : nullptr, s.h16s, ch, st);
         return launch_generic_gateup(s.qt_gu, s.gate, s.up, s.sz_gu, x, sa, pl.slots, d, s.F,
                                      s.Hf, nullptr, nullptr, nullptr, nullptr, ch, st);
     }));
@@ -386,7 +405,7 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
         if (s.q6_dn)
             return launch_mfma_down_q6(s.down, s.sz_dn, s.h16, sa, pl.slots, pl.chunks, d, s.F,
                                        pl.ks, s.Y, s.positions * d, st);
-        if (s.rpl_dn && pl.mfma)
+        if (s.split_dn || (s.rpl_dn && pl.mfma))
             return launch_mfma_down(s.down, s.sz_dn, s.h16, s.h16s, sa, pl.slots, pl.chunks, d,
                                     s.F, pl.ks, s.Y, s.positions * d, st);
         if (s.rpl_dn)

@@ -307,6 +307,66 @@ void repack_rpl64_q4k(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t co
             }
 }
 
+// The 6-bit scales and mins of a Q4_K block's 12 packed bytes
+// (get_scale_min_k4, rust/src/kernels/mod.rs:54-63), and the inverse.
+static void unpack_scales_k4(const uint8_t *q, uint8_t sc[8], uint8_t m[8]) {
+    for (int j = 0; j < 4; j++) {
+        sc[j] = q[j] & 63;
+        m[j] = q[j + 4] & 63;
+    }
+    for (int j = 4; j < 8; j++) {
+        sc[j] = (uint8_t)((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+        m[j] = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+    }
+}
+
+static void pack_scales_k4(const uint8_t sc[8], const uint8_t m[8], uint8_t *q) {
+    for (int j = 0; j < 4; j++) {
+        q[j] = (uint8_t)(sc[j] | ((sc[j + 4] >> 4) << 6));
+        q[j + 4] = (uint8_t)(m[j] | ((m[j + 4] >> 4) << 6));
+        q[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((m[j + 4] & 0xF) << 4));
+    }
+}
+
+// Split repack of a GGUF Q4_K [rows, cols] matrix with cols an odd multiple
+// of 128, whose 256-element blocks straddle rows: each row gets
+// ceil(cols / 256) virtual super-blocks of its own columns 256 kb .. +255.
+// A virtual block's halves (sub-blocks 0-3 and 4-7) are half blocks of the
+// original (the first or second half of one block each; a half past the row
+// end is zero).  Its header holds the first half's (d, dmin) and the eight
+// (scale, min) pairs packed as in Q4_K; its qs are the halves' qs bytes (a
+// half is two 32-byte pairs of qs); the second half's (d, dmin) goes to a
+// 4-byte entry per row after the nine 1 KiB chunks of the RPL64 layout:
+// 9,472 bytes per 64-row tile and virtual block.  The decoded values are the
+// original ones, with zeros past the row end.
+void repack_rpl64_q4k_split(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t cols) {
+    const int64_t NB = (cols + 255) / 256, tb = 9 * 1024 + 256;
+    for (int64_t rt = 0; rt < rows / 64; rt++)
+        for (int64_t kb = 0; kb < NB; kb++) {
+            uint8_t *o = dst + (rt * NB + kb) * tb;
+            for (int r = 0; r < 64; r++) {
+                uint8_t vb[144] = {0}, db[4] = {0}, sc[8] = {0}, mm[8] = {0};
+                for (int part = 0; part < 2; part++) {
+                    const int64_t c0 = 256 * kb + 128 * part;
+                    if (c0 >= cols) break;
+                    const int64_t e = (rt * 64 + r) * cols + c0, half = (e % 256) / 128;
+                    const uint8_t *blk = src + (e / 256) * 144;
+                    uint8_t bs[8], bm[8];
+                    unpack_scales_k4(blk + 4, bs, bm);
+                    for (int k = 0; k < 4; k++) {
+                        sc[4 * part + k] = bs[4 * half + k];
+                        mm[4 * part + k] = bm[4 * half + k];
+                    }
+                    std::memcpy(vb + 16 + 64 * part, blk + 16 + 64 * half, 64);
+                    std::memcpy(part ? db : vb, blk, 4);
+                }
+                pack_scales_k4(sc, mm, vb + 4);
+                for (int c = 0; c < 9; c++) std::memcpy(o + c * 1024 + r * 16, vb + c * 16, 16);
+                std::memcpy(o + 9 * 1024 + r * 4, db, 4);
+            }
+        }
+}
+
 // RPL64 repack of a GGUF Q6_K [rows, cols] matrix (rows % 64 == 0,
 // cols % 256 == 0): per 64-row tile and super-block, the 210-byte blocks of
 // the 64 rows are cut into thirteen 16-byte chunks (ql: 0-7, qh: 8-11,

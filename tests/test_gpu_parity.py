@@ -72,6 +72,12 @@ SMALL = {
     "e60-tail": small_config("e60", 256, 256, 60, 4, L.ROUTE_SOFTMAX, Q4, Q4),
     "q6k-all": small_config("q6", 512, 512, 16, 8, L.ROUTE_SOFTMAX_RENORM, Q6, Q6),
     "f32": small_config("f32", 128, 256, 4, 2, L.ROUTE_SOFTMAX_RENORM, L.TYPE_F32, L.TYPE_F32),
+    # d_ff an odd multiple of 128: Q4_K down blocks straddle rows (split layout)
+    "q4k-split-shared": small_config(
+        "split", 256, 384, 8, 2, L.ROUTE_SOFTMAX_RENORM, Q4, Q4, n_shared=2, d_ff_shared=640),
+    # Q6_K down with a 4-way column split and 4 shared experts
+    "q6k-down-e16": small_config(
+        "q6dn", 512, 1024, 16, 4, L.ROUTE_SOFTMAX, Q4, Q6, n_shared=1, d_ff_shared=512),
 }
 
 
