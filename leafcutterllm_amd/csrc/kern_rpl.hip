@@ -160,6 +160,106 @@ __device__ __forceinline__ void pass1(const uint4 *__restrict__ W, int kb0, int 
     if (kb < kb1) dot_sb<NT>(c0, kb, X, row, acc);
 }
 
+// ---- Q6_K down in the RPL64 Q6_K layout -----------------------------------
+// Per 64-row tile and super-block: thirteen chunks of 64 rows x 16 bytes (ql
+// in 0-7, qh in 8-11, the 16 int8 scales in 12), then the rows' f16 d; 840
+// uint4 in all.  Element 128n + 32j + l (l < 32) of a row's block has the
+// code q = (ql nibble) | (qh bits 2j, 2j+1) << 4 with the nibble the low (j
+// < 2) or high half of ql[64n + 32(j & 1) + l] and the qh byte qh[32n + l],
+// and the value d * sc[8n + 2j + l/16] * (q - 32) (dequantize_q6_k,
+// rust/src/kernels/mod.rs:145-180).  Per 16-element scale group the integer
+// sum sc * sum (q - 32) (128 hi + lo) is exact in int32 (|.| <= 2^30.99 for a
+// 32-element sub-block).
+constexpr int kQ6Uint4 = (13 * 1024 + 128) / 16;
+
+struct Q6Regs {
+    uint4 c[13];
+    uint32_t d;
+};
+
+__device__ __forceinline__ void load_q6(Q6Regs &w, const uint4 *W, const uint16_t *D, int kb) {
+    const uint4 *p = W + (int64_t)kb * kQ6Uint4;
+#pragma unroll
+    for (int i = 0; i < 13; i++) w.c[i] = p[i * 64];
+    w.d = D[(int64_t)kb * (kQ6Uint4 * 8)];
+}
+
+// q - 32 of four 6-bit codes (one per byte) as signed bytes
+__device__ __forceinline__ int q6_signed(uint32_t q) {
+    const uint32_t v = q ^ 0x20202020u, b = v & 0x20202020u;
+    return (int)(v | (b << 1) | (b << 2));
+}
+
+template <int NT>
+__device__ __forceinline__ void q6_block_dot(const Q6Regs &w, const int *const (&xh)[NT],
+                                             const int *const (&xl)[NT],
+                                             const float *const (&xs)[NT], float (&acc)[NT]) {
+    const float d = dh2f(w.d & 0xffff);
+    const uint32_t scw[4] = {w.c[12].x, w.c[12].y, w.c[12].z, w.c[12].w};
+#pragma unroll
+    for (int n = 0; n < 2; n++) {
+        const uint4 ha = w.c[8 + 2 * n], hb = w.c[9 + 2 * n];
+        const uint32_t qh[8] = {ha.x, ha.y, ha.z, ha.w, hb.x, hb.y, hb.z, hb.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint4 qa = w.c[4 * n + 2 * (j & 1)], qb = w.c[4 * n + 2 * (j & 1) + 1];
+            const uint32_t ql[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+            int sq[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint32_t nib = j < 2 ? ql[i] & 0x0F0F0F0Fu : (ql[i] >> 4) & 0x0F0F0F0Fu;
+                const uint32_t hi2 = ((qh[i] >> (2 * j)) & 0x03030303u) << 4;
+                sq[i] = q6_signed(nib | hi2);
+            }
+            const int sb = 4 * n + j, k0 = 8 * n + 2 * j;
+            const int s0 = (int)(int8_t)(scw[k0 >> 2] >> (8 * (k0 & 3)));
+            const int s1 = (int)(int8_t)(scw[(k0 + 1) >> 2] >> (8 * ((k0 + 1) & 3)));
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                const int *ph = xh[t] + 8 * sb, *pl = xl[t] + 8 * sb;
+                int h0 = 0, l0 = 0, h1 = 0, l1 = 0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    h0 = __builtin_amdgcn_sdot4(sq[i], ph[i], h0, false);
+                    l0 = __builtin_amdgcn_sdot4(sq[i], pl[i], l0, false);
+                    h1 = __builtin_amdgcn_sdot4(sq[4 + i], ph[4 + i], h1, false);
+                    l1 = __builtin_amdgcn_sdot4(sq[4 + i], pl[4 + i], l1, false);
+                }
+                const int isb = (h0 * 128 + l0) * s0 + (h1 * 128 + l1) * s1;
+                acc[t] = __builtin_fmaf(d * xs[t][sb], (float)isb, acc[t]);
+            }
+        }
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void dot_sb_q6(const Q6Regs &w, int kb, const Limbs &X,
+                                          const int (&row)[NT], float (&acc)[NT]) {
+    const int *xh[NT], *xl[NT];
+    const float *xs[NT], *xm[NT];
+    token_ptrs<NT>(X, row, kb, xh, xl, xs, xm);
+    q6_block_dot<NT>(w, xh, xl, xs, acc);
+}
+
+// pass1() for Q6_K: two register sets, the next super-block loading while
+// the current one is computed
+template <int NT>
+__device__ __forceinline__ void pass1_q6(const uint4 *__restrict__ W, const uint16_t *D, int kb0,
+                                         int kb1, const Limbs &X, const int (&row)[NT],
+                                         float (&acc)[NT]) {
+    if (kb0 >= kb1) return;
+    Q6Regs c0, c1;
+    load_q6(c0, W, D, kb0);
+    int kb = kb0;
+    for (; kb + 2 <= kb1; kb += 2) {
+        load_q6(c1, W, D, kb + 1);
+        dot_sb_q6<NT>(c0, kb, X, row, acc);
+        load_q6(c0, W, D, min(kb + 2, kb1 - 1));
+        dot_sb_q6<NT>(c1, kb + 1, X, row, acc);
+    }
+    if (kb < kb1) dot_sb_q6<NT>(c0, kb, X, row, acc);
+}
+
 struct HOut {
     float *f;       // H f32 [positions, F] or null
     int8_t *h, *l;  // H limbs [positions, F] or null
@@ -295,10 +395,11 @@ __global__ __launch_bounds__(256) void k_rpl_gateup(
     }
 }
 
-template <int NT>
-__device__ __forceinline__ void down_chunk(const uint4 *W, int kb0, int kb1, const Limbs &X,
-                                           int p0, int n, int c, int d, int r, float *Y,
-                                           float (*s_red)[kMaxNT][64]) {
+// Q6: Q6_K weights (D: the rows' d) instead of Q4_K
+template <int NT, bool Q6>
+__device__ __forceinline__ void down_chunk(const uint4 *W, const uint16_t *D, int kb0, int kb1,
+                                           const Limbs &X, int p0, int n, int c, int d, int r,
+                                           float *Y, float (*s_red)[kMaxNT][64]) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     int row[NT];
 #pragma unroll
@@ -306,7 +407,10 @@ __device__ __forceinline__ void down_chunk(const uint4 *W, int kb0, int kb1, con
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) acc[t] = 0.0f;
-    pass1<NT>(W, kb0, kb1, X, row, acc);
+    if constexpr (Q6)
+        pass1_q6<NT>(W, D, kb0, kb1, X, row, acc);
+    else
+        pass1<NT>(W, kb0, kb1, X, row, acc);
 #pragma unroll
     for (int t = 0; t < NT; t++) s_red[wave][t][lane] = acc[t];
     __syncthreads();
@@ -322,6 +426,9 @@ __device__ __forceinline__ void down_chunk(const uint4 *W, int kb0, int kb1, con
 // grid (d/64 tiles, slots, ksplit): block z covers super-block slices
 // 4z .. 4z+3 of the 4*ksplit slices of the F dimension; its partial row sums
 // go to Y + z * split_stride and the combine adds the splits in order.
+// Q6: RPL64 Q6_K weights (840 uint4 per tile and super-block) instead of
+// RPL64 Q4_K (576).
+template <bool Q6>
 __global__ __launch_bounds__(256) void k_rpl_down(
     const uint8_t *__restrict__ down, int64_t estride, const int8_t *__restrict__ xh,
     const int8_t *__restrict__ xl, const float *__restrict__ xs, const float *__restrict__ xm,
@@ -337,18 +444,21 @@ __global__ __launch_bounds__(256) void k_rpl_down(
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int slices = kWaves * gridDim.z, s = blockIdx.z * kWaves + wave;
     const int kb0 = (int)((int64_t)NB * s / slices), kb1 = (int)((int64_t)NB * (s + 1) / slices);
-    const uint4 *W = reinterpret_cast<const uint4 *>(down + (int64_t)e * estride) +
-                     (int64_t)rt * NB * 9 * 64 + lane;
+    const int tsb = Q6 ? kQ6Uint4 : 9 * 64;  // uint4 per tile and super-block
+    const uint4 *T = reinterpret_cast<const uint4 *>(down + (int64_t)e * estride) +
+                     (int64_t)rt * NB * tsb;
+    const uint4 *W = T + lane;
+    const uint16_t *D = reinterpret_cast<const uint16_t *>(T + 13 * 64) + lane;
     float *Yz = Y + (int64_t)blockIdx.z * split_stride;
     const int r = rt * 64 + lane;
     for (int c = 0; c < n; c += kMaxNT) {
         const int left = n - c;
         if (left > 2)
-            down_chunk<4>(W, kb0, kb1, X, p0, n, c, d, r, Yz, s_red);
+            down_chunk<4, Q6>(W, D, kb0, kb1, X, p0, n, c, d, r, Yz, s_red);
         else if (left == 2)
-            down_chunk<2>(W, kb0, kb1, X, p0, n, c, d, r, Yz, s_red);
+            down_chunk<2, Q6>(W, D, kb0, kb1, X, p0, n, c, d, r, Yz, s_red);
         else
-            down_chunk<1>(W, kb0, kb1, X, p0, n, c, d, r, Yz, s_red);
+            down_chunk<1, Q6>(W, D, kb0, kb1, X, p0, n, c, d, r, Yz, s_red);
     }
 }
 
@@ -374,10 +484,14 @@ hipError_t launch_rpl_gateup(const uint8_t *gate, const uint8_t *up, int64_t est
 hipError_t launch_rpl_down(const uint8_t *down, int64_t estride, const int8_t *hh,
                            const int8_t *hl, const float *hs, const float *hm,
                            const SlotArgsHost &sa, int slots, int d, int F, int ksplit, float *Y,
-                           int64_t split_stride, hipStream_t st) {
+                           int64_t split_stride, hipStream_t st, bool q6) {
     SlotArgs s{sa.perm, sa.counts, sa.offsets, sa.touched, sa.E, sa.K, sa.T, sa.shared};
-    hipLaunchKernelGGL(k_rpl_down, dim3(d / 64, slots, ksplit), dim3(256), 0, st, down, estride, hh,
-                       hl, hs, hm, s, d, F, Y, split_stride);
+    if (q6)
+        hipLaunchKernelGGL(k_rpl_down<true>, dim3(d / 64, slots, ksplit), dim3(256), 0, st, down,
+                           estride, hh, hl, hs, hm, s, d, F, Y, split_stride);
+    else
+        hipLaunchKernelGGL(k_rpl_down<false>, dim3(d / 64, slots, ksplit), dim3(256), 0, st, down,
+                           estride, hh, hl, hs, hm, s, d, F, Y, split_stride);
     return hipGetLastError();
 }
 

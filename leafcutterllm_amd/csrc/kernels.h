@@ -74,10 +74,11 @@ hipError_t launch_rpl_gateup(const uint8_t *gate, const uint8_t *up, int64_t est
                              const SlotArgsHost &sa, int slots, int d, int F, float *Hf, int8_t *hh,
                              int8_t *hl, float *hs, float *hm, _Float16 *h16, _Float16 *hs16,
                              const ChainArgs &ch, hipStream_t st);
+// q6: the down matrices are RPL64 Q6_K instead of RPL64 Q4_K
 hipError_t launch_rpl_down(const uint8_t *down, int64_t estride, const int8_t *hh,
                            const int8_t *hl, const float *hs, const float *hm,
                            const SlotArgsHost &sa, int slots, int d, int F, int ksplit, float *Y,
-                           int64_t split_stride, hipStream_t st);
+                           int64_t split_stride, hipStream_t st, bool q6 = false);
 
 // Matrix-core path on the RPL64 layout: activations as f16 hi/lo pieces
 // (per token and super-block: hi[256] then lo[256]) plus per-sub-block sums,

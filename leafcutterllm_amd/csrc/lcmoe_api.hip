@@ -201,7 +201,7 @@ hipError_t timed(lcmoe_handle *h, hipStream_t st, int slot, Fn fn) {
 // launch 10% faster at 4 splits than at 2); each wave keeps >= 2 super-blocks
 // where it can (it loads the next while computing the current one).
 int choose_ksplit(const ExpertSet &s, int d, int active) {
-    if (!s.rpl_dn) return 1;
+    if (!s.rpl_dn && !s.q6_dn) return 1;
     const int NB = s.F / 256, tiles = (d / 64) * std::max(1, active);
     int ks = 1;
     while (ks < s.kmax && tiles * ks < 1024 && NB >= 4 * ks * 2 * 2) ks *= 2;
@@ -238,7 +238,7 @@ lcmoe_status setup_set(lcmoe_handle *h, ExpertSet &s, int n, int F, int qgu, int
     if ((st = upload_stack(h, &s.down, down, n, qdn, d, F, s.rpl_dn || s.q6_dn, &s.sz_dn,
                            s.split_dn)))
         return st;
-    if (s.rpl_dn) {
+    if (s.rpl_dn || s.q6_dn) {  // limbs for the row-per-lane down
         if ((st = alloc_n(h, &s.hh, positions * F))) return st;
         if ((st = alloc_n(h, &s.hl, positions * F))) return st;
         if ((st = alloc_n(h, &s.hs, positions * F / 32))) return st;
@@ -375,7 +375,7 @@ static Plan plan_set(lcmoe_handle *h, const ExpertSet &s, bool shared, int T) {
     // passes per block)
     const int64_t per_slot = shared ? T : ((int64_t)T * D.n_expert_used + p.slots - 1) / p.slots;
     p.chunks = p.mfma ? (int)std::min<int64_t>(64, std::max<int64_t>(1, (per_slot + 31) / 32)) : 1;
-    p.ks = (p.mfma && s.rpl_dn) || s.q6_dn || s.split_dn
+    p.ks = (p.mfma && (s.rpl_dn || s.q6_dn)) || s.split_dn
                ? choose_ksplit_mfma(s, D.d_model, p.slots * p.chunks)
                : choose_ksplit(s, D.d_model, p.slots);
     return p;
@@ -386,9 +386,11 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
     const lcmoe_desc &D = h->desc;
     const int d = D.d_model, K = D.n_expert_used, E = D.n_expert;
     SlotArgsHost sa{h->perm, h->counts, h->offsets, h->touched, E, K, T, shared ? 1 : 0};
-    // H between the products in the form the down kernel reads
-    const bool mfma_dn_only = s.q6_dn || s.split_dn;
-    const bool h16_out = (pl.mfma && s.rpl_dn) || mfma_dn_only;
+    // H between the products in the form the down kernel reads: f16 pieces
+    // for the matrix-core downs, int8 limbs for the row-per-lane ones (Q4_K
+    // and Q6_K below one token per expert), f32 for the generic one
+    const bool h16_out = (pl.mfma && (s.rpl_dn || s.q6_dn)) || s.split_dn;
+    const bool limb_out = !pl.mfma && (s.rpl_dn || s.q6_dn);
     HIP_TRY(timed(h, st, shared ? kSlotGateUpSh : kSlotGateUp, [&] {
         if (pl.mfma)
             return launch_mfma_gateup(s.gate, s.up, s.sz_gu, h->x16, h->x16s, sa, pl.slots,
@@ -396,15 +398,18 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
                                       h16_out ? nullptr : s.Hf, ch, st);
         if (s.rpl_gu)
             return launch_rpl_gateup(s.gate, s.up, s.sz_gu, h->xh, h->xl, h->xs, h->xm, sa,
-                                     pl.slots, d, s.F, s.Hf, s.rpl_dn ? s.hh : nullptr, s.hl,
-                                     s.hs, s.hm, mfma_dn_only ? s.h16 : nullptr, s.h16s, ch, st);
+                                     pl.slots, d, s.F, s.Hf, limb_out ? s.hh : nullptr, s.hl,
+                                     s.hs, s.hm, h16_out ? s.h16 : nullptr, s.h16s, ch, st);
         return launch_generic_gateup(s.qt_gu, s.gate, s.up, s.sz_gu, x, sa, pl.slots, d, s.F,
                                      s.Hf, nullptr, nullptr, nullptr, nullptr, ch, st);
     }));
     HIP_TRY(timed(h, st, shared ? kSlotDownSh : kSlotDown, [&] {
-        if (s.q6_dn)
+        if (s.q6_dn && pl.mfma)
             return launch_mfma_down_q6(s.down, s.sz_dn, s.h16, sa, pl.slots, pl.chunks, d, s.F,
                                        pl.ks, s.Y, s.positions * d, st);
+        if (s.q6_dn)
+            return launch_rpl_down(s.down, s.sz_dn, s.hh, s.hl, s.hs, s.hm, sa, pl.slots, d, s.F,
+                                   pl.ks, s.Y, s.positions * d, st, true);
         if (s.split_dn || (s.rpl_dn && pl.mfma))
             return launch_mfma_down(s.down, s.sz_dn, s.h16, s.h16s, sa, pl.slots, pl.chunks, d,
                                     s.F, pl.ks, s.Y, s.positions * d, st);
