@@ -170,13 +170,17 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // Which expert a block of an expert-product launch serves.  Routed launch:
-// slot i serves touched[i] (nothing when i >= number touched) over positions
-// p in [offsets[e], offsets[e] + counts[e]) whose token is perm[p] / K.
-// Shared launch: slot s is shared expert s over all T tokens, positions
-// s*T + t.
+// slot i < nr serves touched[i] (nothing when i >= number touched) over
+// positions p in [offsets[e], offsets[e] + counts[e]) whose token is
+// perm[p] / K; slot nr + s*ns + c serves tokens [c*sl, c*sl + sl) of shared
+// expert s < S, stored as expert E + s, at positions sbase + s*T + t (shared
+// experts fused into the routed launch, in ns slices of sl tokens).  Shared
+// launch (shared = 1): slot s is shared expert s over all T tokens,
+// positions s*T + t.
 struct SlotArgs {
     const int32_t *perm, *counts, *offsets, *touched;
     int E, K, T, shared;
+    int nr, S, sbase, ns, sl;
 };
 
 __device__ __forceinline__ bool slot_info(const SlotArgs &sa, int slot, int &e, int &p0, int &n) {
@@ -186,6 +190,14 @@ __device__ __forceinline__ bool slot_info(const SlotArgs &sa, int slot, int &e, 
         n = sa.T;
         return true;
     }
+    if (slot >= sa.nr) {
+        const int v = slot - sa.nr, s = v / sa.ns, c = v - s * sa.ns;
+        if (s >= sa.S) return false;
+        e = sa.E + s;
+        p0 = sa.sbase + s * sa.T + c * sa.sl;
+        n = min(sa.sl, sa.T - c * sa.sl);
+        return n > 0;
+    }
     if (slot >= sa.touched[sa.E]) return false;
     e = sa.touched[slot];
     p0 = sa.offsets[e];
@@ -193,8 +205,11 @@ __device__ __forceinline__ bool slot_info(const SlotArgs &sa, int slot, int &e, 
     return true;
 }
 
+// token of position p0 + q; positions from sbase on belong to fused shared
+// experts and follow the tokens (T per expert)
 __device__ __forceinline__ int slot_token(const SlotArgs &sa, int p0, int q) {
-    return sa.shared ? q : sa.perm[p0 + q] / sa.K;
+    if (sa.shared) return q;
+    return p0 >= sa.sbase ? (p0 - sa.sbase) % sa.T + q : sa.perm[p0 + q] / sa.K;
 }
 
 // Two-limb int8 quantisation of 32 values held one per lane in a 32-lane

@@ -47,9 +47,13 @@ bool route_fast_ok(const RouterArgs &a);
 hipError_t launch_route_fast(const RouterArgs &a, const ChainArgs &ch, hipStream_t st);
 int router_token_groups(int T, int d, int E);
 
+// See SlotArgs (device_common.h): nr routed slots, then S fused shared
+// experts (stored as experts E .. E+S-1) in ns slots of sl tokens each, at
+// positions from sbase.
 struct SlotArgsHost {
     const int32_t *perm, *counts, *offsets, *touched;
     int E, K, T, shared;
+    int nr, S, sbase, ns, sl;
 };
 
 // Generic decode path on GGUF-layout tensors (any supported type, any

@@ -33,8 +33,6 @@ enum Slot { kSlotRouter, kSlotPrep, kSlotGateUp, kSlotGateUpSh, kSlotDown, kSlot
 const char *kSlotNames[kNumSlots] = {"router", "act16", "gateup", "gateup_shared", "down",
                                      "down_shared", "combine"};
 constexpr int kMaxKSplit = 4;
-// matrix-core path when an expert family averages at least this many tokens
-constexpr int kMfmaMinTokens = 1;
 // largest T * E * d served by the certified per-token router
 constexpr int64_t kFastRouterElems = (int64_t)1 << 24;
 
@@ -71,6 +69,7 @@ struct lcmoe_handle {
     // ((e * C/4 + i) * 64 + lane) * 4 + j, C = d / 64
     float *wlc = nullptr;
     ExpertSet routed, shared;
+    bool fused = false;  // shared experts stored and launched with the routed ones
     float *x_dev = nullptr, *y_dev = nullptr, *logits = nullptr;
     float *chain_part = nullptr;  // [max_tokens, E] router chain running sums
     int8_t *xh = nullptr, *xl = nullptr;
@@ -117,21 +116,24 @@ lcmoe_status alloc_n(lcmoe_handle *h, T **dst, size_t n) {
 // to RPL64 (Q4_K or Q6_K, by qt) when `rpl`, or to the split Q4_K layout
 // when `split` (one expert at a time through a host staging buffer).
 // *sz_out: device bytes per expert.
+// n2 > 0: n2 more experts from src2 follow as experts n .. n+n2-1.
 lcmoe_status upload_stack(lcmoe_handle *h, uint8_t **dst, const uint8_t *src, int n, int qt,
                           int64_t rows, int64_t cols, bool rpl, int64_t *sz_out,
-                          bool split = false) {
+                          bool split = false, const uint8_t *src2 = nullptr, int n2 = 0) {
     const int64_t sz = (int64_t)lcmoe_tensor_size(qt, rows * cols);
     const int64_t dsz = split ? rows / 64 * ((cols + 255) / 256) * (9 * 1024 + 256) : sz;
     *sz_out = dsz;
-    lcmoe_status st = alloc_n(h, dst, (size_t)dsz * n);
+    lcmoe_status st = alloc_n(h, dst, (size_t)dsz * (n + n2));
     if (st) return st;
     if (!rpl && !split) {
         HIP_TRY(hipMemcpy(*dst, src, (size_t)sz * n, hipMemcpyHostToDevice));
+        if (n2)
+            HIP_TRY(hipMemcpy(*dst + (size_t)sz * n, src2, (size_t)sz * n2, hipMemcpyHostToDevice));
         return LCMOE_OK;
     }
     std::vector<uint8_t> buf((size_t)dsz);
-    for (int e = 0; e < n; e++) {
-        const uint8_t *s = src + (size_t)e * sz;
+    for (int e = 0; e < n + n2; e++) {
+        const uint8_t *s = e < n ? src + (size_t)e * sz : src2 + (size_t)(e - n) * sz;
         if (split) {  // straddling blocks: one thread (the layout reads across rows)
             repack_rpl64_q4k_split(s, buf.data(), rows, cols);
             HIP_TRY(hipMemcpy(*dst + (size_t)e * dsz, buf.data(), (size_t)dsz,
@@ -218,8 +220,12 @@ int choose_ksplit_mfma(const ExpertSet &s, int d, int active) {
     return ks;
 }
 
+// n experts from gate/up/down, plus n2 fused shared experts from
+// gate2/up2/down2 stored after them (experts n .. n+n2-1)
 lcmoe_status setup_set(lcmoe_handle *h, ExpertSet &s, int n, int F, int qgu, int qdn,
-                       const uint8_t *gate, const uint8_t *up, const uint8_t *down, int64_t positions) {
+                       const uint8_t *gate, const uint8_t *up, const uint8_t *down, int64_t positions,
+                       int n2 = 0, const uint8_t *gate2 = nullptr, const uint8_t *up2 = nullptr,
+                       const uint8_t *down2 = nullptr) {
     const int64_t d = h->desc.d_model;
     s.n = n;
     s.F = F;
@@ -233,10 +239,11 @@ lcmoe_status setup_set(lcmoe_handle *h, ExpertSet &s, int n, int F, int qgu, int
     s.kmax = s.rpl_dn || s.q6_dn || s.split_dn ? kMaxKSplit : 1;
     int64_t szu = 0;
     lcmoe_status st;
-    if ((st = upload_stack(h, &s.gate, gate, n, qgu, F, d, s.rpl_gu, &s.sz_gu))) return st;
-    if ((st = upload_stack(h, &s.up, up, n, qgu, F, d, s.rpl_gu, &szu))) return st;
+    if ((st = upload_stack(h, &s.gate, gate, n, qgu, F, d, s.rpl_gu, &s.sz_gu, false, gate2, n2)))
+        return st;
+    if ((st = upload_stack(h, &s.up, up, n, qgu, F, d, s.rpl_gu, &szu, false, up2, n2))) return st;
     if ((st = upload_stack(h, &s.down, down, n, qdn, d, F, s.rpl_dn || s.q6_dn, &s.sz_dn,
-                           s.split_dn)))
+                           s.split_dn, down2, n2)))
         return st;
     if (s.rpl_dn || s.q6_dn) {  // limbs for the row-per-lane down
         if ((st = alloc_n(h, &s.hh, positions * F))) return st;
@@ -317,13 +324,24 @@ extern "C" lcmoe_status lcmoe_create(const lcmoe_desc *desc, const lcmoe_weights
         if (hipMemcpy(h->bias, w->bias, E * 4, hipMemcpyHostToDevice) != hipSuccess)
             return bail(fail(LCMOE_ERR_HIP, "bias upload failed"));
     }
-    if ((st = setup_set(h, h->routed, (int)E, D.d_ff, D.type_gate, D.type_down, w->gate, w->up,
-                        w->down, A)))
-        return bail(st);
-    if (S > 0 && (st = setup_set(h, h->shared, (int)S, D.d_ff_shared, D.type_gate_sh,
-                                 D.type_down_sh, w->gate_sh, w->up_sh, w->down_sh, S * Tm)))
-        return bail(st);
-    const bool limbs = h->routed.rpl_gu || (S > 0 && h->shared.rpl_gu);
+    // shared experts of the routed experts' shape and types run as extra
+    // slots of the routed launches (their positions follow the A routed ones)
+    h->fused = S > 0 && D.d_ff_shared == D.d_ff && D.type_gate_sh == D.type_gate &&
+               D.type_down_sh == D.type_down;
+    if (h->fused) {
+        if ((st = setup_set(h, h->routed, (int)E, D.d_ff, D.type_gate, D.type_down, w->gate,
+                            w->up, w->down, A + S * Tm, (int)S, w->gate_sh, w->up_sh,
+                            w->down_sh)))
+            return bail(st);
+    } else {
+        if ((st = setup_set(h, h->routed, (int)E, D.d_ff, D.type_gate, D.type_down, w->gate,
+                            w->up, w->down, A)))
+            return bail(st);
+        if (S > 0 && (st = setup_set(h, h->shared, (int)S, D.d_ff_shared, D.type_gate_sh,
+                                     D.type_down_sh, w->gate_sh, w->up_sh, w->down_sh, S * Tm)))
+            return bail(st);
+    }
+    const bool limbs = h->routed.rpl_gu || (S > 0 && !h->fused && h->shared.rpl_gu);
     if ((st = alloc_n(h, &h->x_dev, Tm * d))) return bail(st);
     if ((st = alloc_n(h, &h->y_dev, Tm * d))) return bail(st);
     if ((st = alloc_n(h, &h->logits, Tm * E))) return bail(st);
@@ -358,65 +376,85 @@ struct Plan {
     bool mfma;
     int slots, ks;
     int chunks;  // blocks sharing one matrix-core slot's 32-token passes
+    int sl, ns;  // fused shared experts: tokens per slot, slots per expert
 };
 
-static Plan plan_set(lcmoe_handle *h, const ExpertSet &s, bool shared, int T) {
+// fused: the routed plan also carries the fused shared experts (slots
+// p.slots .. p.slots + n_shared - 1, all T tokens each)
+// fused_only: a launch of the fused shared experts alone (no routed slots)
+static Plan plan_set(lcmoe_handle *h, const ExpertSet &s, bool shared, int T, int fused = 0,
+                     bool fused_only = false) {
     const lcmoe_desc &D = h->desc;
     Plan p;
-    p.slots = shared ? s.n : std::min(D.n_expert, T * D.n_expert_used);
-    // tokens per expert averaged over all experts (over the touched ones it
-    // is >= 1 by construction): the matrix-core kernels decode each weight
-    // once for up to 32 tokens, the row-per-lane ones once per token pass
-    const int64_t per_expert =
-        shared ? T : (int64_t)T * D.n_expert_used / std::max(1, D.n_expert);
-    p.mfma = s.rpl_gu && per_expert >= kMfmaMinTokens;
+    if (fused_only) shared = true;
+    p.slots = fused_only ? 0 : shared ? s.n : std::min(D.n_expert, T * D.n_expert_used);
+    // the matrix-core kernels decode each weight once for up to 32 tokens,
+    // the row-per-lane ones once per pass of up to 4 tokens: matrix cores
+    // when there are more assignments than experts (T K > E; a shared expert
+    // sees every token, so T > 1).  Measured at the boundary T K = E: config 2
+    // T = 4 runs 141 us row-per-lane against 148 us, config 4 T = 32 1.01 ms
+    // against 1.17 ms.
+    const int64_t assign = shared ? T : (int64_t)T * D.n_expert_used;
+    p.mfma = s.rpl_gu && assign > (shared ? 1 : (int64_t)D.n_expert);
     // passes per slot: all T tokens for a shared expert, the average over
     // the touched experts for the routed ones (busier experts run several
     // passes per block)
-    const int64_t per_slot = shared ? T : ((int64_t)T * D.n_expert_used + p.slots - 1) / p.slots;
+    const int64_t per_slot =
+        shared ? T : ((int64_t)T * D.n_expert_used + p.slots - 1) / std::max(1, p.slots);
     p.chunks = p.mfma ? (int)std::min<int64_t>(64, std::max<int64_t>(1, (per_slot + 31) / 32)) : 1;
+    // fused shared experts: slices of the tokens one slot takes (the passes
+    // of its chunk blocks, or one row-per-lane pass)
+    p.sl = p.mfma ? 32 * p.chunks : 4;
+    p.ns = fused ? (T + p.sl - 1) / p.sl : 0;
+    const int all = p.slots + fused * p.ns;
     p.ks = (p.mfma && (s.rpl_dn || s.q6_dn)) || s.split_dn
-               ? choose_ksplit_mfma(s, D.d_model, p.slots * p.chunks)
-               : choose_ksplit(s, D.d_model, p.slots);
+               ? choose_ksplit_mfma(s, D.d_model, all * p.chunks)
+               : choose_ksplit(s, D.d_model, all);
     return p;
 }
 
+// fused: number of shared experts run as extra slots of this (routed) set;
+// fused_only: no routed slots (pl from plan_set(..., fused_only))
 static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const float *x, int T,
-                            const Plan &pl, const ChainArgs &ch, hipStream_t st) {
+                            const Plan &pl, const ChainArgs &ch, hipStream_t st, int fused = 0,
+                            bool fused_only = false) {
     const lcmoe_desc &D = h->desc;
     const int d = D.d_model, K = D.n_expert_used, E = D.n_expert;
-    SlotArgsHost sa{h->perm, h->counts, h->offsets, h->touched, E, K, T, shared ? 1 : 0};
+    const int A = D.max_tokens * K;  // routed positions; fused shared ones follow
+    SlotArgsHost sa{h->perm, h->counts, h->offsets, h->touched, E, K, T, shared ? 1 : 0,
+                    pl.slots, fused, fused ? A : INT32_MAX, std::max(1, pl.ns), pl.sl};
+    const int slots = pl.slots + fused * pl.ns;
     // H between the products in the form the down kernel reads: f16 pieces
     // for the matrix-core downs, int8 limbs for the row-per-lane ones (Q4_K
     // and Q6_K below one token per expert), f32 for the generic one
     const bool h16_out = (pl.mfma && (s.rpl_dn || s.q6_dn)) || s.split_dn;
     const bool limb_out = !pl.mfma && (s.rpl_dn || s.q6_dn);
-    HIP_TRY(timed(h, st, shared ? kSlotGateUpSh : kSlotGateUp, [&] {
+    HIP_TRY(timed(h, st, shared || fused_only ? kSlotGateUpSh : kSlotGateUp, [&] {
         if (pl.mfma)
-            return launch_mfma_gateup(s.gate, s.up, s.sz_gu, h->x16, h->x16s, sa, pl.slots,
+            return launch_mfma_gateup(s.gate, s.up, s.sz_gu, h->x16, h->x16s, sa, slots,
                                       pl.chunks, d, s.F, h16_out ? s.h16 : nullptr, s.h16s,
                                       h16_out ? nullptr : s.Hf, ch, st);
         if (s.rpl_gu)
             return launch_rpl_gateup(s.gate, s.up, s.sz_gu, h->xh, h->xl, h->xs, h->xm, sa,
-                                     pl.slots, d, s.F, s.Hf, limb_out ? s.hh : nullptr, s.hl,
+                                     slots, d, s.F, s.Hf, limb_out ? s.hh : nullptr, s.hl,
                                      s.hs, s.hm, h16_out ? s.h16 : nullptr, s.h16s, ch, st);
-        return launch_generic_gateup(s.qt_gu, s.gate, s.up, s.sz_gu, x, sa, pl.slots, d, s.F,
+        return launch_generic_gateup(s.qt_gu, s.gate, s.up, s.sz_gu, x, sa, slots, d, s.F,
                                      s.Hf, nullptr, nullptr, nullptr, nullptr, ch, st);
     }));
-    HIP_TRY(timed(h, st, shared ? kSlotDownSh : kSlotDown, [&] {
+    HIP_TRY(timed(h, st, shared || fused_only ? kSlotDownSh : kSlotDown, [&] {
         if (s.q6_dn && pl.mfma)
-            return launch_mfma_down_q6(s.down, s.sz_dn, s.h16, sa, pl.slots, pl.chunks, d, s.F,
+            return launch_mfma_down_q6(s.down, s.sz_dn, s.h16, sa, slots, pl.chunks, d, s.F,
                                        pl.ks, s.Y, s.positions * d, st);
         if (s.q6_dn)
-            return launch_rpl_down(s.down, s.sz_dn, s.hh, s.hl, s.hs, s.hm, sa, pl.slots, d, s.F,
+            return launch_rpl_down(s.down, s.sz_dn, s.hh, s.hl, s.hs, s.hm, sa, slots, d, s.F,
                                    pl.ks, s.Y, s.positions * d, st, true);
         if (s.split_dn || (s.rpl_dn && pl.mfma))
-            return launch_mfma_down(s.down, s.sz_dn, s.h16, s.h16s, sa, pl.slots, pl.chunks, d,
+            return launch_mfma_down(s.down, s.sz_dn, s.h16, s.h16s, sa, slots, pl.chunks, d,
                                     s.F, pl.ks, s.Y, s.positions * d, st);
         if (s.rpl_dn)
-            return launch_rpl_down(s.down, s.sz_dn, s.hh, s.hl, s.hs, s.hm, sa, pl.slots, d, s.F,
+            return launch_rpl_down(s.down, s.sz_dn, s.hh, s.hl, s.hs, s.hm, sa, slots, d, s.F,
                                    pl.ks, s.Y, s.positions * d, st);
-        return launch_generic_down(s.qt_dn, s.down, s.sz_dn, s.Hf, sa, pl.slots, d, s.F, s.Y, st);
+        return launch_generic_down(s.qt_dn, s.down, s.sz_dn, s.Hf, sa, slots, d, s.F, s.Y, st);
     }));
     return LCMOE_OK;
 }
@@ -425,11 +463,22 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
                                     hipStream_t st) {
     const lcmoe_desc &D = h->desc;
     const int d = D.d_model, E = D.n_expert, K = D.n_expert_used, S = D.n_shared;
-    const Plan pr = plan_set(h, h->routed, false, T);
-    const Plan ps = S > 0 ? plan_set(h, h->shared, true, T) : Plan{false, 0, 1, 1};
-    const bool mfma = pr.mfma || ps.mfma;
+    // Fused shared experts ride in the routed launches while every routed
+    // slot is one matrix-core block (or a row-per-lane one); past that
+    // (prefill) they get launches of their own, which schedule better.
+    const int Sf = h->fused ? S : 0;
+    const Plan pr0 = plan_set(h, h->routed, false, T);
+    const bool together = Sf > 0 && pr0.chunks == 1;
+    const int fused = together ? Sf : 0;
+    const Plan pr = together ? plan_set(h, h->routed, false, T, Sf) : pr0;
+    const Plan off{false, 0, 1, 1, 4, 0};
+    const Plan pf = Sf > 0 && !together ? plan_set(h, h->routed, false, T, Sf, true) : off;
+    const Plan ps = S > 0 && !h->fused ? plan_set(h, h->shared, true, T) : off;
+    const bool sep_f = Sf > 0 && !together;
+    const bool mfma = pr.mfma || ps.mfma || pf.mfma;
     // int8 limbs only feed the row-per-lane kernels
-    const bool limbs = (h->routed.rpl_gu && !pr.mfma) || (S > 0 && h->shared.rpl_gu && !ps.mfma);
+    const bool limbs = (h->routed.rpl_gu && (!pr.mfma || (sep_f && !pf.mfma))) ||
+                       (S > 0 && !h->fused && h->shared.rpl_gu && !ps.mfma);
     RouterArgs ra{};
     ra.x = x;
     ra.wrt = h->wrt;
@@ -485,16 +534,22 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
             }));
     }
     lcmoe_status s;
-    if ((s = run_set(h, h->routed, false, x, T, pr, ch_g, st))) return s;
-    if (S > 0 && (s = run_set(h, h->shared, true, x, T, ps, ChainArgs{}, st))) return s;
+    if ((s = run_set(h, h->routed, false, x, T, pr, ch_g, st, fused))) return s;
+    if (sep_f && (s = run_set(h, h->routed, false, x, T, pf, ChainArgs{}, st, Sf, true))) return s;
+    if (S > 0 && !h->fused && (s = run_set(h, h->shared, true, x, T, ps, ChainArgs{}, st)))
+        return s;
     const int ks_r = pr.ks, ks_s = ps.ks;
     CombineRoute cr{};
     if (fast)
         cr = CombineRoute{h->logits, h->topk_idx, D.has_bias ? h->bias : nullptr, D.route_kind,
                           E, D.routed_scale};
     HIP_TRY(timed(h, st, kSlotCombine, [&] {
-        return launch_combine(h->routed.Y, ks_r, h->routed.positions * d, h->shared.Y, ks_s,
-                              h->shared.positions * d, h->inv, h->topk_w, T, K, S, d, cr, y, st);
+        // fused shared experts' partials follow the routed positions
+        const float *Ys = Sf ? h->routed.Y + (int64_t)D.max_tokens * K * d : h->shared.Y;
+        const int64_t ss = Sf ? h->routed.positions * d : h->shared.positions * d;
+        const int kss = !Sf ? ks_s : together ? ks_r : pf.ks;
+        return launch_combine(h->routed.Y, ks_r, h->routed.positions * d, Ys, kss, ss, h->inv,
+                              h->topk_w, T, K, S, d, cr, y, st);
     }));
     h->last_T = T;
     h->last_stream = st;
