@@ -90,19 +90,41 @@ __device__ void select_token(const RouterArgs &a, int t, float *s_z, float *s_s,
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     if (rp.kind == LCMOE_ROUTE_SIGMOID_GROUP) {
         const int G = rp.n_group, gs = E / G;
-        for (int g = lane; g < G; g += 64) {  // group score = top-1 z + top-2 z
-            int b1 = -1, b2 = -1;
-            for (int i = 0; i < gs; i++) {
-                int e = g * gs + i;
-                float k = sel_key(s_z[e]);
-                if (b1 < 0 || better(k, e, sel_key(s_z[b1]), b1)) {
-                    b2 = b1;
-                    b1 = e;
-                } else if (b2 < 0 || better(k, e, sel_key(s_z[b2]), b2)) {
-                    b2 = e;
+        // group score = top-1 z + top-2 z (ties -> lower index), one group
+        // at a time across the wave: per lane the best two of its experts,
+        // then a butterfly merge of (best, second) pairs
+        for (int g = 0; g < G; g++) {
+            float k1 = -__builtin_inff(), k2 = -__builtin_inff();
+            int e1 = INT_MAX, e2 = INT_MAX;
+            for (int i = lane; i < gs; i += 64) {
+                const int e = g * gs + i;
+                const float k = sel_key(s_z[e]);
+                if (better(k, e, k1, e1)) {
+                    k2 = k1;
+                    e2 = e1;
+                    k1 = k;
+                    e1 = e;
+                } else if (better(k, e, k2, e2)) {
+                    k2 = k;
+                    e2 = e;
                 }
             }
-            s_g[g] = gs >= 2 ? s_z[b1] + s_z[b2] : s_z[b1];
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                const float o1 = __shfl_xor(k1, off, 64), o2 = __shfl_xor(k2, off, 64);
+                const int f1 = __shfl_xor(e1, off, 64), f2 = __shfl_xor(e2, off, 64);
+                if (better(o1, f1, k1, e1)) {  // other's best leads
+                    const bool keep = better(k1, e1, o2, f2);
+                    k2 = keep ? k1 : o2;
+                    e2 = keep ? e1 : f2;
+                    k1 = o1;
+                    e1 = f1;
+                } else if (better(o1, f1, k2, e2)) {
+                    k2 = o1;
+                    e2 = f1;
+                }
+            }
+            if (lane == 0) s_g[g] = gs >= 2 ? s_z[e1] + s_z[min(e2, E - 1)] : s_z[e1];
         }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
@@ -811,7 +833,9 @@ __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a, Chain
 // ---------------------------------------------------------------------------
 
 constexpr int kChainWaves = 4;
-constexpr int kChainLds = chain_lds_floats(16, 128);
+constexpr int kChainLds = chain_lds_floats(9, 256) > chain_lds_floats(16, 128)
+                              ? chain_lds_floats(9, 256)
+                              : chain_lds_floats(16, 128);
 constexpr int kSelWaves = 8;
 
 __global__ __launch_bounds__(64 * kChainWaves) void k_route_chains(RouterArgs a, ChainArgs ch,
@@ -819,7 +843,12 @@ __global__ __launch_bounds__(64 * kChainWaves) void k_route_chains(RouterArgs a,
     __shared__ __attribute__((aligned(16))) float s_lds[kChainWaves][kChainLds];
     if ((int)blockIdx.x < chain_blocks) {
         const int wave = threadIdx.x >> 6, tile = blockIdx.x * kChainWaves + wave;
-        if (tile < ch.tiles) chain_tile<8, 128, 4>(ch, tile, s_lds[wave]);
+        if (tile < ch.tiles) {
+            if (ch.nt == 1)  // fewer than 8 tokens: 1-token tiles, 256-column chunks
+                chain_tile<1, 256, 2>(ch, tile, s_lds[wave]);
+            else
+                chain_tile<8, 128, 4>(ch, tile, s_lds[wave]);
+        }
         return;
     }
     quantise_token<1, 64 * kChainWaves>(a, blockIdx.x - chain_blocks, nullptr);
@@ -892,10 +921,11 @@ hipError_t launch_router(const RouterArgs &a, hipStream_t st) {
     return hipGetLastError();
 }
 
-bool route_chains_ok(const RouterArgs &a) { return a.d % 128 == 0; }
+bool route_chains_ok(const RouterArgs &a) { return a.d % 128 == 0 && (a.T >= 8 || a.d % 256 == 0); }
 
 hipError_t launch_route_chains(const RouterArgs &a, hipStream_t st) {
-    const ChainArgs ch = make_chains(a.x, a.wrt, a.logits, nullptr, a.T, a.d, a.E, 0, a.d, 8);
+    const ChainArgs ch =
+        make_chains(a.x, a.wrt, a.logits, nullptr, a.T, a.d, a.E, 0, a.d, a.T < 8 ? 1 : 8);
     const int cb = (ch.tiles + kChainWaves - 1) / kChainWaves;
     const int ab = (a.xh || a.x16) ? a.T : 0;
     hipLaunchKernelGGL(k_route_chains, dim3(cb + ab), dim3(64 * kChainWaves), 0, st, a, ch, cb);
