@@ -260,6 +260,86 @@ __device__ __forceinline__ void pass1_q6(const uint4 *__restrict__ W, const uint
     if (kb < kb1) dot_sb_q6<NT>(c0, kb, X, row, acc);
 }
 
+// ---- Q8_0 in the RPL64 Q8_0 layout ----------------------------------------
+// Per 64-row tile and 256-column group (eight Q8_0 blocks of 32): chunk 0
+// holds each row's eight f16 d (16 bytes), chunks 1-16 its 256 int8 quants
+// in column order, 16 bytes per chunk: 1,088 uint4 per tile and group, the
+// GGUF bytes permuted.  A Q8_0 block is one 32-column activation sub-block,
+// so sum_k q_k (128 hi_k + lo_k) is one exact int32 per block and token
+// (|.| <= 32 * 127 * 16256): value d * s * that (dequantize_q8_0,
+// rust/src/kernels/mod.rs:37-51, times the activation limbs).
+constexpr int kQ8Chunks = 17;
+
+template <int NT>
+__device__ __forceinline__ void q8_block_dot(const uint4 (&c)[kQ8Chunks], const int *const (&xh)[NT],
+                                             const int *const (&xl)[NT],
+                                             const float *const (&xs)[NT], float (&acc)[NT]) {
+    const uint32_t dw[4] = {c[0].x, c[0].y, c[0].z, c[0].w};
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+        const float d = dh2f((dw[b >> 1] >> (16 * (b & 1))) & 0xffff);
+        const uint4 qa = c[1 + 2 * b], qb = c[2 + 2 * b];
+        const int q[8] = {(int)qa.x, (int)qa.y, (int)qa.z, (int)qa.w,
+                          (int)qb.x, (int)qb.y, (int)qb.z, (int)qb.w};
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const int *ph = xh[t] + 8 * b, *pl = xl[t] + 8 * b;
+            int h = 0, l = 0;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                h = __builtin_amdgcn_sdot4(q[i], ph[i], h, false);
+                l = __builtin_amdgcn_sdot4(q[i], pl[i], l, false);
+            }
+            acc[t] = __builtin_fmaf(d * xs[t][b], (float)(h * 128 + l), acc[t]);
+        }
+    }
+}
+
+__device__ __forceinline__ void load_q8(uint4 (&c)[kQ8Chunks], const uint4 *W, int kb) {
+    const uint4 *p = W + (int64_t)kb * kQ8Chunks * 64;
+#pragma unroll
+    for (int i = 0; i < kQ8Chunks; i++) c[i] = p[i * 64];
+}
+
+template <int NT>
+__device__ __forceinline__ void dot_sb_q8(const uint4 (&c)[kQ8Chunks], int kb, const Limbs &X,
+                                          const int (&row)[NT], float (&acc)[NT]) {
+    const int *xh[NT], *xl[NT];
+    const float *xs[NT], *xm[NT];
+    token_ptrs<NT>(X, row, kb, xh, xl, xs, xm);
+    q8_block_dot<NT>(c, xh, xl, xs, acc);
+}
+
+template <int NT>
+__device__ __forceinline__ void pass1_q8(const uint4 *__restrict__ W, int kb0, int kb1,
+                                         const Limbs &X, const int (&row)[NT], float (&acc)[NT]) {
+    if (kb0 >= kb1) return;
+    uint4 c0[kQ8Chunks], c1[kQ8Chunks];
+    load_q8(c0, W, kb0);
+    int kb = kb0;
+    for (; kb + 2 <= kb1; kb += 2) {
+        load_q8(c1, W, kb + 1);
+        dot_sb_q8<NT>(c0, kb, X, row, acc);
+        load_q8(c0, W, min(kb + 2, kb1 - 1));
+        dot_sb_q8<NT>(c1, kb + 1, X, row, acc);
+    }
+    if (kb < kb1) dot_sb_q8<NT>(c0, kb, X, row, acc);
+}
+
+// gate and up rows of this lane, Q8_0
+template <int NT>
+__device__ __forceinline__ void pass2_q8(const uint4 *__restrict__ G, const uint4 *__restrict__ U,
+                                         int kb0, int kb1, const Limbs &X, const int (&row)[NT],
+                                         float (&ag)[NT], float (&au)[NT]) {
+    for (int kb = kb0; kb < kb1; kb++) {
+        uint4 cg[kQ8Chunks], cu[kQ8Chunks];
+        load_q8(cg, G, kb);
+        load_q8(cu, U, kb);
+        dot_sb_q8<NT>(cg, kb, X, row, ag);
+        dot_sb_q8<NT>(cu, kb, X, row, au);
+    }
+}
+
 struct HOut {
     float *f;       // H f32 [positions, F] or null
     int8_t *h, *l;  // H limbs [positions, F] or null
@@ -278,7 +358,7 @@ constexpr int kMaxNT = 4;
 // Token rows c .. c+NT-1 of one gate/up tile (rows past n repeat the last
 // token and are not written): the 4 waves' partial sums meet in LDS, then
 // wave w finishes token w (SwiGLU, H out).
-template <int NT>
+template <int NT, bool Q8>
 __device__ __forceinline__ void gateup_chunk(const uint4 *G, const uint4 *U, int kb0, int kb1,
                                              const Limbs &X, const SlotArgs &sa, int p0, int n,
                                              int c, int F, int f, const HOut &out,
@@ -291,7 +371,10 @@ __device__ __forceinline__ void gateup_chunk(const uint4 *G, const uint4 *U, int
     float ag[NT], au[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) ag[t] = au[t] = 0.0f;
-    pass2<NT>(G, U, kb0, kb1, X, row, ag, au);
+    if constexpr (Q8)
+        pass2_q8<NT>(G, U, kb0, kb1, X, row, ag, au);
+    else
+        pass2<NT>(G, U, kb0, kb1, X, row, ag, au);
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         s_red[wave][0][t][lane] = ag[t];
@@ -351,7 +434,8 @@ __device__ __forceinline__ void run_chains(const ChainArgs &ch, float *lds) {
     }
 }
 
-// grid (F/64 row tiles, [chain row +] slots)
+// grid (F/64 row tiles, [chain row +] slots); Q8: RPL64 Q8_0 weights
+template <bool Q8>
 __global__ __launch_bounds__(256) void k_rpl_gateup(
     const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up, int64_t estride,
     const int8_t *__restrict__ xh, const int8_t *__restrict__ xl, const float *__restrict__ xs,
@@ -380,23 +464,23 @@ __global__ __launch_bounds__(256) void k_rpl_gateup(
     const int NB = d >> 8, rt = blockIdx.x, lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kb0 = NB * wave / kWaves, kb1 = NB * (wave + 1) / kWaves;
-    const int64_t tile = (int64_t)rt * NB * 9 * 64 + lane;
+    const int64_t tile = (int64_t)rt * NB * (Q8 ? kQ8Chunks : 9) * 64 + lane;
     const uint4 *G = reinterpret_cast<const uint4 *>(gate + (int64_t)e * estride) + tile;
     const uint4 *U = reinterpret_cast<const uint4 *>(up + (int64_t)e * estride) + tile;
     const int f = rt * 64 + lane;
     for (int c = 0; c < n; c += kMaxNT) {
         const int left = n - c;
         if (left > 2)
-            gateup_chunk<4>(G, U, kb0, kb1, X, sa, p0, n, c, F, f, out, s_red);
+            gateup_chunk<4, Q8>(G, U, kb0, kb1, X, sa, p0, n, c, F, f, out, s_red);
         else if (left == 2)
-            gateup_chunk<2>(G, U, kb0, kb1, X, sa, p0, n, c, F, f, out, s_red);
+            gateup_chunk<2, Q8>(G, U, kb0, kb1, X, sa, p0, n, c, F, f, out, s_red);
         else
-            gateup_chunk<1>(G, U, kb0, kb1, X, sa, p0, n, c, F, f, out, s_red);
+            gateup_chunk<1, Q8>(G, U, kb0, kb1, X, sa, p0, n, c, F, f, out, s_red);
     }
 }
 
-// Q6: Q6_K weights (D: the rows' d) instead of Q4_K
-template <int NT, bool Q6>
+// weight format: 0 Q4_K, 1 Q6_K (D: the rows' d), 2 Q8_0
+template <int NT, int FMT>
 __device__ __forceinline__ void down_chunk(const uint4 *W, const uint16_t *D, int kb0, int kb1,
                                            const Limbs &X, int p0, int n, int c, int d, int r,
                                            float *Y, float (*s_red)[kMaxNT][64]) {
@@ -407,8 +491,10 @@ __device__ __forceinline__ void down_chunk(const uint4 *W, const uint16_t *D, in
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) acc[t] = 0.0f;
-    if constexpr (Q6)
+    if constexpr (FMT == 1)
         pass1_q6<NT>(W, D, kb0, kb1, X, row, acc);
+    else if constexpr (FMT == 2)
+        pass1_q8<NT>(W, kb0, kb1, X, row, acc);
     else
         pass1<NT>(W, kb0, kb1, X, row, acc);
 #pragma unroll
@@ -426,9 +512,9 @@ __device__ __forceinline__ void down_chunk(const uint4 *W, const uint16_t *D, in
 // grid (d/64 tiles, slots, ksplit): block z covers super-block slices
 // 4z .. 4z+3 of the 4*ksplit slices of the F dimension; its partial row sums
 // go to Y + z * split_stride and the combine adds the splits in order.
-// Q6: RPL64 Q6_K weights (840 uint4 per tile and super-block) instead of
-// RPL64 Q4_K (576).
-template <bool Q6>
+// FMT: RPL64 Q4_K (576 uint4 per tile and super-block), Q6_K (840) or
+// Q8_0 (1,088)
+template <int FMT>
 __global__ __launch_bounds__(256) void k_rpl_down(
     const uint8_t *__restrict__ down, int64_t estride, const int8_t *__restrict__ xh,
     const int8_t *__restrict__ xl, const float *__restrict__ xs, const float *__restrict__ xm,
@@ -444,7 +530,7 @@ __global__ __launch_bounds__(256) void k_rpl_down(
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int slices = kWaves * gridDim.z, s = blockIdx.z * kWaves + wave;
     const int kb0 = (int)((int64_t)NB * s / slices), kb1 = (int)((int64_t)NB * (s + 1) / slices);
-    const int tsb = Q6 ? kQ6Uint4 : 9 * 64;  // uint4 per tile and super-block
+    const int tsb = FMT == 1 ? kQ6Uint4 : FMT == 2 ? kQ8Chunks * 64 : 9 * 64;
     const uint4 *T = reinterpret_cast<const uint4 *>(down + (int64_t)e * estride) +
                      (int64_t)rt * NB * tsb;
     const uint4 *W = T + lane;
@@ -454,11 +540,11 @@ __global__ __launch_bounds__(256) void k_rpl_down(
     for (int c = 0; c < n; c += kMaxNT) {
         const int left = n - c;
         if (left > 2)
-            down_chunk<4, Q6>(W, D, kb0, kb1, X, p0, n, c, d, r, Yz, s_red);
+            down_chunk<4, FMT>(W, D, kb0, kb1, X, p0, n, c, d, r, Yz, s_red);
         else if (left == 2)
-            down_chunk<2, Q6>(W, D, kb0, kb1, X, p0, n, c, d, r, Yz, s_red);
+            down_chunk<2, FMT>(W, D, kb0, kb1, X, p0, n, c, d, r, Yz, s_red);
         else
-            down_chunk<1, Q6>(W, D, kb0, kb1, X, p0, n, c, d, r, Yz, s_red);
+            down_chunk<1, FMT>(W, D, kb0, kb1, X, p0, n, c, d, r, Yz, s_red);
     }
 }
 
@@ -468,30 +554,38 @@ hipError_t launch_rpl_gateup(const uint8_t *gate, const uint8_t *up, int64_t est
                              const int8_t *xh, const int8_t *xl, const float *xs, const float *xm,
                              const SlotArgsHost &sa, int slots, int d, int F, float *Hf, int8_t *hh,
                              int8_t *hl, float *hs, float *hm, _Float16 *h16, _Float16 *hs16,
-                             const ChainArgs &ch, hipStream_t st) {
+                             const ChainArgs &ch, hipStream_t st, bool q8) {
     SlotArgs s{sa.perm, sa.counts, sa.offsets, sa.touched, sa.E, sa.K, sa.T, sa.shared, sa.nr, sa.S, sa.sbase, sa.ns, sa.sl};
     ChainArgs c = ch;
     if (c.tiles) {
         if (c.k0 % 256 || c.k1 % 256) return hipErrorInvalidValue;
         c = with_nt(ch, ch.T == 1 ? 1 : 8);
     }
-    hipLaunchKernelGGL(k_rpl_gateup, dim3(F / 64, slots + (c.tiles ? 1 : 0)), dim3(256), 0, st,
-                       gate, up, estride, xh, xl, xs, xm, s, d, F, Hf, hh, hl, hs, hm, h16, hs16,
-                       c);
+    const dim3 grid(F / 64, slots + (c.tiles ? 1 : 0));
+    if (q8)
+        hipLaunchKernelGGL(k_rpl_gateup<true>, grid, dim3(256), 0, st, gate, up, estride, xh, xl,
+                           xs, xm, s, d, F, Hf, hh, hl, hs, hm, h16, hs16, c);
+    else
+        hipLaunchKernelGGL(k_rpl_gateup<false>, grid, dim3(256), 0, st, gate, up, estride, xh, xl,
+                           xs, xm, s, d, F, Hf, hh, hl, hs, hm, h16, hs16, c);
     return hipGetLastError();
 }
 
 hipError_t launch_rpl_down(const uint8_t *down, int64_t estride, const int8_t *hh,
                            const int8_t *hl, const float *hs, const float *hm,
                            const SlotArgsHost &sa, int slots, int d, int F, int ksplit, float *Y,
-                           int64_t split_stride, hipStream_t st, bool q6) {
+                           int64_t split_stride, hipStream_t st, int fmt) {
     SlotArgs s{sa.perm, sa.counts, sa.offsets, sa.touched, sa.E, sa.K, sa.T, sa.shared, sa.nr, sa.S, sa.sbase, sa.ns, sa.sl};
-    if (q6)
-        hipLaunchKernelGGL(k_rpl_down<true>, dim3(d / 64, slots, ksplit), dim3(256), 0, st, down,
-                           estride, hh, hl, hs, hm, s, d, F, Y, split_stride);
+    const dim3 grid(d / 64, slots, ksplit);
+    if (fmt == 1)
+        hipLaunchKernelGGL(k_rpl_down<1>, grid, dim3(256), 0, st, down, estride, hh, hl, hs, hm, s,
+                           d, F, Y, split_stride);
+    else if (fmt == 2)
+        hipLaunchKernelGGL(k_rpl_down<2>, grid, dim3(256), 0, st, down, estride, hh, hl, hs, hm, s,
+                           d, F, Y, split_stride);
     else
-        hipLaunchKernelGGL(k_rpl_down<false>, dim3(d / 64, slots, ksplit), dim3(256), 0, st, down,
-                           estride, hh, hl, hs, hm, s, d, F, Y, split_stride);
+        hipLaunchKernelGGL(k_rpl_down<0>, grid, dim3(256), 0, st, down, estride, hh, hl, hs, hm, s,
+                           d, F, Y, split_stride);
     return hipGetLastError();
 }
 

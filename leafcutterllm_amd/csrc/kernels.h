@@ -77,12 +77,12 @@ hipError_t launch_rpl_gateup(const uint8_t *gate, const uint8_t *up, int64_t est
                              const int8_t *xh, const int8_t *xl, const float *xs, const float *xm,
                              const SlotArgsHost &sa, int slots, int d, int F, float *Hf, int8_t *hh,
                              int8_t *hl, float *hs, float *hm, _Float16 *h16, _Float16 *hs16,
-                             const ChainArgs &ch, hipStream_t st);
-// q6: the down matrices are RPL64 Q6_K instead of RPL64 Q4_K
+                             const ChainArgs &ch, hipStream_t st, bool q8 = false);
+// fmt: the down matrices are RPL64 Q4_K (0), Q6_K (1) or Q8_0 (2)
 hipError_t launch_rpl_down(const uint8_t *down, int64_t estride, const int8_t *hh,
                            const int8_t *hl, const float *hs, const float *hm,
                            const SlotArgsHost &sa, int slots, int d, int F, int ksplit, float *Y,
-                           int64_t split_stride, hipStream_t st, bool q6 = false);
+                           int64_t split_stride, hipStream_t st, int fmt = 0);
 
 // Matrix-core path on the RPL64 layout: activations as f16 hi/lo pieces
 // (per token and super-block: hi[256] then lo[256]) plus per-sub-block sums,
@@ -127,6 +127,10 @@ hipError_t launch_debug_sigmoid(const float *x, int64_t n, float *out, hipStream
 // RPL64 eligibility: Q4_K, rows tile by 64, columns are whole super-blocks.
 inline bool rpl64_ok(int qt, int64_t rows, int64_t cols) {
     return qt == 12 && rows % 64 == 0 && cols % 256 == 0;
+}
+// Q8_0 matrices the row-per-lane kernels serve (RPL64 Q8_0 layout)
+inline bool rpl64_q8_ok(int qt, int64_t rows, int64_t cols) {
+    return qt == 8 && rows % 64 == 0 && cols % 256 == 0;
 }
 // Q6_K matrices the matrix-core down serves (RPL64 Q6_K layout)
 inline bool rpl64_q6_ok(int qt, int64_t rows, int64_t cols) {

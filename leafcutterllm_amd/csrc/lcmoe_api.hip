@@ -42,6 +42,7 @@ struct ExpertSet {  // one family of experts (routed or shared)
     // RPL64 Q6_K down and split-layout Q4_K down (F an odd multiple of 128),
     // both matrix-core only
     bool rpl_gu = false, rpl_dn = false, q6_dn = false, split_dn = false;
+    bool q8 = false;  // RPL64 Q8_0 gate, up and down (row-per-lane only)
     uint8_t *gate = nullptr, *up = nullptr, *down = nullptr;
     int64_t sz_gu = 0, sz_dn = 0;
     // H between the two products: f32 (generic down), int8 limbs (row-per-lane
@@ -147,11 +148,14 @@ lcmoe_status upload_stack(lcmoe_handle *h, uint8_t **dst, const uint8_t *src, in
         for (unsigned t = 0; t < nth; t++)
             th.emplace_back([&, t] {
                 const int64_t NB = cols / 256;
-                const bool q6 = qt == LCMOE_TYPE_Q6_K;
-                const int64_t tb = NB * (q6 ? 13 * 1024 + 128 : 9 * 1024), bb = q6 ? 210 : 144;
+                const bool q6 = qt == LCMOE_TYPE_Q6_K, q8 = qt == LCMOE_TYPE_Q8_0;
+                const int64_t tb = NB * (q6 ? 13 * 1024 + 128 : q8 ? 17 * 1024 : 9 * 1024);
+                const int64_t bb = q6 ? 210 : q8 ? 272 : 144;  // bytes per row and 256 columns
                 for (int64_t rt = t; rt < tiles; rt += nth) {
                     if (q6)
                         repack_rpl64_q6k(s + rt * 64 * NB * bb, buf.data() + rt * tb, 64, cols);
+                    else if (q8)
+                        repack_rpl64_q8(s + rt * 64 * NB * bb, buf.data() + rt * tb, 64, cols);
                     else
                         repack_rpl64_q4k(s + rt * 64 * NB * bb, buf.data() + rt * tb, 64, cols);
                 }
@@ -203,7 +207,7 @@ hipError_t timed(lcmoe_handle *h, hipStream_t st, int slot, Fn fn) {
 // launch 10% faster at 4 splits than at 2); each wave keeps >= 2 super-blocks
 // where it can (it loads the next while computing the current one).
 int choose_ksplit(const ExpertSet &s, int d, int active) {
-    if (!s.rpl_dn && !s.q6_dn) return 1;
+    if (!s.rpl_dn && !s.q6_dn && !s.q8) return 1;
     const int NB = s.F / 256, tiles = (d / 64) * std::max(1, active);
     int ks = 1;
     while (ks < s.kmax && tiles * ks < 1024 && NB >= 4 * ks * 2 * 2) ks *= 2;
@@ -236,21 +240,23 @@ lcmoe_status setup_set(lcmoe_handle *h, ExpertSet &s, int n, int F, int qgu, int
     s.rpl_dn = s.rpl_gu && rpl64_ok(qdn, d, F);
     s.q6_dn = s.rpl_gu && rpl64_q6_ok(qdn, d, F);
     s.split_dn = s.rpl_gu && qdn == LCMOE_TYPE_Q4_K && d % 64 == 0 && F % 256 == 128;
-    s.kmax = s.rpl_dn || s.q6_dn || s.split_dn ? kMaxKSplit : 1;
+    s.q8 = rpl64_q8_ok(qgu, F, d) && rpl64_q8_ok(qdn, d, F);
+    s.kmax = s.rpl_dn || s.q6_dn || s.split_dn || s.q8 ? kMaxKSplit : 1;
     int64_t szu = 0;
     lcmoe_status st;
-    if ((st = upload_stack(h, &s.gate, gate, n, qgu, F, d, s.rpl_gu, &s.sz_gu, false, gate2, n2)))
+    const bool rgu = s.rpl_gu || s.q8;
+    if ((st = upload_stack(h, &s.gate, gate, n, qgu, F, d, rgu, &s.sz_gu, false, gate2, n2)))
         return st;
-    if ((st = upload_stack(h, &s.up, up, n, qgu, F, d, s.rpl_gu, &szu, false, up2, n2))) return st;
-    if ((st = upload_stack(h, &s.down, down, n, qdn, d, F, s.rpl_dn || s.q6_dn, &s.sz_dn,
+    if ((st = upload_stack(h, &s.up, up, n, qgu, F, d, rgu, &szu, false, up2, n2))) return st;
+    if ((st = upload_stack(h, &s.down, down, n, qdn, d, F, s.rpl_dn || s.q6_dn || s.q8, &s.sz_dn,
                            s.split_dn, down2, n2)))
         return st;
-    if (s.rpl_dn || s.q6_dn) {  // limbs for the row-per-lane down
+    if (s.rpl_dn || s.q6_dn || s.q8) {  // limbs for the row-per-lane down
         if ((st = alloc_n(h, &s.hh, positions * F))) return st;
         if ((st = alloc_n(h, &s.hl, positions * F))) return st;
         if ((st = alloc_n(h, &s.hs, positions * F / 32))) return st;
         if ((st = alloc_n(h, &s.hm, positions * F / 32))) return st;
-    } else if (!s.q6_dn && !s.split_dn) {
+    } else if (!s.split_dn) {
         if ((st = alloc_n(h, &s.Hf, positions * F))) return st;
     }
     if (s.rpl_gu) {
@@ -341,7 +347,8 @@ extern "C" lcmoe_status lcmoe_create(const lcmoe_desc *desc, const lcmoe_weights
                                      D.type_down_sh, w->gate_sh, w->up_sh, w->down_sh, S * Tm)))
             return bail(st);
     }
-    const bool limbs = h->routed.rpl_gu || (S > 0 && !h->fused && h->shared.rpl_gu);
+    const bool limbs = h->routed.rpl_gu || h->routed.q8 ||
+                       (S > 0 && !h->fused && (h->shared.rpl_gu || h->shared.q8));
     if ((st = alloc_n(h, &h->x_dev, Tm * d))) return bail(st);
     if ((st = alloc_n(h, &h->y_dev, Tm * d))) return bail(st);
     if ((st = alloc_n(h, &h->logits, Tm * E))) return bail(st);
@@ -428,16 +435,16 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
     // for the matrix-core downs, int8 limbs for the row-per-lane ones (Q4_K
     // and Q6_K below one token per expert), f32 for the generic one
     const bool h16_out = (pl.mfma && (s.rpl_dn || s.q6_dn)) || s.split_dn;
-    const bool limb_out = !pl.mfma && (s.rpl_dn || s.q6_dn);
+    const bool limb_out = !pl.mfma && (s.rpl_dn || s.q6_dn || s.q8);
     HIP_TRY(timed(h, st, shared || fused_only ? kSlotGateUpSh : kSlotGateUp, [&] {
         if (pl.mfma)
             return launch_mfma_gateup(s.gate, s.up, s.sz_gu, h->x16, h->x16s, sa, slots,
                                       pl.chunks, d, s.F, h16_out ? s.h16 : nullptr, s.h16s,
                                       h16_out ? nullptr : s.Hf, ch, st);
-        if (s.rpl_gu)
+        if (s.rpl_gu || s.q8)
             return launch_rpl_gateup(s.gate, s.up, s.sz_gu, h->xh, h->xl, h->xs, h->xm, sa,
                                      slots, d, s.F, s.Hf, limb_out ? s.hh : nullptr, s.hl,
-                                     s.hs, s.hm, h16_out ? s.h16 : nullptr, s.h16s, ch, st);
+                                     s.hs, s.hm, h16_out ? s.h16 : nullptr, s.h16s, ch, st, s.q8);
         return launch_generic_gateup(s.qt_gu, s.gate, s.up, s.sz_gu, x, sa, slots, d, s.F,
                                      s.Hf, nullptr, nullptr, nullptr, nullptr, ch, st);
     }));
@@ -445,9 +452,9 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
         if (s.q6_dn && pl.mfma)
             return launch_mfma_down_q6(s.down, s.sz_dn, s.h16, sa, slots, pl.chunks, d, s.F,
                                        pl.ks, s.Y, s.positions * d, st);
-        if (s.q6_dn)
+        if (s.q6_dn || s.q8)
             return launch_rpl_down(s.down, s.sz_dn, s.hh, s.hl, s.hs, s.hm, sa, slots, d, s.F,
-                                   pl.ks, s.Y, s.positions * d, st, true);
+                                   pl.ks, s.Y, s.positions * d, st, s.q8 ? 2 : 1);
         if (s.split_dn || (s.rpl_dn && pl.mfma))
             return launch_mfma_down(s.down, s.sz_dn, s.h16, s.h16s, sa, slots, pl.chunks, d,
                                     s.F, pl.ks, s.Y, s.positions * d, st);
@@ -477,8 +484,8 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
     const bool sep_f = Sf > 0 && !together;
     const bool mfma = pr.mfma || ps.mfma || pf.mfma;
     // int8 limbs only feed the row-per-lane kernels
-    const bool limbs = (h->routed.rpl_gu && (!pr.mfma || (sep_f && !pf.mfma))) ||
-                       (S > 0 && !h->fused && h->shared.rpl_gu && !ps.mfma);
+    const bool limbs = ((h->routed.rpl_gu || h->routed.q8) && (!pr.mfma || (sep_f && !pf.mfma))) ||
+                       (S > 0 && !h->fused && (h->shared.rpl_gu || h->shared.q8) && !ps.mfma);
     RouterArgs ra{};
     ra.x = x;
     ra.wrt = h->wrt;

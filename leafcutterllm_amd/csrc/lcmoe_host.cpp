@@ -367,6 +367,27 @@ void repack_rpl64_q4k_split(const uint8_t *src, uint8_t *dst, int64_t rows, int6
         }
 }
 
+// RPL64 repack of a GGUF Q8_0 [rows, cols] matrix (rows % 64 == 0,
+// cols % 256 == 0): per 64-row tile and 256-column group (eight 34-byte
+// blocks per row), chunk 0 holds each row's eight f16 d (16 bytes) and
+// chunks 1-16 its 256 quants, 16 per chunk, each chunk's 64 rows
+// contiguous: 17 KiB per tile and group.  Same bytes, new order.
+void repack_rpl64_q8(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t cols) {
+    const int64_t NG = cols / 256, row_bytes = cols / 32 * 34;
+    for (int64_t rt = 0; rt < rows / 64; rt++)
+        for (int64_t g = 0; g < NG; g++) {
+            uint8_t *o = dst + (rt * NG + g) * 17 * 1024;
+            for (int r = 0; r < 64; r++) {
+                const uint8_t *grp = src + (rt * 64 + r) * row_bytes + g * 8 * 34;
+                for (int b = 0; b < 8; b++) {
+                    std::memcpy(o + r * 16 + 2 * b, grp + 34 * b, 2);
+                    std::memcpy(o + (1 + 2 * b) * 1024 + r * 16, grp + 34 * b + 2, 16);
+                    std::memcpy(o + (2 + 2 * b) * 1024 + r * 16, grp + 34 * b + 18, 16);
+                }
+            }
+        }
+}
+
 // RPL64 repack of a GGUF Q6_K [rows, cols] matrix (rows % 64 == 0,
 // cols % 256 == 0): per 64-row tile and super-block, the 210-byte blocks of
 // the 64 rows are cut into thirteen 16-byte chunks (ql: 0-7, qh: 8-11,

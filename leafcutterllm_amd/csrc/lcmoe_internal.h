@@ -88,6 +88,8 @@ lcmoe_status scan_weights(const lcmoe_desc *d, const lcmoe_weights *w);
 void repack_rpl64_q4k(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t cols);
 // RPL64 repack of Q6_K (defined in lcmoe_host.cpp, layout documented there).
 void repack_rpl64_q6k(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t cols);
+// RPL64 repack of Q8_0 (lcmoe_host.cpp).
+void repack_rpl64_q8(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t cols);
 // Split repack of Q4_K with cols an odd multiple of 128 (lcmoe_host.cpp).
 void repack_rpl64_q4k_split(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t cols);
 

@@ -75,6 +75,9 @@ SMALL = {
     # d_ff an odd multiple of 128: Q4_K down blocks straddle rows (split layout)
     "q4k-split-shared": small_config(
         "split", 256, 384, 8, 2, L.ROUTE_SOFTMAX_RENORM, Q4, Q4, n_shared=2, d_ff_shared=640),
+    # Q8_0 everywhere in the row-per-lane layout, with a fused shared expert
+    "q8-rpl-shared": small_config(
+        "q8rpl", 256, 512, 8, 2, L.ROUTE_SOFTMAX, Q8, Q8, n_shared=1, d_ff_shared=512),
     # Q6_K down with a 4-way column split and 4 shared experts
     "q6k-down-e16": small_config(
         "q6dn", 512, 1024, 16, 4, L.ROUTE_SOFTMAX, Q4, Q6, n_shared=1, d_ff_shared=512),
