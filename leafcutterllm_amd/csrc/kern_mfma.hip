@@ -1018,8 +1018,142 @@ __device__ __forceinline__ void block_pass_q6(g_u8 *wb, const uint32_t (&lo)[2],
     if (kb < kb1) step_q6(wb, lo, rlo, dlo, kb, s_stage0, s_stage1, src, w, acc, wave, lane);
 }
 
-// grid (d/256 row blocks, slots, ksplit x pass groups), as k_mfma_down; every
-// pass takes 32 tokens.
+// ---- Q6_K down, 16-token passes (v_mfma_f32_16x16x32_f16) ------------------
+// A wave's 64 rows are four 16-row tiles (half m, tile t: rows 32m + 16t ..).
+// Lane (r16, c4) takes row r16 of each tile and, per 32-column group j of
+// block half n, columns 8c4 .. 8c4+7: the 8 bytes at 8(c4 & 1) of ql chunks
+// 4n + c4/2 (groups 0, 2) and 4n + 2 + c4/2 (groups 1, 3) and of qh chunk
+// 8 + 2n + c4/2; its scale is sc[8n + 2j + c4/2].  The split B1, B2 of the
+// 32-token kernel is per element, so one MFMA may span two scale groups.
+struct W6t {
+    u32x4 sc;
+    uint32_t d;
+    u32x2 q[2][3];  // per half n: ql (groups 0, 2), ql (groups 1, 3), qh
+};
+
+__device__ __forceinline__ void load_w6t_head(W6t &w, g_u8 *base, uint32_t rlo, uint32_t dlo,
+                                              int kb) {
+    w.sc = gload<u32x4>(base + (rlo + (uint32_t)(kb * kQ6Stride + 12 * 1024)));
+    w.d = gload<uint16_t>(base + (dlo + (uint32_t)(kb * kQ6Stride + kQ6Chunks * 1024)));
+}
+
+// lo: row offset (row * 16) + 8 (c4 & 1); cb = c4 / 2
+__device__ __forceinline__ void load_w6t_half(W6t &w, g_u8 *base, uint32_t lo, int kb, int n,
+                                              int cb) {
+    w.q[n][0] = load_q6(base, lo, kb, 4 * n + cb);
+    w.q[n][1] = load_q6(base, lo, kb, 4 * n + 2 + cb);
+    w.q[n][2] = load_q6(base, lo, kb, 8 + 2 * n + cb);
+}
+
+__device__ __forceinline__ void step16_q6(g_u8 *wb, const uint32_t (&lo)[2][2],
+                                          const uint32_t (&rlo)[2][2], const uint32_t (&dlo)[2][2],
+                                          int kn, const uint8_t *cur, uint8_t *nxt,
+                                          const StageSrc &src, W6t (&w)[2][2],
+                                          float4v (&acc)[2][2], int wave, int lane) {
+    const int r16 = lane & 15, c4 = lane >> 4, cb = c4 >> 1;
+    StageRegs<4> act;
+    stage_load(act, src, kn, wave, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    // scales are read from w and reloaded with kn after the last group
+    float dd[2][2];
+#pragma unroll
+    for (int m = 0; m < 2; m++)
+#pragma unroll
+        for (int t = 0; t < 2; t++) dd[m][t] = dh2f(w[m][t].d & 0xffff);
+    float4v S1[2][2], S2[2][2];
+#pragma unroll
+    for (int m = 0; m < 2; m++)
+#pragma unroll
+        for (int t = 0; t < 2; t++) S1[m][t] = S2[m][t] = float4v{};
+    const uint8_t *tokrow = cur + r16 * kTokBytes;
+    const half2v k1024 = half2v{(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const half2v k1032 = half2v{(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const half2v k1056 = half2v{(_Float16)-1056.0f, (_Float16)-1056.0f};
+#pragma unroll
+    for (int n = 0; n < 2; n++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int col = 2 * (128 * n + 32 * j + 8 * c4);  // bytes
+            const half8 ah = *reinterpret_cast<const half8 *>(tokrow + col);
+            const half8 al = *reinterpret_cast<const half8 *>(tokrow + 512 + col);
+            const int b = 2 * (j & 1) + cb;  // scale byte within word 2n + j/2
+#pragma unroll
+            for (int m = 0; m < 2; m++)
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const uint32_t wv = w[m][t].sc[2 * n + (j >> 1)];
+                    const half2v sl2 = magic_bb(wv & 0x0F0F0F0Fu, b) + k1024;
+                    const half2v sh2 = magic_bb(((wv >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u, b) + k1032;
+                    const half2v c1 = sh2 * k1056, c2 = sl2 * k1056;
+                    const u32x2 qa = w[m][t].q[n][0], qb = w[m][t].q[n][1], qh = w[m][t].q[n][2];
+                    const uint32_t g0 = q6_group(qa.x, qb.x, qh.x, j);
+                    const uint32_t g1 = q6_group(qa.y, qb.y, qh.y, j);
+                    half8 b1, b2;
+                    dec6(g0, g1, sh2, c1, sl2, c2, b1, b2);
+                    S1[m][t] = mfma16(ah, b1, S1[m][t]);
+                    S1[m][t] = mfma16(al, b1, S1[m][t]);
+                    S2[m][t] = mfma16(ah, b2, S2[m][t]);
+                    S2[m][t] = mfma16(al, b2, S2[m][t]);
+                }
+        }
+#pragma unroll
+        for (int m = 0; m < 2; m++)
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                load_w6t_half(w[m][t], wb, lo[m][t], kn, n, cb);
+                if (n == 1) load_w6t_head(w[m][t], wb, rlo[m][t], dlo[m][t], kn);
+            }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int m = 0; m < 2; m++)
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const float d16 = 16.0f * dd[m][t];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                acc[m][t][i] = __builtin_fmaf(d16, S1[m][t][i], acc[m][t][i]);
+                acc[m][t][i] = __builtin_fmaf(dd[m][t], S2[m][t][i], acc[m][t][i]);
+            }
+        }
+    stage_store(nxt, act, wave, lane);
+    lds_barrier();
+}
+
+__device__ __forceinline__ void block_pass16_q6(g_u8 *wb, const uint32_t (&lo)[2][2],
+                                                const uint32_t (&rlo)[2][2],
+                                                const uint32_t (&dlo)[2][2], int kb0, int kb1,
+                                                const StageSrc &src, float4v (&acc)[2][2]) {
+    const int lane = threadIdx.x & 63, cb = (lane >> 4) >> 1;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int last = kb1 - 1;
+    asm volatile("" : "+s"(kb0));  // see block_pass()
+    W6t w[2][2];
+    StageRegs<4> act;
+    stage_load(act, src, kb0, wave, lane);
+#pragma unroll
+    for (int m = 0; m < 2; m++)
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            load_w6t_head(w[m][t], wb, rlo[m][t], dlo[m][t], kb0);
+#pragma unroll
+            for (int n = 0; n < 2; n++) load_w6t_half(w[m][t], wb, lo[m][t], kb0, n, cb);
+        }
+    stage_store(s_stage0, act, wave, lane);
+    lds_barrier();
+    int kb = kb0;
+    for (; kb + 2 <= kb1; kb += 2) {
+        step16_q6(wb, lo, rlo, dlo, kb + 1, s_stage0, s_stage1, src, w, acc, wave, lane);
+        step16_q6(wb, lo, rlo, dlo, min(kb + 2, last), s_stage1, s_stage0, src, w, acc, wave,
+                  lane);
+    }
+    if (kb < kb1) step16_q6(wb, lo, rlo, dlo, kb, s_stage0, s_stage1, src, w, acc, wave, lane);
+}
+
+// grid (d/256 row blocks, slots, ksplit x pass groups), as k_mfma_down.  P16:
+// passes of 16 tokens (16x16x32 MFMAs), else of 32 (32x32x16); one kind per
+// kernel keeps each within the register file.
+template <bool P16>
 __global__ __launch_bounds__(256, 2) void k_mfma_down_q6(
     const uint8_t *__restrict__ down, int64_t estride, const _Float16 *__restrict__ h16,
     SlotArgs sa, int d, int F, int ksplit, float *__restrict__ Y, int64_t split_stride) {
@@ -1051,7 +1185,8 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down_q6(
     const uint32_t dlo[2] = {(uint32_t)r * 2, (uint32_t)(32 + r) * 2};
     float *Yz = Y + (int64_t)bz * split_stride;
     const uint8_t *hb = reinterpret_cast<const uint8_t *>(h16);
-    for (int c = cz * kTok; c < n; c += nz * kTok) {
+    constexpr int kPass = P16 ? 16 : kTok;
+    for (int c = cz * kPass; c < n; c += nz * kPass) {
         StageSrc src;
 #pragma unroll
         for (int i = 0; i < 8; i++)
@@ -1059,6 +1194,35 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down_q6(
         // the sums are not used (Q6_K has no mins): stage a valid row
         src.sums = uniform(hb);
         src.soff = 16 * (uint32_t)lane;
+        if constexpr (P16) {
+            const int r16 = lane & 15, c4 = lane >> 4;
+            uint32_t lo16[2][2], rlo16[2][2], dlo16[2][2];
+#pragma unroll
+            for (int m = 0; m < 2; m++)
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const uint32_t row = 32 * m + 16 * t + r16;
+                    rlo16[m][t] = row * 16;
+                    lo16[m][t] = row * 16 + 8 * (c4 & 1);
+                    dlo16[m][t] = row * 2;
+                }
+            float4v acc[2][2] = {};
+            block_pass16_q6(wb, lo16, rlo16, dlo16, kb0, kb1, src, acc);
+            if (tile0 >= ntile) continue;
+            int rb = tile * 64 + r16;  // opaque: output addresses are formed here
+            asm volatile("" : "+v"(rb));
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int q = c + 4 * c4 + i;
+                if (q < n) {
+                    float *yrow = Yz + (int64_t)(p0 + q) * d + rb;
+#pragma unroll
+                    for (int m = 0; m < 2; m++)
+#pragma unroll
+                        for (int t = 0; t < 2; t++) yrow[32 * m + 16 * t] = acc[m][t][i];
+                }
+            }
+        } else {
         float16v acc[2] = {float16v{}, float16v{}};
         block_pass_q6(wb, lo, rlo, dlo, kb0, kb1, src, acc);
         if (tile0 >= ntile) continue;
@@ -1072,6 +1236,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down_q6(
                 yrow[0] = acc[0][i];
                 yrow[32] = acc[1][i];
             }
+        }
         }
     }
 }
@@ -1121,12 +1286,17 @@ SlotArgs dev_slots(const SlotArgsHost &s) {
 
 hipError_t launch_mfma_down_q6(const uint8_t *down, int64_t estride, const _Float16 *h16,
                                const SlotArgsHost &sa, int slots, int chunks, int d, int F,
-                               int ksplit, float *Y, int64_t split_stride, hipStream_t st) {
+                               int ksplit, float *Y, int64_t split_stride, hipStream_t st,
+                               bool p16) {
     const int tiles = d / 64;
     if (chunks < 1 || ksplit < 1 || (int64_t)chunks * ksplit > 65535) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_mfma_down_q6, dim3((tiles + kWaves - 1) / kWaves, slots, ksplit * chunks),
-                       dim3(256), 0, st, down, estride, h16, dev_slots(sa), d, F, ksplit, Y,
-                       split_stride);
+    const dim3 grid((tiles + kWaves - 1) / kWaves, slots, ksplit * chunks);
+    if (p16)
+        hipLaunchKernelGGL(k_mfma_down_q6<true>, grid, dim3(256), 0, st, down, estride, h16,
+                           dev_slots(sa), d, F, ksplit, Y, split_stride);
+    else
+        hipLaunchKernelGGL(k_mfma_down_q6<false>, grid, dim3(256), 0, st, down, estride, h16,
+                           dev_slots(sa), d, F, ksplit, Y, split_stride);
     return hipGetLastError();
 }
 

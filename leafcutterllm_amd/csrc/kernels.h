@@ -98,11 +98,12 @@ hipError_t launch_mfma_down(const uint8_t *down, int64_t estride, const _Float16
                             const _Float16 *hs, const SlotArgsHost &sa, int slots, int chunks,
                             int d, int F, int ksplit, float *Y, int64_t split_stride,
                             hipStream_t st);
-// The same down product for Q6_K weights in the RPL64 Q6_K layout (32-token
-// passes; H as f16 pieces, no sums needed).
+// The same down product for Q6_K weights in the RPL64 Q6_K layout (H as f16
+// pieces, no sums needed), in passes of 16 tokens (p16) or 32.
 hipError_t launch_mfma_down_q6(const uint8_t *down, int64_t estride, const _Float16 *h16,
                                const SlotArgsHost &sa, int slots, int chunks, int d, int F,
-                               int ksplit, float *Y, int64_t split_stride, hipStream_t st);
+                               int ksplit, float *Y, int64_t split_stride, hipStream_t st,
+                               bool p16);
 
 // Routing weights computed by the combine from exact logits (fast-router
 // path); logits == null: the weights are already in topk_w.

@@ -384,6 +384,7 @@ struct Plan {
     int slots, ks;
     int chunks;  // blocks sharing one matrix-core slot's 32-token passes
     int sl, ns;  // fused shared experts: tokens per slot, slots per expert
+    int per_slot;  // average tokens per slot
 };
 
 // fused: the routed plan also carries the fused shared experts (slots
@@ -409,6 +410,7 @@ static Plan plan_set(lcmoe_handle *h, const ExpertSet &s, bool shared, int T, in
     const int64_t per_slot =
         shared ? T : ((int64_t)T * D.n_expert_used + p.slots - 1) / std::max(1, p.slots);
     p.chunks = p.mfma ? (int)std::min<int64_t>(64, std::max<int64_t>(1, (per_slot + 31) / 32)) : 1;
+    p.per_slot = (int)std::min<int64_t>(per_slot, INT32_MAX);
     // fused shared experts: slices of the tokens one slot takes (the passes
     // of its chunk blocks, or one row-per-lane pass)
     p.sl = p.mfma ? 32 * p.chunks : 4;
@@ -449,9 +451,9 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
                                      s.Hf, nullptr, nullptr, nullptr, nullptr, ch, st);
     }));
     HIP_TRY(timed(h, st, shared || fused_only ? kSlotDownSh : kSlotDown, [&] {
-        if (s.q6_dn && pl.mfma)
+        if (s.q6_dn && pl.mfma)  // 16-token passes while slots average at most 16 tokens
             return launch_mfma_down_q6(s.down, s.sz_dn, s.h16, sa, slots, pl.chunks, d, s.F,
-                                       pl.ks, s.Y, s.positions * d, st);
+                                       pl.ks, s.Y, s.positions * d, st, pl.per_slot <= 16);
         if (s.q6_dn || s.q8)
             return launch_rpl_down(s.down, s.sz_dn, s.hh, s.hl, s.hs, s.hm, sa, slots, d, s.F,
                                    pl.ks, s.Y, s.positions * d, st, s.q8 ? 2 : 1);
@@ -478,7 +480,7 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
     const bool together = Sf > 0 && pr0.chunks == 1;
     const int fused = together ? Sf : 0;
     const Plan pr = together ? plan_set(h, h->routed, false, T, Sf) : pr0;
-    const Plan off{false, 0, 1, 1, 4, 0};
+    const Plan off{false, 0, 1, 1, 4, 0, 0};
     const Plan pf = Sf > 0 && !together ? plan_set(h, h->routed, false, T, Sf, true) : off;
     const Plan ps = S > 0 && !h->fused ? plan_set(h, h->shared, true, T) : off;
     const bool sep_f = Sf > 0 && !together;

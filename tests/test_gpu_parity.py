@@ -94,6 +94,18 @@ def test_small_layer_parity(name, T):
     assert res["rel_l2"] < 1e-3
 
 
+@pytest.mark.parametrize("name,T", [("q6k-down-e16", 160), ("q4k-split-shared", 200),
+                                    ("sigmoid-group-q6k", 300)])
+def test_small_layer_parity_many_tokens(name, T):
+    """Tens of tokens per expert: 32-token matrix-core passes (Q6_K, split
+    Q4_K), several pass groups per slot and prefill-style shared launches."""
+    cfg = SMALL[name]
+    layer = L.synth_layer(cfg, seed=5)
+    x = L.synth_x(cfg, T, seed=5, index=T)
+    res = run_and_check(cfg, layer, x, y_subset=[0, 1, T // 2, T - 1])
+    assert res["rel_l2"] < 1e-3
+
+
 def test_handle_reuse_and_determinism():
     cfg = SMALL["sigmoid-group-q6k"]
     layer = L.synth_layer(cfg, seed=2)
