@@ -509,6 +509,38 @@ void lco_transpose(const float *a, float *b, int rows, int cols) {
 /* CpuBackend::silu, rust/src/backend/cpu.rs:62-64: v * (1 / (1 + exp(-v))). */
 float lco_silu(float v) { return v * (1.0f / (1.0f + expf(-v))); }
 
+/* CpuBackend::rms_norm, rust/src/backend/cpu.rs:49-60, on the x86_64 SIMD
+ * paths it calls: simd_sum_sq (rust/src/kernels/simd.rs:390-409) keeps four
+ * lane sums, lane j adding x[i]*x[i] (multiply, then add) for i = j, j+4,
+ * ... up to the last full group of four; the lanes are summed in order from
+ * 0.0 (Iterator::sum) and the remaining elements added one by one.
+ * mean_sq = sum / hidden; scale = 1 / sqrt(mean_sq + eps); then
+ * simd_vec_scale_mul (simd.rs:353-369) writes (x[i] * scale) * w[i]. */
+void lco_rms_norm(const float *x, const float *w, float eps, int T, int d, float *out) {
+    for (int t = 0; t < T; t++) {
+        const float *r = x + (size_t)t * d;
+        float lane[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        int i = 0;
+        for (; i + 4 <= d; i += 4)
+            for (int j = 0; j < 4; j++) {
+                const float p = r[i + j] * r[i + j];
+                lane[j] = p + lane[j];
+            }
+        float sum = 0.0f;
+        for (int j = 0; j < 4; j++) sum = sum + lane[j];
+        for (; i < d; i++) {
+            const float p = r[i] * r[i];
+            sum = sum + p;
+        }
+        const float mean_sq = sum / (float)d;
+        const float scale = 1.0f / sqrtf(mean_sq + eps);
+        for (int k = 0; k < d; k++) {
+            const float a = r[k] * scale;
+            out[(size_t)t * d + k] = a * w[k];
+        }
+    }
+}
+
 /* CpuBackend::softmax, rust/src/backend/cpu.rs:66-79 (one row): max folded
  * from -inf with f32::max, sum of exp(x - max) in order, then divide. */
 void lco_softmax(const float *x, float *y, int n) {

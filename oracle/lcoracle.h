@@ -24,6 +24,8 @@
  *                          float64, FMA-lane vs mul+add-tail bit behaviour
  *   silu / softmax       : closed form in float64, tensor.rs:211-217 KAT
  *   lc_expf / sigmoid    : <= 2 ulp vs float64 exp over a dense sweep
+ *   rms_norm             : reference test tensor.rs:204-209, float64 closed form,
+ *                          exact constant rows, scale-then-weight rounding order
  *   top-k, group top-k   : brute force (full sort) incl. adversarial ties / NaN
  *   dispatch             : brute-force stable sort + permutation invariants
  *   layer forward        : float64 re-computation from dequantised weights,
@@ -105,6 +107,7 @@ void lco_synth_normal(uint64_t seed, uint64_t stream, float stddev, float *out, 
 void lco_matmul(const float *a, const float *b, float *c, int m, int k, int n, int threads);
 void lco_transpose(const float *a, float *b, int rows, int cols);
 float lco_silu(float v);
+void lco_rms_norm(const float *x, const float *w, float eps, int T, int d, float *out);
 void lco_softmax(const float *x, float *y, int n);
 float lco_expf_cw(float x);
 float lco_sigmoid_cw(float x);

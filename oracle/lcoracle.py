@@ -73,6 +73,7 @@ def lib() -> C.CDLL:
             "lco_matmul": (None, [vp, vp, vp, i32, i32, i32, i32]),
             "lco_transpose": (None, [vp, vp, i32, i32]),
             "lco_silu": (f32, [f32]),
+            "lco_rms_norm": (None, [vp, vp, f32, i32, i32, vp]),
             "lco_softmax": (None, [vp, vp, i32]),
             "lco_expf_cw": (f32, [f32]),
             "lco_sigmoid_cw": (f32, [f32]),
@@ -167,6 +168,16 @@ def matmul(a: np.ndarray, b: np.ndarray, threads: int = 1) -> np.ndarray:
 
 def silu(v: float) -> float:
     return float(lib().lco_silu(v))
+
+
+def rms_norm(x: np.ndarray, w: np.ndarray, eps: float = 1e-5) -> np.ndarray:
+    """CpuBackend::rms_norm over the rows of x [T, d] (lco_rms_norm)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    T, d = x.shape
+    out = np.empty_like(x)
+    lib().lco_rms_norm(_p(x), _p(w), eps, T, d, _p(out))
+    return out
 
 
 def softmax(x: np.ndarray) -> np.ndarray:

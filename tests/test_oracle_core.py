@@ -275,6 +275,33 @@ def test_silu_closed_form():
     assert O.silu(0.0) == 0.0
 
 
+def test_rms_norm_reference_test_and_float64():
+    """CpuBackend::rms_norm: the reference's own test (tensor.rs:204-209: finite
+    output for [1, 2, 3]), a float64 closed form within a few ulp, exact
+    results for constant rows, and the weight applied after the scale."""
+    y = O.rms_norm(np.array([[1, 2, 3]], np.float32), np.ones(3, np.float32))
+    assert np.all(np.isfinite(y))
+    rng = np.random.default_rng(3)
+    for d in (3, 8, 33, 256, 4096):
+        x = rng.standard_normal((5, d)).astype(np.float32) * 3
+        w = rng.standard_normal(d).astype(np.float32)
+        y = O.rms_norm(x, w, 1e-5)
+        x64 = x.astype(np.float64)
+        ref = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-5) * w
+        assert np.allclose(y, ref, rtol=4e-6, atol=1e-30), d
+    # a constant row c: mean_sq = c^2 exactly (powers of two), scale = 1/sqrt(c^2 + eps)
+    for c in (0.5, 2.0, 8.0):
+        x = np.full((1, 64), c, np.float32)
+        y = O.rms_norm(x, np.ones(64, np.float32), 0.0)
+        assert np.all(y == np.float32(1.0)), c
+    # scale before weight: (x * s) * w, two roundings
+    x = np.array([[3.0, 4.0, 0.0, 0.0]], np.float32)
+    w = np.array([1.1, 0.7, 1.0, 1.0], np.float32)
+    s = np.float32(1.0) / np.sqrt(np.float32(25.0 / 4.0) + np.float32(1e-5))
+    assert np.array_equal(O.rms_norm(x, w, 1e-5)[0, :2],
+                          (np.float32(x[0, :2] * s) * w[:2]).astype(np.float32))
+
+
 def test_softmax_kat_and_closed_form():
     y = O.softmax(np.array([1.0, 2.0, 3.0], np.float32))  # tensor.rs:211-217
     assert abs(float(np.sum(y)) - 1.0) < 1e-5
