@@ -103,6 +103,9 @@ def main():
     ap.add_argument("--tokens", type=int, default=64, help="headline batch")
     ap.add_argument("--sweep", default="1,8,64")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--norm-residual", action="store_true",
+                    help="time lcmoe_forward_norm_residual_dev (post-attention RMSNorm, "
+                         "the layer and the residual add) instead of lcmoe_forward_dev")
     ap.add_argument("--kernel-events", type=int, default=1,
                     help="time each kernel with HIP events in a second timed region")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -134,6 +137,16 @@ def main():
     min_touched = min(cfg.n_expert, cfg.n_expert_used) * cfg.expert_bytes()
     R = max(2, math.ceil(2 * MALL_BYTES / min_touched) + 1)
     moes = [L.MoeFfn(cfg.desc(Tmax), layer) for _ in range(R)]
+    if args.norm_residual:
+        w_norm = 1.0 + 0.1 * L.configs.synth_normal(0, 77, 1.0, cfg.d_model)
+        for m in moes:
+            m.set_norm(w_norm, 1e-5)
+
+    def step(r: int, T: int) -> None:
+        if args.norm_residual:
+            moes[r].forward_norm_residual_dev(xbufs[(r, T)].ptr, T, ybufs[r].ptr, stream.ptr)
+        else:
+            moes[r].forward_dev(xbufs[(r, T)].ptr, T, ybufs[r].ptr, stream.ptr)
     stream = hip.Stream()
     xbufs = {}
     ybufs = [hip.DeviceBuffer(4 * Tmax * cfg.d_model) for _ in range(R)]
@@ -147,7 +160,7 @@ def main():
         # realised routing of every replica's input -> algorithmic bytes
         call_bytes, gu_bytes, touched = [], [], []
         for r in range(R):
-            moes[r].forward_dev(xbufs[(r, T)].ptr, T, ybufs[r].ptr, stream.ptr)
+            step(r, T)
             stream.synchronize()
             counts = moes[r].dispatch()["counts"]
             b, g, n = algorithmic_bytes(cfg, counts, T)
@@ -155,8 +168,7 @@ def main():
             gu_bytes.append(g)
             touched.append(n)
         for i in range(args.warmup):
-            r = i % R
-            moes[r].forward_dev(xbufs[(r, T)].ptr, T, ybufs[r].ptr, stream.ptr)
+            step(i % R, T)
         stream.synchronize()
 
         def timed_region(events: bool):
@@ -169,8 +181,7 @@ def main():
             stream.synchronize()
             ev0.record(stream)
             for i in range(args.steps):
-                r = i % R
-                moes[r].forward_dev(xbufs[(r, T)].ptr, T, ybufs[r].ptr, stream.ptr)
+                step(i % R, T)
             ev1.record(stream)
             stream.synchronize()
             kern = {}
@@ -217,7 +228,9 @@ def main():
         "data": "synthetic (seeded splitmix64 N(0,1) activations, N(0,0.02) weights quantised to Q4_K)",
         "config": {
             "workload": f"config {args.config}: {cfg.note}, d_model={cfg.d_model}, d_ff={cfg.d_ff}, "
-                        f"E={cfg.n_expert}, top-{cfg.n_expert_used}, T={args.tokens} tokens/step",
+                        f"E={cfg.n_expert}, top-{cfg.n_expert_used}, T={args.tokens} tokens/step"
+                        + (", with RMSNorm + residual" if args.norm_residual else ""),
+            "entry": "lcmoe_forward_norm_residual_dev" if args.norm_residual else "lcmoe_forward_dev",
             "batch": args.tokens, "d_model": cfg.d_model, "d_ff": cfg.d_ff,
             "n_expert": cfg.n_expert, "top_k": cfg.n_expert_used, "replicas": R,
         },

@@ -127,6 +127,25 @@ lcmoe_status lcmoe_forward(lcmoe_handle *h, const float *x, int32_t T, float *y,
 lcmoe_status lcmoe_forward_dev(lcmoe_handle *h, const float *x_dev, int32_t T, float *y_dev,
                                void *stream);
 
+/* Post-attention RMSNorm weight [d_model] f32 and epsilon used by the
+ * lcmoe_forward_norm_residual* calls below (the reference passes 1e-5,
+ * engine.rs:111).  Copied to the device; may be called again to replace it. */
+lcmoe_status lcmoe_set_norm(lcmoe_handle *h, const float *weight, float eps);
+
+/* The FFN half of a decoder layer with its norm and residual fused:
+ *   out = hidden + ffn_forward(rms_norm(hidden, weight, eps))
+ * replacing rust/src/inference/engine.rs:110-115 (rms_norm is
+ * CpuBackend::rms_norm, rust/src/backend/cpu.rs:49-60, reproduced bit for
+ * bit; the add is Tensor::add).  Host buffers, synchronous, as
+ * lcmoe_forward; out may be hidden itself.  LCMOE_ERR_STATE before
+ * lcmoe_set_norm. */
+lcmoe_status lcmoe_forward_norm_residual(lcmoe_handle *h, const float *hidden, int32_t T,
+                                         float *out, int32_t *topk_idx, float *topk_w);
+/* Device-buffer, stream-ordered form (as lcmoe_forward_dev); out_dev is
+ * hidden_dev itself (in place) or does not overlap it. */
+lcmoe_status lcmoe_forward_norm_residual_dev(lcmoe_handle *h, const float *hidden_dev, int32_t T,
+                                             float *out_dev, void *stream);
+
 /* Routing and dispatch of the most recent forward (waits for it):
  * topk_idx/topk_w [T, K]; counts [E]; offsets [E+1] (exclusive scan, offsets[E]
  * = T*K); perm [T*K]: position -> assignment a = t*K + k (stable by a within
@@ -228,6 +247,10 @@ lcmoe_status lcmoe_gguf_moe_layer(lcmoe_gguf *g, int32_t layer, int32_t max_toke
 /* Decode `count` elements of a GGUF tensor with the device decoders and
  * return them as f32 (bit-exact with dequantize_* in kernels/mod.rs). */
 lcmoe_status lcmoe_debug_dequant(int32_t type, const uint8_t *data, int64_t count, float *out);
+/* The device RMSNorm (rows of x [T, d], d % 4 == 0), for bit parity with
+ * CpuBackend::rms_norm (rust/src/backend/cpu.rs:49-60). */
+lcmoe_status lcmoe_debug_rmsnorm(const float *x, const float *w, float eps, int32_t T, int32_t d,
+                                 float *out);
 /* The router's sigmoid evaluated on the device, for host/device bit parity. */
 lcmoe_status lcmoe_debug_sigmoid(const float *x, int64_t n, float *out);
 

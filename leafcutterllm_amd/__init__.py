@@ -7,10 +7,10 @@ from ._lib import (ROUTE_SIGMOID_GROUP, ROUTE_SOFTMAX, ROUTE_SOFTMAX_RENORM, TYP
                    TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0, Desc, LcmoeError, Weights, lib)
 from .configs import CONFIGS, LayerConfig, synth_layer, synth_x
 from .gguf import GgufFile
-from .moe import MoeFfn, debug_dequant, debug_sigmoid
+from .moe import MoeFfn, debug_dequant, debug_rmsnorm, debug_sigmoid
 
 __all__ = [
     "CONFIGS", "LayerConfig", "synth_layer", "synth_x", "MoeFfn", "GgufFile", "Desc", "Weights",
-    "LcmoeError", "lib", "debug_dequant", "debug_sigmoid", "TYPE_F32", "TYPE_Q8_0",
+    "LcmoeError", "lib", "debug_dequant", "debug_rmsnorm", "debug_sigmoid", "TYPE_F32", "TYPE_Q8_0",
     "TYPE_Q4_K", "TYPE_Q6_K", "ROUTE_SOFTMAX_RENORM", "ROUTE_SOFTMAX", "ROUTE_SIGMOID_GROUP",
 ]

@@ -29,7 +29,8 @@ EXPORTS = (
     "lcmoe_quantize", "lcmoe_synth_normal", "lcmoe_debug_dequant", "lcmoe_debug_sigmoid",
     "lcmoe_gguf_open", "lcmoe_gguf_close", "lcmoe_gguf_meta_int", "lcmoe_gguf_meta_str",
     "lcmoe_gguf_tensor", "lcmoe_gguf_block_count", "lcmoe_gguf_is_moe_layer",
-    "lcmoe_gguf_moe_layer",
+    "lcmoe_gguf_moe_layer", "lcmoe_set_norm", "lcmoe_forward_norm_residual",
+    "lcmoe_forward_norm_residual_dev", "lcmoe_debug_rmsnorm",
 )
 
 
@@ -96,6 +97,10 @@ def lib() -> C.CDLL:
         "lcmoe_synth_normal": (None, [u64, u64, f32, vp, i64]),
         "lcmoe_debug_dequant": (i32, [i32, vp, i64, vp]),
         "lcmoe_debug_sigmoid": (i32, [vp, i64, vp]),
+        "lcmoe_debug_rmsnorm": (i32, [vp, vp, f32, i32, i32, vp]),
+        "lcmoe_set_norm": (i32, [vp, vp, f32]),
+        "lcmoe_forward_norm_residual": (i32, [vp, vp, i32, vp, vp, vp]),
+        "lcmoe_forward_norm_residual_dev": (i32, [vp, vp, i32, vp, vp]),
         "lcmoe_gguf_open": (i32, [C.c_char_p, P(vp)]),
         "lcmoe_gguf_close": (None, [vp]),
         "lcmoe_gguf_meta_int": (i32, [vp, C.c_char_p, P(i64)]),

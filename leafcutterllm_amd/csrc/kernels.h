@@ -119,7 +119,12 @@ struct CombineRoute {
 // With cr.logits, w[t,k] is computed here (and stored to topk_w).
 hipError_t launch_combine(const float *Yr, int ks_r, int64_t stride_r, const float *Ys, int ks_s,
                           int64_t stride_s, const int32_t *inv, float *topk_w, int T, int K,
-                          int S, int d, const CombineRoute &cr, float *y, hipStream_t st);
+                          int S, int d, const CombineRoute &cr, float *y, hipStream_t st,
+                          const float *resid = nullptr);
+// out[t] = rms_norm(x[t]) * w, bit-exact with the reference CPU backend
+// (rust/src/backend/cpu.rs:49-60); x, w, out 16-byte aligned, d % 4 == 0.
+hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int T, int d, float *out,
+                          hipStream_t st);
 
 hipError_t launch_debug_dequant(int qt, const uint8_t *src, int64_t count, float *out,
                                 hipStream_t st);

@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <new>
 #include <thread>
 #include <vector>
@@ -29,9 +30,9 @@ using namespace lcmoe;
 namespace {
 
 enum Slot { kSlotRouter, kSlotPrep, kSlotGateUp, kSlotGateUpSh, kSlotDown, kSlotDownSh,
-            kSlotCombine, kNumSlots };
+            kSlotCombine, kSlotNorm, kNumSlots };
 const char *kSlotNames[kNumSlots] = {"router", "act16", "gateup", "gateup_shared", "down",
-                                     "down_shared", "combine"};
+                                     "down_shared", "combine", "rmsnorm"};
 constexpr int kMaxKSplit = 4;
 // largest T * E * d served by the certified per-token router
 constexpr int64_t kFastRouterElems = (int64_t)1 << 24;
@@ -73,6 +74,8 @@ struct lcmoe_handle {
     bool fused = false;  // shared experts stored and launched with the routed ones
     float *x_dev = nullptr, *y_dev = nullptr, *logits = nullptr;
     float *chain_part = nullptr;  // [max_tokens, E] router chain running sums
+    float *norm_w = nullptr, *xn = nullptr;  // post-attention RMSNorm weight, normed rows
+    float norm_eps = 1e-5f;
     int8_t *xh = nullptr, *xl = nullptr;
     float *xs = nullptr, *xm = nullptr;
     _Float16 *x16 = nullptr, *x16s = nullptr;
@@ -468,8 +471,9 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
     return LCMOE_OK;
 }
 
+// y = ffn(x), or y = resid + ffn(x) when resid is given (y may be resid)
 static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, float *y,
-                                    hipStream_t st) {
+                                    hipStream_t st, const float *resid = nullptr) {
     const lcmoe_desc &D = h->desc;
     const int d = D.d_model, E = D.n_expert, K = D.n_expert_used, S = D.n_shared;
     // Fused shared experts ride in the routed launches while every routed
@@ -558,7 +562,7 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
         const int64_t ss = Sf ? h->routed.positions * d : h->shared.positions * d;
         const int kss = !Sf ? ks_s : together ? ks_r : pf.ks;
         return launch_combine(h->routed.Y, ks_r, h->routed.positions * d, Ys, kss, ss, h->inv,
-                              h->topk_w, T, K, S, d, cr, y, st);
+                              h->topk_w, T, K, S, d, cr, y, st, resid);
     }));
     h->last_T = T;
     h->last_stream = st;
@@ -603,6 +607,89 @@ extern "C" lcmoe_status lcmoe_forward(lcmoe_handle *h, const float *x, int32_t T
     lcmoe_status st = enqueue_forward(h, h->x_dev, T, h->y_dev, h->stream);
     if (st) return st;
     HIP_TRY(hipMemcpyAsync(y, h->y_dev, xb, hipMemcpyDeviceToHost, h->stream));
+    if (topk_idx)
+        HIP_TRY(hipMemcpyAsync(topk_idx, h->topk_idx, kb * 4, hipMemcpyDeviceToHost, h->stream));
+    if (topk_w) HIP_TRY(hipMemcpyAsync(topk_w, h->topk_w, kb * 4, hipMemcpyDeviceToHost, h->stream));
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    return LCMOE_OK;
+}
+
+extern "C" lcmoe_status lcmoe_set_norm(lcmoe_handle *h, const float *weight, float eps) {
+    clear_error();
+    if (!h || !weight) return fail(LCMOE_ERR_INVALID_ARG, "handle or weight is NULL");
+    if (!(eps >= 0.0f) || !std::isfinite(eps))
+        return fail(LCMOE_ERR_INVALID_ARG, "eps must be finite and >= 0");
+    HIP_TRY(hipSetDevice(h->device));
+    const int d = h->desc.d_model;
+    lcmoe_status st;
+    if (!h->norm_w) {
+        if ((st = alloc_n(h, &h->norm_w, d))) return st;
+        if ((st = alloc_n(h, &h->xn, (size_t)h->desc.max_tokens * d))) return st;
+    }
+    // the stream may still be reading the previous weight
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    if (h->last_stream) HIP_TRY(hipStreamSynchronize(h->last_stream));
+    HIP_TRY(hipMemcpy(h->norm_w, weight, sizeof(float) * d, hipMemcpyHostToDevice));
+    h->norm_eps = eps;
+    return LCMOE_OK;
+}
+
+static lcmoe_status enqueue_norm_residual(lcmoe_handle *h, const float *hidden, int32_t T,
+                                          float *out, hipStream_t st) {
+    HIP_TRY(timed(h, st, kSlotNorm, [&] {
+        return launch_rmsnorm(hidden, h->norm_w, h->norm_eps, T, h->desc.d_model, h->xn, st);
+    }));
+    return enqueue_forward(h, h->xn, T, out, st, hidden);
+}
+
+extern "C" lcmoe_status lcmoe_forward_norm_residual_dev(lcmoe_handle *h, const float *hidden_dev,
+                                                        int32_t T, float *out_dev, void *stream) {
+    clear_error();
+    if (!h) return fail(LCMOE_ERR_INVALID_ARG, "handle is NULL");
+    if (!h->norm_w) return fail(LCMOE_ERR_STATE, "lcmoe_set_norm has not been called");
+    if (T < 0 || T > h->desc.max_tokens)
+        return fail(LCMOE_ERR_INVALID_ARG, "T=%d outside [0, max_tokens=%d]", T, h->desc.max_tokens);
+    if (T > 0 && (!hidden_dev || !out_dev))
+        return fail(LCMOE_ERR_INVALID_ARG, "hidden or out is NULL");
+    if (((uintptr_t)hidden_dev | (uintptr_t)out_dev) & 15)
+        return fail(LCMOE_ERR_INVALID_ARG, "hidden and out must be 16-byte aligned");
+    if (out_dev != hidden_dev && T > 0) {
+        const size_t rb = sizeof(float) * (size_t)T * h->desc.d_model;
+        const uintptr_t a = (uintptr_t)hidden_dev, b = (uintptr_t)out_dev;
+        if (a < b + rb && b < a + rb)
+            return fail(LCMOE_ERR_INVALID_ARG, "out must be hidden itself or not overlap it");
+    }
+    HIP_TRY(hipSetDevice(h->device));
+    hipStream_t st = stream ? (hipStream_t)stream : h->stream;
+    if (T == 0) {
+        h->last_T = 0;
+        h->last_stream = st;
+        return LCMOE_OK;
+    }
+    return enqueue_norm_residual(h, hidden_dev, T, out_dev, st);
+}
+
+extern "C" lcmoe_status lcmoe_forward_norm_residual(lcmoe_handle *h, const float *hidden,
+                                                    int32_t T, float *out, int32_t *topk_idx,
+                                                    float *topk_w) {
+    clear_error();
+    if (!h) return fail(LCMOE_ERR_INVALID_ARG, "handle is NULL");
+    if (!h->norm_w) return fail(LCMOE_ERR_STATE, "lcmoe_set_norm has not been called");
+    if (T < 0 || T > h->desc.max_tokens)
+        return fail(LCMOE_ERR_INVALID_ARG, "T=%d outside [0, max_tokens=%d]", T, h->desc.max_tokens);
+    HIP_TRY(hipSetDevice(h->device));
+    if (T == 0) {
+        h->last_T = 0;
+        h->last_stream = h->stream;
+        return LCMOE_OK;
+    }
+    if (!hidden || !out) return fail(LCMOE_ERR_INVALID_ARG, "hidden or out is NULL");
+    const size_t xb = sizeof(float) * (size_t)T * h->desc.d_model;
+    const size_t kb = (size_t)T * h->desc.n_expert_used;
+    HIP_TRY(hipMemcpyAsync(h->x_dev, hidden, xb, hipMemcpyHostToDevice, h->stream));
+    lcmoe_status st = enqueue_norm_residual(h, h->x_dev, T, h->y_dev, h->stream);
+    if (st) return st;
+    HIP_TRY(hipMemcpyAsync(out, h->y_dev, xb, hipMemcpyDeviceToHost, h->stream));
     if (topk_idx)
         HIP_TRY(hipMemcpyAsync(topk_idx, h->topk_idx, kb * 4, hipMemcpyDeviceToHost, h->stream));
     if (topk_w) HIP_TRY(hipMemcpyAsync(topk_w, h->topk_w, kb * 4, hipMemcpyDeviceToHost, h->stream));
@@ -692,6 +779,26 @@ extern "C" lcmoe_status lcmoe_debug_dequant(int32_t type, const uint8_t *data, i
     (void)hipFree(src);
     if (dst) (void)hipFree(dst);
     if (e != hipSuccess) return fail(LCMOE_ERR_HIP, "debug_dequant: %s", hipGetErrorString(e));
+    return LCMOE_OK;
+}
+
+extern "C" lcmoe_status lcmoe_debug_rmsnorm(const float *x, const float *w, float eps, int32_t T,
+                                            int32_t d, float *out) {
+    clear_error();
+    if (!x || !w || !out || T <= 0 || d <= 0 || d % 4)
+        return fail(LCMOE_ERR_INVALID_ARG, "bad arguments (T > 0, d > 0 and d %% 4 == 0)");
+    const size_t n = (size_t)T * d;
+    void *a = nullptr, *b = nullptr, *c = nullptr;
+    hipError_t e = hipMalloc(&a, sizeof(float) * n);
+    if (e == hipSuccess) e = hipMalloc(&b, sizeof(float) * d);
+    if (e == hipSuccess) e = hipMalloc(&c, sizeof(float) * n);
+    if (e == hipSuccess) e = hipMemcpy(a, x, sizeof(float) * n, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(b, w, sizeof(float) * d, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = launch_rmsnorm((const float *)a, (const float *)b, eps, T, d, (float *)c, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(out, c, sizeof(float) * n, hipMemcpyDeviceToHost);
+    for (void *p : {a, b, c})
+        if (p) (void)hipFree(p);
+    if (e != hipSuccess) return fail(LCMOE_ERR_HIP, "debug_rmsnorm: %s", hipGetErrorString(e));
     return LCMOE_OK;
 }
 

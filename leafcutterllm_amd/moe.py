@@ -87,6 +87,32 @@ class MoeFfn:
     def forward_dev(self, x_dev: int, T: int, y_dev: int, stream: int | None = None) -> None:
         check(lib().lcmoe_forward_dev(self._h, x_dev, T, y_dev, stream), "lcmoe_forward_dev")
 
+    def set_norm(self, weight: np.ndarray, eps: float = 1e-5) -> None:
+        """Post-attention RMSNorm weight [d_model] for forward_norm_residual."""
+        weight = np.ascontiguousarray(weight, np.float32)
+        if weight.shape != (self.desc.d_model,):
+            raise LcmoeError(1, "set_norm", f"weight must be [{self.desc.d_model}]")
+        check(lib().lcmoe_set_norm(self._h, _ptr(weight), eps), "lcmoe_set_norm")
+
+    def forward_norm_residual(self, hidden: np.ndarray):
+        """hidden + ffn_forward(rms_norm(hidden)) (engine.rs:110-115);
+        returns (out, topk_idx, topk_w)."""
+        hidden = np.ascontiguousarray(hidden, np.float32)
+        if hidden.ndim != 2 or hidden.shape[1] != self.desc.d_model:
+            raise LcmoeError(1, "forward_norm_residual", f"hidden must be [T, {self.desc.d_model}]")
+        T, K = hidden.shape[0], self.desc.n_expert_used
+        out = np.empty_like(hidden)
+        idx = np.empty((T, K), np.int32)
+        w = np.empty((T, K), np.float32)
+        check(lib().lcmoe_forward_norm_residual(self._h, _ptr(hidden), T, _ptr(out), _ptr(idx),
+                                                _ptr(w)), "lcmoe_forward_norm_residual")
+        return out, idx, w
+
+    def forward_norm_residual_dev(self, hidden_dev: int, T: int, out_dev: int,
+                                  stream: int | None = None) -> None:
+        check(lib().lcmoe_forward_norm_residual_dev(self._h, hidden_dev, T, out_dev, stream),
+              "lcmoe_forward_norm_residual_dev")
+
     def dispatch(self) -> dict:
         E, K = self.desc.n_expert, self.desc.n_expert_used
         T = C.c_int32()
@@ -141,4 +167,14 @@ def debug_sigmoid(x: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, np.float32).ravel()
     out = np.empty_like(x)
     check(lib().lcmoe_debug_sigmoid(_ptr(x), x.size, _ptr(out)), "lcmoe_debug_sigmoid")
+    return out
+
+
+def debug_rmsnorm(x: np.ndarray, w: np.ndarray, eps: float = 1e-5) -> np.ndarray:
+    """The device RMSNorm over the rows of x [T, d]."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    check(lib().lcmoe_debug_rmsnorm(_ptr(x), _ptr(w), eps, x.shape[0], x.shape[1], _ptr(out)),
+          "lcmoe_debug_rmsnorm")
     return out

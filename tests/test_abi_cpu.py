@@ -142,3 +142,19 @@ def test_quantize_errors():
     out = np.zeros(64, np.uint8)
     assert L.lib().lcmoe_quantize(L.TYPE_Q8_0, x.ctypes.data, out.ctypes.data, 33) == 1
     assert L.lib().lcmoe_quantize(3, x.ctypes.data, out.ctypes.data, 32) == 2
+
+
+def test_norm_residual_argument_errors():
+    """Checked before any device work, so they need no GPU."""
+    lib = L.lib()
+    w = np.ones(8, np.float32)
+    x = np.ones((2, 8), np.float32)
+    assert lib.lcmoe_set_norm(None, w.ctypes.data, 1e-5) == 1
+    assert lib.lcmoe_forward_norm_residual(None, x.ctypes.data, 2, x.ctypes.data,
+                                           None, None) == 1
+    assert lib.lcmoe_forward_norm_residual_dev(None, None, 0, None, None) == 1
+    x6 = np.ones((2, 6), np.float32)
+    assert lib.lcmoe_debug_rmsnorm(x6.ctypes.data, w.ctypes.data, 1e-5, 2, 6,
+                                   x6.ctypes.data) == 1
+    assert lib.lcmoe_debug_rmsnorm(x.ctypes.data, w.ctypes.data, 1e-5, 0, 8,
+                                   x.ctypes.data) == 1
