@@ -94,6 +94,56 @@ def copy_probe(mib: int):
     print(json.dumps({"copy_probe_bytes": n, "copies": 3}), flush=True)
 
 
+def shard_matmul_bench(args) -> None:
+    """Times the shard-layout GEMM (Tensor::matmul's Q8_0 / Q4_0 arms) on
+    resident device buffers: HIP events around `steps` launches."""
+    import numpy as np
+
+    import leafcutterllm_amd as L
+    from leafcutterllm_amd import hip
+    from leafcutterllm_amd._lib import check
+
+    name, m, k, n = args.shard_matmul.split(",")
+    m, k, n = int(m), int(k), int(n)
+    qt = {"q8": L.TYPE_Q8_0, "q4": L.TYPE_Q4_0}[name]
+    bb = k * (n // 32) * (34 if qt == L.TYPE_Q8_0 else 18)
+    rng = np.random.default_rng(0)
+    b = rng.integers(0, 256, bb, dtype=np.uint8)
+    b.reshape(-1, 34 if qt == L.TYPE_Q8_0 else 18)[:, :2] = \
+        np.full(1, 0.01, np.float16).view(np.uint8)  # finite scales
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    # weight replicas cycled so that re-reads cannot come from the MALL
+    R = max(2, -(-2 * MALL_BYTES // bb) + 1)
+    dbs = [hip.DeviceBuffer(bb).upload(b) for _ in range(R)]
+    da, dc = hip.DeviceBuffer(a.nbytes).upload(a), hip.DeviceBuffer(4 * m * n)
+    st = hip.Stream()
+
+    def launch(i):
+        check(L.lib().lcmoe_shard_matmul_dev(qt, da.ptr, dbs[i % R].ptr, dc.ptr, m, k, n,
+                                              st.ptr), "lcmoe_shard_matmul_dev")
+
+    for i in range(args.warmup):
+        launch(i)
+    st.synchronize()
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record(st)
+    for i in range(args.steps):
+        launch(i)
+    e1.record(st)
+    ms = e0.elapsed_ms(e1) / args.steps
+    alg = bb + a.nbytes + 4 * m * n
+    print(json.dumps({
+        "metric": "shard-layout quantised GEMM time", "value": round(ms * 1e3, 3), "unit": "us",
+        "higher_is_better": False, "steps": args.steps, "warmup": args.warmup,
+        "config": {"workload": f"lcmoe_shard_matmul_dev {name} m={m} k={k} n={n}",
+                   "replicas": R},
+        "roofline": {"bound": "hbm", "achieved": round(alg / (ms * 1e-3) / 1e9, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "algorithmic_bytes": alg},
+    }))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -110,10 +160,15 @@ def main():
                     help="time each kernel with HIP events in a second timed region")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run device-to-device copies of this size (FETCH_SIZE calibration)")
+    ap.add_argument("--shard-matmul", default="", metavar="TYPE,M,K,N",
+                    help="only time lcmoe_shard_matmul_dev (TYPE q8 or q4) on one shape")
     args = ap.parse_args()
 
     if args.copy_probe:
         copy_probe(args.copy_probe)
+        return
+    if args.shard_matmul:
+        shard_matmul_bench(args)
         return
 
     if args.gpus != 1:

@@ -48,6 +48,7 @@ typedef enum {
 /* GGUF ggml_type codes, QuantType::code, rust/src/model/quant.rs:45-73. */
 enum {
     LCMOE_TYPE_F32 = 0,
+    LCMOE_TYPE_Q4_0 = 2, /* lcmoe_shard_matmul only: the shard engine's Q4_0 */
     LCMOE_TYPE_Q8_0 = 8,
     LCMOE_TYPE_Q4_K = 12,
     LCMOE_TYPE_Q6_K = 14
@@ -241,6 +242,27 @@ int32_t lcmoe_gguf_is_moe_layer(const lcmoe_gguf *g, int32_t layer);
  * expert, ffn_gate_inp_shexp) return LCMOE_ERR_UNSUPPORTED. */
 lcmoe_status lcmoe_gguf_moe_layer(lcmoe_gguf *g, int32_t layer, int32_t max_tokens,
                                   lcmoe_desc *desc, lcmoe_weights *w);
+
+/* ---- shard-layout quantised GEMM -------------------------------------- */
+
+/* C[m,n] = A[m,k] B[k,n] for the shard engine's quantised matrices: the
+ * Q8_0 / Q4_0 arms of Tensor::matmul (rust/src/model/tensor.rs:118-128),
+ * which call q8_0_matmul / q4_0_matmul (rust/src/kernels/int8_gemm.rs
+ * :172-194, :336-358).  B is k rows of n/32 blocks along n, row-major: type
+ * LCMOE_TYPE_Q8_0 = 34-byte blocks (f16 scale, 32 int8; q8_0.rs:24-32),
+ * LCMOE_TYPE_Q4_0 = the shard engine's 18-byte blocks (f16 scale, 16 bytes,
+ * element 2t the low nibble of byte t and 2t+1 the high one, minus 8;
+ * q4_0.rs:27-46 -- not GGUF's Q4_0 order).  A and C are row-major f32.
+ * Results are bit-identical to the reference's x86 path
+ * (q8_0_matmul_avx2_inner :47-98 and its Q4_0 twin :240-290): per output,
+ * c = fma(a[i,l], q * scale, c) for l = 0 .. k-1 from 0.  n % 32 == 0,
+ * 0 <= m <= 524280, k >= 0.  Host buffers, synchronous (B is copied to
+ * the device on every call). */
+lcmoe_status lcmoe_shard_matmul(int32_t type, const float *a, const uint8_t *b, float *c,
+                                int32_t m, int32_t k, int32_t n);
+/* Device buffers, enqueued on `stream` (NULL: the null stream); B resident. */
+lcmoe_status lcmoe_shard_matmul_dev(int32_t type, const float *a_dev, const uint8_t *b_dev,
+                                    float *c_dev, int32_t m, int32_t k, int32_t n, void *stream);
 
 /* ---- device self-tests (need a GPU; used by the parity tests) ---------- */
 

@@ -4,13 +4,13 @@ The compute lives in liblcmoe.so (HIP kernels + C ABI, include/lcmoe.h); this
 package binds it with ctypes and carries the benchmark layer shapes.
 """
 from ._lib import (ROUTE_SIGMOID_GROUP, ROUTE_SOFTMAX, ROUTE_SOFTMAX_RENORM, TYPE_F32,
-                   TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0, Desc, LcmoeError, Weights, lib)
+                   TYPE_Q4_0, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0, Desc, LcmoeError, Weights, lib)
 from .configs import CONFIGS, LayerConfig, synth_layer, synth_x
 from .gguf import GgufFile
-from .moe import MoeFfn, debug_dequant, debug_rmsnorm, debug_sigmoid
+from .moe import MoeFfn, debug_dequant, debug_rmsnorm, debug_sigmoid, shard_matmul
 
 __all__ = [
     "CONFIGS", "LayerConfig", "synth_layer", "synth_x", "MoeFfn", "GgufFile", "Desc", "Weights",
-    "LcmoeError", "lib", "debug_dequant", "debug_rmsnorm", "debug_sigmoid", "TYPE_F32", "TYPE_Q8_0",
+    "LcmoeError", "lib", "debug_dequant", "debug_rmsnorm", "debug_sigmoid", "shard_matmul", "TYPE_F32", "TYPE_Q4_0", "TYPE_Q8_0",
     "TYPE_Q4_K", "TYPE_Q6_K", "ROUTE_SOFTMAX_RENORM", "ROUTE_SOFTMAX", "ROUTE_SIGMOID_GROUP",
 ]

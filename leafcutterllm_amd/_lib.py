@@ -13,6 +13,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "liblcmoe.so")
 
 TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 0, 8, 12, 14
+TYPE_Q4_0 = 2  # lcmoe_shard_matmul only: the shard engine's interleaved Q4_0
 ROUTE_SOFTMAX_RENORM, ROUTE_SOFTMAX, ROUTE_SIGMOID_GROUP = 0, 1, 2
 
 STATUS = {
@@ -30,7 +31,8 @@ EXPORTS = (
     "lcmoe_gguf_open", "lcmoe_gguf_close", "lcmoe_gguf_meta_int", "lcmoe_gguf_meta_str",
     "lcmoe_gguf_tensor", "lcmoe_gguf_block_count", "lcmoe_gguf_is_moe_layer",
     "lcmoe_gguf_moe_layer", "lcmoe_set_norm", "lcmoe_forward_norm_residual",
-    "lcmoe_forward_norm_residual_dev", "lcmoe_debug_rmsnorm",
+    "lcmoe_forward_norm_residual_dev", "lcmoe_debug_rmsnorm", "lcmoe_shard_matmul",
+    "lcmoe_shard_matmul_dev",
 )
 
 
@@ -99,6 +101,8 @@ def lib() -> C.CDLL:
         "lcmoe_debug_sigmoid": (i32, [vp, i64, vp]),
         "lcmoe_debug_rmsnorm": (i32, [vp, vp, f32, i32, i32, vp]),
         "lcmoe_set_norm": (i32, [vp, vp, f32]),
+        "lcmoe_shard_matmul": (i32, [i32, vp, vp, vp, i32, i32, i32]),
+        "lcmoe_shard_matmul_dev": (i32, [i32, vp, vp, vp, i32, i32, i32, vp]),
         "lcmoe_forward_norm_residual": (i32, [vp, vp, i32, vp, vp, vp]),
         "lcmoe_forward_norm_residual_dev": (i32, [vp, vp, i32, vp, vp]),
         "lcmoe_gguf_open": (i32, [C.c_char_p, P(vp)]),

@@ -1,0 +1,133 @@
+// The shard engine's quantised GEMM (rust/src/kernels/int8_gemm.rs),
+// C[m,n] = A[m,k] B[k,n] with B stored as blocks of 32 along n, row-major
+// over k: Q8_0 blocks of 34 bytes (f16 scale, 32 int8) or the shard Q4_0
+// blocks of 18 bytes (f16 scale, 16 bytes; element 2t is the low nibble of
+// byte t, 2t+1 the high one, value nibble - 8: q4_0.rs:36-46).
+//
+// Results are bit-identical to the x86 path the reference always takes for
+// these shapes (q8_0_matmul_avx2_inner int8_gemm.rs:47-98, the Q4_0 twin
+// :240-290): each output starts at 0 and takes, for l = 0 .. k-1 in order,
+// c = fma(a[i,l], q * scale, c), the dequantised weight rounded once.  That
+// order is sequential in k, so the parallelism is over outputs: one lane per
+// column, kShardRows rows of A per block held as independent chains, the
+// weights and A staged through LDS a window of kShardWin k-rows ahead.
+
+#include "device_common.h"
+#include "kernels.h"
+
+namespace lcmoe {
+namespace {
+
+constexpr int kShardCols = 64;   // columns per block: one wave, one lane per column
+constexpr int kShardRows = 8;    // rows of A per block, at most
+constexpr int kShardWin = 128;   // k-rows per window
+
+// One wave per block.  Per window the wave fetches kShardWin k-rows of its
+// two (or, at a ragged end, one) blocks per row with 2-byte loads spread over
+// the lanes, and the A window, into registers; they are written to LDS after
+// the previous window has been consumed from the other buffer, so a window's
+// loads are in flight while the one before it is computed.
+// R rows of A per block (1, 2, 4 or 8): every chain runs unguarded (A rows
+// past m are zeros in LDS) and only rows < m are stored.
+template <int QT, int R>
+__global__ __launch_bounds__(kShardCols) void k_shard_matmul(const float *__restrict__ a,
+                                                             const uint8_t *__restrict__ b,
+                                                             float *__restrict__ c, int m, int k,
+                                                             int n) {
+    constexpr int BB = QT == LCMOE_TYPE_Q8_0 ? 34 : 18;  // bytes per block
+    constexpr int UG = BB;                               // u16 per k-row of two blocks
+    constexpr int NB = kShardWin * UG / kShardCols;      // u16 loads per lane per window
+    constexpr int NA = R * kShardWin / kShardCols;       // A loads per lane per window
+    __shared__ uint16_t s_b[2][kShardWin * UG];
+    __shared__ float s_a[2][R * kShardWin];
+    const int lane = threadIdx.x, j = blockIdx.x * kShardCols + lane;
+    const int i0 = blockIdx.y * R, mt = min(R, m - i0);
+    const int nblk = min(2, (n >> 5) - 2 * (int)blockIdx.x);  // blocks of this group per row
+    const int ug = nblk * BB / 2;                               // valid u16 per row
+    const int64_t rs = (int64_t)(n >> 5) * BB;                  // bytes per k-row
+    const uint16_t *pg = reinterpret_cast<const uint16_t *>(b + (int64_t)blockIdx.x * 2 * BB);
+    const int g = lane >> 5, t = lane & 31;
+    const bool col = j < n;
+    uint16_t rb[NB];
+    float ra[NA];
+    auto fetch = [&](int l0) {
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const int e = lane + kShardCols * i, w = e / UG, u = e % UG;
+            if (l0 + w < k && u < ug) rb[i] = pg[((int64_t)(l0 + w) * rs >> 1) + u];
+        }
+#pragma unroll
+        for (int i = 0; i < NA; i++) {
+            const int e = lane + kShardCols * i, r = e / kShardWin, w = e % kShardWin;
+            ra[i] = r < mt && l0 + w < k ? a[(int64_t)(i0 + r) * k + l0 + w] : 0.0f;
+        }
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < NB; i++) s_b[buf][lane + kShardCols * i] = rb[i];
+#pragma unroll
+        for (int i = 0; i < NA; i++) s_a[buf][lane + kShardCols * i] = ra[i];
+    };
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    int buf = 0;
+    for (int l0 = 0; l0 < k; l0 += kShardWin, buf ^= 1) {
+        const bool more = l0 + kShardWin < k;
+        if (more) fetch(l0 + kShardWin);
+        if (col) {
+            const uint8_t *sb = reinterpret_cast<const uint8_t *>(s_b[buf]) + g * BB;
+            const int wn = min(kShardWin, k - l0);
+#pragma unroll 8
+            for (int w = 0; w < wn; w++) {
+                const uint8_t *blk = sb + w * 2 * UG;
+                const float sc = dh2f(*reinterpret_cast<const uint16_t *>(blk));
+                float q;
+                if constexpr (QT == LCMOE_TYPE_Q8_0) {
+                    q = (float)(int8_t)blk[2 + t];
+                } else {
+                    const uint32_t by = blk[2 + (t >> 1)];
+                    q = (float)((t & 1) ? (by >> 4) : (by & 15u)) - 8.0f;
+                }
+                const float dq = q * sc;
+#pragma unroll
+                for (int r = 0; r < R; r++)
+                    acc[r] = __builtin_fmaf(s_a[buf][r * kShardWin + w], dq, acc[r]);
+            }
+        }
+        if (more) stage(buf ^ 1);  // the other buffer was last read before the barrier
+        __syncthreads();
+    }
+    if (!col) return;
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        if (r < mt) c[(int64_t)(i0 + r) * n + j] = acc[r];
+}
+
+}  // namespace
+
+template <int R>
+static void launch_rows(int qt, const float *a, const uint8_t *b, float *c, int m, int k, int n,
+                        hipStream_t st) {
+    const dim3 grid((n + kShardCols - 1) / kShardCols, (m + R - 1) / R);
+    if (qt == LCMOE_TYPE_Q8_0)
+        hipLaunchKernelGGL((k_shard_matmul<LCMOE_TYPE_Q8_0, R>), grid, dim3(kShardCols), 0, st, a,
+                           b, c, m, k, n);
+    else
+        hipLaunchKernelGGL((k_shard_matmul<LCMOE_TYPE_Q4_0, R>), grid, dim3(kShardCols), 0, st, a,
+                           b, c, m, k, n);
+}
+
+hipError_t launch_shard_matmul(int qt, const float *a, const uint8_t *b, float *c, int m, int k,
+                               int n, hipStream_t st) {
+    if (m == 1) launch_rows<1>(qt, a, b, c, m, k, n, st);
+    else if (m == 2) launch_rows<2>(qt, a, b, c, m, k, n, st);
+    else if (m <= 4) launch_rows<4>(qt, a, b, c, m, k, n, st);
+    else launch_rows<kShardRows>(qt, a, b, c, m, k, n, st);
+    return hipGetLastError();
+}
+
+}  // namespace lcmoe

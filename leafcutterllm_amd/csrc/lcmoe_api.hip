@@ -782,6 +782,54 @@ extern "C" lcmoe_status lcmoe_debug_dequant(int32_t type, const uint8_t *data, i
     return LCMOE_OK;
 }
 
+static lcmoe_status shard_args(int32_t type, int32_t m, int32_t k, int32_t n, size_t *b_bytes) {
+    if (type != LCMOE_TYPE_Q8_0 && type != LCMOE_TYPE_Q4_0)
+        return fail(LCMOE_ERR_UNSUPPORTED, "shard matmul type %d (Q8_0 = 8 or Q4_0 = 2)", type);
+    if (m < 0 || k < 0 || n < 0 || n % 32 || m > 65535 * 8)
+        return fail(LCMOE_ERR_INVALID_ARG, "shard matmul shape m=%d k=%d n=%d (n %% 32 == 0)", m,
+                    k, n);
+    *b_bytes = (size_t)k * (n / 32) * (type == LCMOE_TYPE_Q8_0 ? 34 : 18);
+    return LCMOE_OK;
+}
+
+extern "C" lcmoe_status lcmoe_shard_matmul_dev(int32_t type, const float *a_dev,
+                                               const uint8_t *b_dev, float *c_dev, int32_t m,
+                                               int32_t k, int32_t n, void *stream) {
+    clear_error();
+    size_t bb;
+    if (lcmoe_status s = shard_args(type, m, k, n, &bb)) return s;
+    if ((size_t)m * n == 0) return LCMOE_OK;
+    if (!c_dev || (k > 0 && (!a_dev || !b_dev)))
+        return fail(LCMOE_ERR_INVALID_ARG, "a, b or c is NULL");
+    if ((uintptr_t)b_dev & 1) return fail(LCMOE_ERR_INVALID_ARG, "b must be 2-byte aligned");
+    HIP_TRY(launch_shard_matmul(type, a_dev, b_dev, c_dev, m, k, n, (hipStream_t)stream));
+    return LCMOE_OK;
+}
+
+extern "C" lcmoe_status lcmoe_shard_matmul(int32_t type, const float *a, const uint8_t *b,
+                                           float *c, int32_t m, int32_t k, int32_t n) {
+    clear_error();
+    size_t bb;
+    if (lcmoe_status s = shard_args(type, m, k, n, &bb)) return s;
+    if ((size_t)m * n == 0) return LCMOE_OK;
+    if (!c || (k > 0 && (!a || !b))) return fail(LCMOE_ERR_INVALID_ARG, "a, b or c is NULL");
+    const size_t ab = sizeof(float) * (size_t)m * k, cb = sizeof(float) * (size_t)m * n;
+    void *da = nullptr, *db = nullptr, *dc = nullptr;
+    hipError_t e = hipMalloc(&da, ab ? ab : 4);
+    if (e == hipSuccess) e = hipMalloc(&db, bb ? bb : 4);
+    if (e == hipSuccess) e = hipMalloc(&dc, cb);
+    if (e == hipSuccess && ab) e = hipMemcpy(da, a, ab, hipMemcpyHostToDevice);
+    if (e == hipSuccess && bb) e = hipMemcpy(db, b, bb, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = launch_shard_matmul(type, (const float *)da, (const uint8_t *)db, (float *)dc, m, k,
+                                n, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(c, dc, cb, hipMemcpyDeviceToHost);
+    for (void *p : {da, db, dc})
+        if (p) (void)hipFree(p);
+    if (e != hipSuccess) return fail(LCMOE_ERR_HIP, "shard_matmul: %s", hipGetErrorString(e));
+    return LCMOE_OK;
+}
+
 extern "C" lcmoe_status lcmoe_debug_rmsnorm(const float *x, const float *w, float eps, int32_t T,
                                             int32_t d, float *out) {
     clear_error();

@@ -178,3 +178,17 @@ def debug_rmsnorm(x: np.ndarray, w: np.ndarray, eps: float = 1e-5) -> np.ndarray
     check(lib().lcmoe_debug_rmsnorm(_ptr(x), _ptr(w), eps, x.shape[0], x.shape[1], _ptr(out)),
           "lcmoe_debug_rmsnorm")
     return out
+
+
+def shard_matmul(qtype: int, a: np.ndarray, b: np.ndarray, k: int, n: int) -> np.ndarray:
+    """C = A B for the shard engine's Q8_0 / Q4_0 matrices (Tensor::matmul's
+    quantised arms, tensor.rs:118-128) on the GPU: a [m, k] f32, b the block
+    bytes (k rows of n/32 blocks along n)."""
+    a = np.ascontiguousarray(a, np.float32)
+    if a.ndim != 2:
+        a = a.reshape(-1, k)
+    b = np.ascontiguousarray(b, np.uint8)
+    out = np.empty((a.shape[0], n), np.float32)
+    check(lib().lcmoe_shard_matmul(qtype, _ptr(a), _ptr(b), _ptr(out), a.shape[0], k, n),
+          "lcmoe_shard_matmul")
+    return out

@@ -891,3 +891,48 @@ void lco_resident_destroy(void *h) {
     free(r->wg);
     free(r);
 }
+
+/* The shard engine's quantised GEMM, C[m,n] = A[m,k] B[k,n], B in blocks of
+ * 32 along n, row-major over k (rust/src/kernels/int8_gemm.rs).  n is a
+ * whole number of blocks, so x86 always takes the AVX2 path
+ * (q8_0_matmul :172-194 -> q8_0_matmul_avx2_inner :47-98; the Q4_0 twin
+ * q4_0_matmul_avx2_inner follows :240-290): C starts at 0; for each k-row l
+ * every block is dequantised to f32 (q * scale, one rounding) and
+ * c = fma(a[i,l], deq, c).  Blocks come from bytes as q8_0.rs:24-32 /
+ * q4_0.rs Block::from_bytes read them: Q8_0 = f16 scale + 32 int8 (34 B);
+ * Q4_0 = f16 scale + 16 bytes, element 2t the low nibble of byte t, 2t+1
+ * the high one, value nibble - 8 (q4_0.rs:36-46; not GGUF's order).
+ * type: LCO_Q8_0 or LCO_Q4_0_SHARD.  Returns -1 on a bad type or shape. */
+int lco_shard_matmul(int type, const float *a, const uint8_t *b, float *c, int m, int k,
+                     int n) {
+    if ((type != LCO_Q8_0 && type != LCO_Q4_0_SHARD) || m < 0 || k < 0 || n < 0 || n % 32)
+        return -1;
+    const int bpr = n / 32;
+    const size_t bb = type == LCO_Q8_0 ? 34 : 18;
+    float *deq = (float *)malloc(sizeof(float) * (size_t)(n ? n : 1));
+    if (!deq) return -1;
+    for (int i = 0; i < m; i++) {
+        float *cr = c + (size_t)i * n;
+        for (int j = 0; j < n; j++) cr[j] = 0.0f;
+        for (int l = 0; l < k; l++) {
+            for (int blk = 0; blk < bpr; blk++) {
+                const uint8_t *p = b + ((size_t)l * bpr + blk) * bb;
+                const float sc = lco_f16_to_f32((uint16_t)(p[0] | (p[1] << 8)));
+                for (int t = 0; t < 32; t++) {
+                    float q;
+                    if (type == LCO_Q8_0) {
+                        q = (float)(int8_t)p[2 + t];
+                    } else {
+                        const uint8_t byte = p[2 + t / 2];
+                        q = (float)((t & 1) ? (byte >> 4) : (byte & 15)) - 8.0f;
+                    }
+                    deq[blk * 32 + t] = q * sc;
+                }
+            }
+            const float av = a[(size_t)i * k + l];
+            for (int j = 0; j < n; j++) cr[j] = fmaf(av, deq[j], cr[j]);
+        }
+    }
+    free(deq);
+    return 0;
+}

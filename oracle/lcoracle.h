@@ -24,6 +24,9 @@
  *                          float64, FMA-lane vs mul+add-tail bit behaviour
  *   silu / softmax       : closed form in float64, tensor.rs:211-217 KAT
  *   lc_expf / sigmoid    : <= 2 ulp vs float64 exp over a dense sweep
+ *   shard_matmul         : reference test matrices int8_gemm.rs:378-511 against
+ *                          dequantise-then-matmul (1e-3), float64 bound, exact
+ *                          small-integer KATs that fix operand order and nibbles
  *   rms_norm             : reference test tensor.rs:204-209, float64 closed form,
  *                          exact constant rows, scale-then-weight rounding order
  *   top-k, group top-k   : brute force (full sort) incl. adversarial ties / NaN
@@ -44,6 +47,8 @@ extern "C" {
 
 /* GGUF ggml_type codes (rust/src/model/quant.rs:45-73). */
 enum { LCO_F32 = 0, LCO_F16 = 1, LCO_Q8_0 = 8, LCO_Q4_K = 12, LCO_Q6_K = 14 };
+/* The shard engine's Q4_0 (interleaved nibbles; GGML's Q4_0 code 2). */
+enum { LCO_Q4_0_SHARD = 2 };
 
 /* Router kinds. */
 enum {
@@ -108,6 +113,7 @@ void lco_matmul(const float *a, const float *b, float *c, int m, int k, int n, i
 void lco_transpose(const float *a, float *b, int rows, int cols);
 float lco_silu(float v);
 void lco_rms_norm(const float *x, const float *w, float eps, int T, int d, float *out);
+int lco_shard_matmul(int type, const float *a, const uint8_t *b, float *c, int m, int k, int n);
 void lco_softmax(const float *x, float *y, int n);
 float lco_expf_cw(float x);
 float lco_sigmoid_cw(float x);

@@ -74,6 +74,7 @@ def lib() -> C.CDLL:
             "lco_transpose": (None, [vp, vp, i32, i32]),
             "lco_silu": (f32, [f32]),
             "lco_rms_norm": (None, [vp, vp, f32, i32, i32, vp]),
+            "lco_shard_matmul": (i32, [i32, vp, vp, vp, i32, i32, i32]),
             "lco_softmax": (None, [vp, vp, i32]),
             "lco_expf_cw": (f32, [f32]),
             "lco_sigmoid_cw": (f32, [f32]),
@@ -311,3 +312,20 @@ class Resident:
             self.close()
         except Exception:
             pass
+
+
+Q4_0_SHARD = 2
+
+
+def shard_matmul(qtype: int, a: np.ndarray, b: np.ndarray, k: int, n: int) -> np.ndarray:
+    """int8_gemm.rs q8_0_matmul / q4_0_matmul on x86 (lco_shard_matmul):
+    a [m, k] f32, b the shard blocks as bytes."""
+    a = np.ascontiguousarray(a, np.float32)
+    if a.ndim != 2:
+        a = a.reshape(-1, k)
+    b = np.ascontiguousarray(b, np.uint8)
+    m = a.shape[0]
+    out = np.zeros((m, n), np.float32)
+    if lib().lco_shard_matmul(qtype, _p(a), _p(b), _p(out), m, k, n) != 0:
+        raise ValueError("lco_shard_matmul: bad type or shape")
+    return out

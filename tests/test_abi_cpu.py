@@ -158,3 +158,16 @@ def test_norm_residual_argument_errors():
                                    x6.ctypes.data) == 1
     assert lib.lcmoe_debug_rmsnorm(x.ctypes.data, w.ctypes.data, 1e-5, 0, 8,
                                    x.ctypes.data) == 1
+
+
+def test_shard_matmul_argument_errors():
+    lib = L.lib()
+    a = np.ones((2, 4), np.float32)
+    b = np.zeros(4 * 34, np.uint8)
+    c = np.zeros((2, 32), np.float32)
+    args = (a.ctypes.data, b.ctypes.data, c.ctypes.data)
+    assert lib.lcmoe_shard_matmul(12, *args, 2, 4, 32) == 2      # Q4_K: not a shard type
+    assert lib.lcmoe_shard_matmul(8, *args, 2, 4, 40) == 1       # n % 32
+    assert lib.lcmoe_shard_matmul(8, *args, -1, 4, 32) == 1
+    assert lib.lcmoe_shard_matmul(8, None, None, None, 2, 4, 32) == 1
+    assert lib.lcmoe_shard_matmul_dev(8, None, None, None, 0, 4, 32, None) == 0  # empty
