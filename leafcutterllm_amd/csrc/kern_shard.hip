@@ -20,7 +20,6 @@ namespace {
 
 constexpr int kShardCols = 64;   // columns per block: one wave, one lane per column
 constexpr int kShardRows = 8;    // rows of A per block, at most
-constexpr int kShardWin = 128;   // k-rows per window
 
 // One wave per block.  Per window the wave fetches kShardWin k-rows of its
 // two (or, at a ragged end, one) blocks per row with 2-byte loads spread over
@@ -29,7 +28,7 @@ constexpr int kShardWin = 128;   // k-rows per window
 // loads are in flight while the one before it is computed.
 // R rows of A per block (1, 2, 4 or 8): every chain runs unguarded (A rows
 // past m are zeros in LDS) and only rows < m are stored.
-template <int QT, int R>
+template <int QT, int R, int kShardWin, bool BATCH>
 __global__ __launch_bounds__(kShardCols) void k_shard_matmul(const float *__restrict__ a,
                                                              const uint8_t *__restrict__ b,
                                                              float *__restrict__ c, int m, int k,
@@ -81,21 +80,45 @@ __global__ __launch_bounds__(kShardCols) void k_shard_matmul(const float *__rest
         if (col) {
             const uint8_t *sb = reinterpret_cast<const uint8_t *>(s_b[buf]) + g * BB;
             const int wn = min(kShardWin, k - l0);
-#pragma unroll 8
-            for (int w = 0; w < wn; w++) {
+            // one row's scale and code from LDS
+            auto read = [&](int w, uint32_t &sv, int32_t &qv) {
                 const uint8_t *blk = sb + w * 2 * UG;
-                const float sc = dh2f(*reinterpret_cast<const uint16_t *>(blk));
+                sv = *reinterpret_cast<const uint16_t *>(blk);
+                if constexpr (QT == LCMOE_TYPE_Q8_0) qv = (int8_t)blk[2 + t];
+                else qv = blk[2 + (t >> 1)];
+            };
+            auto step = [&](int w, uint32_t sv, int32_t qv) {
                 float q;
-                if constexpr (QT == LCMOE_TYPE_Q8_0) {
-                    q = (float)(int8_t)blk[2 + t];
-                } else {
-                    const uint32_t by = blk[2 + (t >> 1)];
-                    q = (float)((t & 1) ? (by >> 4) : (by & 15u)) - 8.0f;
-                }
-                const float dq = q * sc;
+                if constexpr (QT == LCMOE_TYPE_Q8_0) q = (float)qv;
+                else q = (float)((t & 1) ? (qv >> 4) : (qv & 15)) - 8.0f;
+                const float dq = q * dh2f(sv);
 #pragma unroll
                 for (int r = 0; r < R; r++)
                     acc[r] = __builtin_fmaf(s_a[buf][r * kShardWin + w], dq, acc[r]);
+            };
+            int w = 0;
+            if constexpr (!BATCH) {  // measured faster for one row of Q4_0
+#pragma unroll 8
+                for (; w < wn; w++) {
+                    uint32_t sv;
+                    int32_t qv;
+                    read(w, sv, qv);
+                    step(w, sv, qv);
+                }
+            }
+            for (; w + 8 <= wn; w += 8) {  // eight rows' reads, then their steps in order
+                uint32_t sv[8];
+                int32_t qv[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) read(w + u, sv[u], qv[u]);
+#pragma unroll
+                for (int u = 0; u < 8; u++) step(w + u, sv[u], qv[u]);
+            }
+            for (; w < wn; w++) {
+                uint32_t sv;
+                int32_t qv;
+                read(w, sv, qv);
+                step(w, sv, qv);
             }
         }
         if (more) stage(buf ^ 1);  // the other buffer was last read before the barrier
@@ -109,24 +132,26 @@ __global__ __launch_bounds__(kShardCols) void k_shard_matmul(const float *__rest
 
 }  // namespace
 
-template <int R>
+template <int R, int W>
 static void launch_rows(int qt, const float *a, const uint8_t *b, float *c, int m, int k, int n,
                         hipStream_t st) {
     const dim3 grid((n + kShardCols - 1) / kShardCols, (m + R - 1) / R);
     if (qt == LCMOE_TYPE_Q8_0)
-        hipLaunchKernelGGL((k_shard_matmul<LCMOE_TYPE_Q8_0, R>), grid, dim3(kShardCols), 0, st, a,
+        hipLaunchKernelGGL((k_shard_matmul<LCMOE_TYPE_Q8_0, R, W, true>), grid, dim3(kShardCols), 0, st, a,
                            b, c, m, k, n);
     else
-        hipLaunchKernelGGL((k_shard_matmul<LCMOE_TYPE_Q4_0, R>), grid, dim3(kShardCols), 0, st, a,
+        hipLaunchKernelGGL((k_shard_matmul<LCMOE_TYPE_Q4_0, R, W, (R > 1)>), grid, dim3(kShardCols), 0, st, a,
                            b, c, m, k, n);
 }
 
 hipError_t launch_shard_matmul(int qt, const float *a, const uint8_t *b, float *c, int m, int k,
                                int n, hipStream_t st) {
-    if (m == 1) launch_rows<1>(qt, a, b, c, m, k, n, st);
-    else if (m == 2) launch_rows<2>(qt, a, b, c, m, k, n, st);
-    else if (m <= 4) launch_rows<4>(qt, a, b, c, m, k, n, st);
-    else launch_rows<kShardRows>(qt, a, b, c, m, k, n, st);
+    // a window of kShardWin k-rows: longer for one row of A, whose chains
+    // are too short per row to cover a window's loads otherwise
+    if (m == 1) launch_rows<1, 128>(qt, a, b, c, m, k, n, st);
+    else if (m == 2) launch_rows<2, 64>(qt, a, b, c, m, k, n, st);
+    else if (m <= 4) launch_rows<4, 64>(qt, a, b, c, m, k, n, st);
+    else launch_rows<kShardRows, 64>(qt, a, b, c, m, k, n, st);
     return hipGetLastError();
 }
 
