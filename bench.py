@@ -116,11 +116,18 @@ def shard_matmul_bench(args) -> None:
     R = max(2, -(-2 * MALL_BYTES // bb) + 1)
     dbs = [hip.DeviceBuffer(bb).upload(b) for _ in range(R)]
     da, dc = hip.DeviceBuffer(a.nbytes).upload(a), hip.DeviceBuffer(4 * m * n)
+    S = args.shard_split
+    ws = hip.DeviceBuffer(4 * S * m * n) if S > 1 else None
     st = hip.Stream()
 
     def launch(i):
-        check(L.lib().lcmoe_shard_matmul_dev(qt, da.ptr, dbs[i % R].ptr, dc.ptr, m, k, n,
-                                              st.ptr), "lcmoe_shard_matmul_dev")
+        if S > 1:
+            check(L.lib().lcmoe_shard_matmul_split_dev(qt, da.ptr, dbs[i % R].ptr, dc.ptr, m, k,
+                                                        n, S, ws.ptr, st.ptr),
+                  "lcmoe_shard_matmul_split_dev")
+        else:
+            check(L.lib().lcmoe_shard_matmul_dev(qt, da.ptr, dbs[i % R].ptr, dc.ptr, m, k, n,
+                                                  st.ptr), "lcmoe_shard_matmul_dev")
 
     for i in range(args.warmup):
         launch(i)
@@ -135,7 +142,8 @@ def shard_matmul_bench(args) -> None:
     print(json.dumps({
         "metric": "shard-layout quantised GEMM time", "value": round(ms * 1e3, 3), "unit": "us",
         "higher_is_better": False, "steps": args.steps, "warmup": args.warmup,
-        "config": {"workload": f"lcmoe_shard_matmul_dev {name} m={m} k={k} n={n}",
+        "config": {"workload": f"lcmoe_shard_matmul{'_split' if S > 1 else ''}_dev {name} "
+                               f"m={m} k={k} n={n}" + (f" k_split={S}" if S > 1 else ""),
                    "replicas": R},
         "roofline": {"bound": "hbm", "achieved": round(alg / (ms * 1e-3) / 1e9, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -162,6 +170,8 @@ def main():
                     help="only run device-to-device copies of this size (FETCH_SIZE calibration)")
     ap.add_argument("--shard-matmul", default="", metavar="TYPE,M,K,N",
                     help="only time lcmoe_shard_matmul_dev (TYPE q8 or q4) on one shape")
+    ap.add_argument("--shard-split", type=int, default=1, metavar="S",
+                    help="with --shard-matmul: time lcmoe_shard_matmul_split_dev with S k-slices")
     args = ap.parse_args()
 
     if args.copy_probe:

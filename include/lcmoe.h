@@ -264,6 +264,19 @@ lcmoe_status lcmoe_shard_matmul(int32_t type, const float *a, const uint8_t *b, 
 lcmoe_status lcmoe_shard_matmul_dev(int32_t type, const float *a_dev, const uint8_t *b_dev,
                                     float *c_dev, int32_t m, int32_t k, int32_t n, void *stream);
 
+/* lcmoe_shard_matmul_dev with k split into k_split slices (1..64, at most
+ * k) run in parallel: each slice an in-order fma chain over its ceil(k /
+ * k_split) rows into `workspace` (k_split * m * n floats, device, 4-byte
+ * aligned), then the slices added in slice order.  Deterministic and within
+ * float rounding of the exact product, but not bit-identical to the
+ * reference (k_split = 1 is, and then needs no workspace).  No counterpart
+ * in the reference: it is this library's faster variant of
+ * q8_0_matmul / q4_0_matmul (int8_gemm.rs:172-194, :336-358) for callers
+ * that accept reassociation. */
+lcmoe_status lcmoe_shard_matmul_split_dev(int32_t type, const float *a_dev, const uint8_t *b_dev,
+                                          float *c_dev, int32_t m, int32_t k, int32_t n,
+                                          int32_t k_split, float *workspace, void *stream);
+
 /* ---- device self-tests (need a GPU; used by the parity tests) ---------- */
 
 /* Decode `count` elements of a GGUF tensor with the device decoders and

@@ -31,8 +31,14 @@ constexpr int kShardRows = 8;    // rows of A per block, at most
 template <int QT, int R, int kShardWin, bool BATCH>
 __global__ __launch_bounds__(kShardCols) void k_shard_matmul(const float *__restrict__ a,
                                                              const uint8_t *__restrict__ b,
-                                                             float *__restrict__ c, int m, int k,
-                                                             int n) {
+                                                             float *__restrict__ c, int m, int kt,
+                                                             int n, int ks) {
+    // blockIdx.z: k slice [z ks, z ks + ks) into its own C plane (one slice:
+    // the whole k straight into C)
+    const int lda = kt, kz = blockIdx.z * ks, k = min(ks, kt - kz);
+    a += kz;
+    b += (int64_t)kz * (n >> 5) * (QT == LCMOE_TYPE_Q8_0 ? 34 : 18);
+    c += (int64_t)blockIdx.z * m * n;
     constexpr int BB = QT == LCMOE_TYPE_Q8_0 ? 34 : 18;  // bytes per block
     constexpr int UG = BB;                               // u16 per k-row of two blocks
     constexpr int NB = kShardWin * UG / kShardCols;      // u16 loads per lane per window
@@ -58,7 +64,7 @@ __global__ __launch_bounds__(kShardCols) void k_shard_matmul(const float *__rest
 #pragma unroll
         for (int i = 0; i < NA; i++) {
             const int e = lane + kShardCols * i, r = e / kShardWin, w = e % kShardWin;
-            ra[i] = r < mt && l0 + w < k ? a[(int64_t)(i0 + r) * k + l0 + w] : 0.0f;
+            ra[i] = r < mt && l0 + w < k ? a[(int64_t)(i0 + r) * lda + l0 + w] : 0.0f;
         }
     };
     auto stage = [&](int buf) {
@@ -134,24 +140,41 @@ __global__ __launch_bounds__(kShardCols) void k_shard_matmul(const float *__rest
 
 template <int R, int W>
 static void launch_rows(int qt, const float *a, const uint8_t *b, float *c, int m, int k, int n,
-                        hipStream_t st) {
-    const dim3 grid((n + kShardCols - 1) / kShardCols, (m + R - 1) / R);
+                        int S, hipStream_t st) {
+    const int ks = (k + S - 1) / S;
+    const dim3 grid((n + kShardCols - 1) / kShardCols, (m + R - 1) / R, S);
     if (qt == LCMOE_TYPE_Q8_0)
         hipLaunchKernelGGL((k_shard_matmul<LCMOE_TYPE_Q8_0, R, W, true>), grid, dim3(kShardCols), 0, st, a,
-                           b, c, m, k, n);
+                           b, c, m, k, n, ks);
     else
         hipLaunchKernelGGL((k_shard_matmul<LCMOE_TYPE_Q4_0, R, W, (R > 1)>), grid, dim3(kShardCols), 0, st, a,
-                           b, c, m, k, n);
+                           b, c, m, k, n, ks);
+}
+
+// C = the slices' planes added in slice order, from the first
+__global__ __launch_bounds__(256) void k_shard_reduce(const float *__restrict__ ws, int S,
+                                                      int64_t plane, float *__restrict__ c) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= plane) return;
+    float s = ws[i];
+    for (int z = 1; z < S; z++) s = s + ws[z * plane + i];
+    c[i] = s;
 }
 
 hipError_t launch_shard_matmul(int qt, const float *a, const uint8_t *b, float *c, int m, int k,
-                               int n, hipStream_t st) {
+                               int n, hipStream_t st, int S, float *ws) {
+    float *dst = S > 1 ? ws : c;
     // a window of kShardWin k-rows: longer for one row of A, whose chains
     // are too short per row to cover a window's loads otherwise
-    if (m == 1) launch_rows<1, 128>(qt, a, b, c, m, k, n, st);
-    else if (m == 2) launch_rows<2, 64>(qt, a, b, c, m, k, n, st);
-    else if (m <= 4) launch_rows<4, 64>(qt, a, b, c, m, k, n, st);
-    else launch_rows<kShardRows, 64>(qt, a, b, c, m, k, n, st);
+    if (m == 1) launch_rows<1, 128>(qt, a, b, dst, m, k, n, S, st);
+    else if (m == 2) launch_rows<2, 64>(qt, a, b, dst, m, k, n, S, st);
+    else if (m <= 4) launch_rows<4, 64>(qt, a, b, dst, m, k, n, S, st);
+    else launch_rows<kShardRows, 64>(qt, a, b, dst, m, k, n, S, st);
+    if (S > 1) {
+        const int64_t plane = (int64_t)m * n;
+        hipLaunchKernelGGL(k_shard_reduce, dim3((unsigned)((plane + 255) / 256)), dim3(256), 0, st,
+                           ws, S, plane, c);
+    }
     return hipGetLastError();
 }
 

@@ -125,8 +125,10 @@ hipError_t launch_combine(const float *Yr, int ks_r, int64_t stride_r, const flo
 // (rust/src/backend/cpu.rs:49-60); x, w, out 16-byte aligned, d % 4 == 0.
 // C[m,n] = A[m,k] B[k,n], B in the shard engine's Q8_0 / Q4_0 block layout
 // (qt LCMOE_TYPE_Q8_0 or LCMOE_TYPE_Q4_0); n % 32 == 0, m <= 65535 * 8.
+// S > 1: k in S slices (ceil(k / S) rows each) into ws [S, m, n], then
+// added in slice order into C.
 hipError_t launch_shard_matmul(int qt, const float *a, const uint8_t *b, float *c, int m, int k,
-                               int n, hipStream_t st);
+                               int n, hipStream_t st, int S = 1, float *ws = nullptr);
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int T, int d, float *out,
                           hipStream_t st);
 

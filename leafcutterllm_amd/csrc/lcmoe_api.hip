@@ -806,6 +806,28 @@ extern "C" lcmoe_status lcmoe_shard_matmul_dev(int32_t type, const float *a_dev,
     return LCMOE_OK;
 }
 
+extern "C" lcmoe_status lcmoe_shard_matmul_split_dev(int32_t type, const float *a_dev,
+                                                     const uint8_t *b_dev, float *c_dev,
+                                                     int32_t m, int32_t k, int32_t n,
+                                                     int32_t k_split, float *workspace,
+                                                     void *stream) {
+    clear_error();
+    size_t bb;
+    if (lcmoe_status s = shard_args(type, m, k, n, &bb)) return s;
+    if (k_split < 1 || k_split > 64)
+        return fail(LCMOE_ERR_INVALID_ARG, "k_split=%d outside [1, 64]", k_split);
+    if ((size_t)m * n == 0) return LCMOE_OK;
+    if (!c_dev || (k > 0 && (!a_dev || !b_dev)))
+        return fail(LCMOE_ERR_INVALID_ARG, "a, b or c is NULL");
+    if ((uintptr_t)b_dev & 1) return fail(LCMOE_ERR_INVALID_ARG, "b must be 2-byte aligned");
+    const int S = std::max(1, std::min<int>(k_split, k));  // no empty slices
+    if (S > 1 && (!workspace || ((uintptr_t)workspace & 3)))
+        return fail(LCMOE_ERR_INVALID_ARG, "k_split > 1 needs a 4-byte aligned workspace");
+    HIP_TRY(launch_shard_matmul(type, a_dev, b_dev, c_dev, m, k, n, (hipStream_t)stream, S,
+                                workspace));
+    return LCMOE_OK;
+}
+
 extern "C" lcmoe_status lcmoe_shard_matmul(int32_t type, const float *a, const uint8_t *b,
                                            float *c, int32_t m, int32_t k, int32_t n) {
     clear_error();

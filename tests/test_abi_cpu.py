@@ -171,3 +171,14 @@ def test_shard_matmul_argument_errors():
     assert lib.lcmoe_shard_matmul(8, *args, -1, 4, 32) == 1
     assert lib.lcmoe_shard_matmul(8, None, None, None, 2, 4, 32) == 1
     assert lib.lcmoe_shard_matmul_dev(8, None, None, None, 0, 4, 32, None) == 0  # empty
+
+
+def test_shard_matmul_split_argument_errors():
+    lib = L.lib()
+    a = np.ones((2, 8), np.float32)
+    b = np.zeros(8 * 34, np.uint8)
+    c = np.zeros((2, 32), np.float32)
+    args = (a.ctypes.data, b.ctypes.data, c.ctypes.data, 2, 8, 32)
+    assert lib.lcmoe_shard_matmul_split_dev(8, *args, 0, None, None) == 1    # k_split < 1
+    assert lib.lcmoe_shard_matmul_split_dev(8, *args, 65, None, None) == 1   # k_split > 64
+    assert lib.lcmoe_shard_matmul_split_dev(8, *args, 4, None, None) == 1    # no workspace

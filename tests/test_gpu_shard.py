@@ -77,3 +77,35 @@ def test_shard_matmul_dev_matches_host():
         for x in (da, db, dc):
             x.free()
     assert np.array_equal(_bits(out), _bits(ref))
+
+
+@pytest.mark.parametrize("qtype", [Q8, Q4])
+@pytest.mark.parametrize("m,k,n,S", [(1, 4096, 512, 16), (3, 101, 96, 4), (9, 250, 288, 64),
+                                     (1, 5, 64, 8), (2, 300, 64, 1)])
+def test_shard_matmul_split(qtype, m, k, n, S):
+    """k split into slices: deterministic, within the float64 error bound of
+    the exact product; one slice is bit-identical to the exact path."""
+    a, b = _case(qtype, m, k, n, seed=7 * k + S)
+    ref = O.shard_matmul(qtype, a, b, k, n)
+    da, db = hip.DeviceBuffer(a.nbytes).upload(a), hip.DeviceBuffer(b.nbytes).upload(b)
+    dc, ws = hip.DeviceBuffer(4 * m * n), hip.DeviceBuffer(4 * S * m * n)
+    st = hip.Stream()
+    outs = []
+    try:
+        for _ in range(2):
+            check(L.lib().lcmoe_shard_matmul_split_dev(qtype, da.ptr, db.ptr, dc.ptr, m, k, n, S,
+                                                       ws.ptr, st.ptr),
+                  "lcmoe_shard_matmul_split_dev")
+            st.synchronize()
+            outs.append(dc.download(np.empty((m, n), np.float32)))
+    finally:
+        for x in (da, db, dc, ws):
+            x.free()
+    assert np.array_equal(_bits(outs[0]), _bits(outs[1]))
+    if S == 1:
+        assert np.array_equal(_bits(outs[0]), _bits(ref))
+    # float64 product of the same dequantised weights, with a k-step bound
+    w = O.shard_matmul(qtype, np.eye(k, dtype=np.float32), b, k, n).astype(np.float64)
+    exact = a.astype(np.float64) @ w
+    bound = (k + S + 2) * 2.0 ** -24 * (np.abs(a.astype(np.float64)) @ np.abs(w))
+    assert np.all(np.abs(outs[0] - exact) <= bound + 1e-30)
