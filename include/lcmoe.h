@@ -68,8 +68,16 @@ enum {
     LCMOE_ROUTE_SIGMOID_GROUP = 2
 };
 
-/* Layer descriptor.  Limits: n_expert <= 256, n_expert_used <= 16,
- * n_shared <= 8, d_model % 256 == 0, d_ff % 32 == 0. */
+/* Layer descriptor.  Limits (checked by lcmoe_create): d_model % 32 == 0
+ * and d_model <= 16384, d_ff % 32 == 0, n_expert <= 256, n_expert_used <= 16,
+ * n_shared <= 8, max_tokens <= 65536.  The fast kernels need more: Q4_K /
+ * Q6_K / Q8_0 experts take the row-tiled layouts when the matrix rows are a
+ * multiple of 64 and d_model % 256 == 0, and the certified softmax router
+ * needs d_model / 256 in {1, 2, 4, 8, 16} and n_expert <= 64; every other
+ * valid shape runs the generic kernels and the exact router (same results,
+ * lower speed).  K-quant blocks of 256 run over the flattened matrix, so a
+ * K-quant matrix whose columns are not a multiple of 256 has blocks that
+ * straddle rows, as the reference decoder allows (kernels/mod.rs:66-70). */
 typedef struct {
     int32_t d_model;       /* d                                           */
     int32_t d_ff;          /* F, routed expert hidden size                */

@@ -622,9 +622,13 @@ extern "C" lcmoe_status lcmoe_set_norm(lcmoe_handle *h, const float *weight, flo
     HIP_TRY(hipSetDevice(h->device));
     const int d = h->desc.d_model;
     lcmoe_status st;
-    if (!h->norm_w) {
-        if ((st = alloc_n(h, &h->norm_w, d))) return st;
-        if ((st = alloc_n(h, &h->xn, (size_t)h->desc.max_tokens * d))) return st;
+    if (!h->norm_w || !h->xn) {
+        // both buffers or neither: the handle keeps them only when both allocations succeed
+        float *w = nullptr, *xn = nullptr;
+        if ((st = alloc_n(h, &xn, (size_t)h->desc.max_tokens * d))) return st;
+        if ((st = alloc_n(h, &w, d))) return st;
+        h->xn = xn;
+        h->norm_w = w;
     }
     // the stream may still be reading the previous weight
     HIP_TRY(hipStreamSynchronize(h->stream));
@@ -646,7 +650,7 @@ extern "C" lcmoe_status lcmoe_forward_norm_residual_dev(lcmoe_handle *h, const f
                                                         int32_t T, float *out_dev, void *stream) {
     clear_error();
     if (!h) return fail(LCMOE_ERR_INVALID_ARG, "handle is NULL");
-    if (!h->norm_w) return fail(LCMOE_ERR_STATE, "lcmoe_set_norm has not been called");
+    if (!h->norm_w || !h->xn) return fail(LCMOE_ERR_STATE, "lcmoe_set_norm has not been called");
     if (T < 0 || T > h->desc.max_tokens)
         return fail(LCMOE_ERR_INVALID_ARG, "T=%d outside [0, max_tokens=%d]", T, h->desc.max_tokens);
     if (T > 0 && (!hidden_dev || !out_dev))
@@ -674,7 +678,7 @@ extern "C" lcmoe_status lcmoe_forward_norm_residual(lcmoe_handle *h, const float
                                                     float *topk_w) {
     clear_error();
     if (!h) return fail(LCMOE_ERR_INVALID_ARG, "handle is NULL");
-    if (!h->norm_w) return fail(LCMOE_ERR_STATE, "lcmoe_set_norm has not been called");
+    if (!h->norm_w || !h->xn) return fail(LCMOE_ERR_STATE, "lcmoe_set_norm has not been called");
     if (T < 0 || T > h->desc.max_tokens)
         return fail(LCMOE_ERR_INVALID_ARG, "T=%d outside [0, max_tokens=%d]", T, h->desc.max_tokens);
     HIP_TRY(hipSetDevice(h->device));
@@ -820,7 +824,10 @@ extern "C" lcmoe_status lcmoe_shard_matmul_split_dev(int32_t type, const float *
     if (!c_dev || (k > 0 && (!a_dev || !b_dev)))
         return fail(LCMOE_ERR_INVALID_ARG, "a, b or c is NULL");
     if ((uintptr_t)b_dev & 1) return fail(LCMOE_ERR_INVALID_ARG, "b must be 2-byte aligned");
-    const int S = std::max(1, std::min<int>(k_split, k));  // no empty slices
+    // slices of ks = ceil(k / k_split) rows, and only as many as it takes to
+    // cover k: every slice holds at least one row (S <= k_split)
+    const int ks = k > 0 ? (k + k_split - 1) / k_split : 1;
+    const int S = k > 0 ? (k + ks - 1) / ks : 1;
     if (S > 1 && (!workspace || ((uintptr_t)workspace & 3)))
         return fail(LCMOE_ERR_INVALID_ARG, "k_split > 1 needs a 4-byte aligned workspace");
     HIP_TRY(launch_shard_matmul(type, a_dev, b_dev, c_dev, m, k, n, (hipStream_t)stream, S,

@@ -308,7 +308,7 @@ lcmoe_status parse(lcmoe_gguf &g) {
         ti.offset = c.get<uint64_t>();
         if (!c.ok) return fail(LCMOE_ERR_CORRUPT, "GGUF file truncated in tensor info %llu", (unsigned long long)k);
         for (int i = 0; i < ti.n_dims; i++) {
-            if (ti.dims[i] > ((uint64_t)1 << 62) / ti.count)
+            if (ti.count && ti.dims[i] > ((uint64_t)1 << 62) / ti.count)
                 return fail(LCMOE_ERR_CORRUPT, "tensor %s: element count overflows", ti.name.c_str());
             ti.count *= ti.dims[i];
         }

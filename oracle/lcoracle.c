@@ -776,15 +776,20 @@ int lco_moe_forward(const lco_desc *desc, const lco_weights *w, const float *x, 
     size_t szu = lco_tensor_size(desc->type_up, (size_t)F * D);
     size_t szd = lco_tensor_size(desc->type_down, (size_t)D * F);
     float *xe = (float *)malloc(sizeof(float) * A * D);
+    /* threads > 1: experts in parallel, each expert's products on one thread
+     * (the per-element arithmetic does not depend on the split) */
+    const int par = threads > 1;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(par ? threads : 1) if (par)
     for (int e = 0; e < E; e++) {
         int n = counts[e];
         if (!n) continue;
+        float *xr = xe + (size_t)offsets[e] * D;
         for (int r = 0; r < n; r++)
-            memcpy(xe + (size_t)r * D, x + (size_t)(perm[offsets[e] + r] / K) * D, sizeof(float) * D);
+            memcpy(xr + (size_t)r * D, x + (size_t)(perm[offsets[e] + r] / K) * D, sizeof(float) * D);
         float *wg = ingest(desc->type_gate, w->gate + (size_t)e * szg, F, D);
         float *wu = ingest(desc->type_up, w->up + (size_t)e * szu, F, D);
         float *wd = ingest(desc->type_down, w->down + (size_t)e * szd, D, F);
-        lco_ffn_dense(xe, n, D, F, wg, wu, wd, Y + (size_t)offsets[e] * D, threads);
+        lco_ffn_dense(xr, n, D, F, wg, wu, wd, Y + (size_t)offsets[e] * D, par ? 1 : threads);
         free(wg); free(wu); free(wd);
     }
     if (S > 0) {

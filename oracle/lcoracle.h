@@ -29,11 +29,23 @@
  *                          small-integer KATs that fix operand order and nibbles
  *   rms_norm             : reference test tensor.rs:204-209, float64 closed form,
  *                          exact constant rows, scale-then-weight rounding order
- *   top-k, group top-k   : brute force (full sort) incl. adversarial ties / NaN
- *   dispatch             : brute-force stable sort + permutation invariants
- *   layer forward        : float64 re-computation from dequantised weights,
- *                          E=1,K=1 reduces to the dense ffn_forward
- *                          (engine.rs:146-164), all-zero weights -> 0
+ *   route (all kinds)    : tests/test_oracle_route.py -- brute force over the
+ *                          full sort of (-z, e) with ties, +-0, +-inf and NaN
+ *                          for the softmax, renormalised-softmax and
+ *                          sigmoid-group routers (group scores, kept groups),
+ *                          weights in float64; hand-checked tie rows
+ *   dispatch             : tests/test_oracle_route.py -- numpy stable argsort,
+ *                          bincount / cumsum, permutation and inverse invariants
+ *   layer forward        : tests/test_oracle_route.py -- float64 recomputation
+ *                          from dequantised weights (selection, weights, experts,
+ *                          shared experts, combine); E=1,K=1 equals the dense
+ *                          ffn_forward (engine.rs:146-164) bit for bit;
+ *                          all-zero experts -> 0; duplicated experts additive;
+ *                          routed_scale exact; shared expert adds its FFN
+ *   golden fixtures      : tests/golden/moe_*.npz (written by
+ *                          tests/golden/make_golden.py) reproduced bit for bit
+ *                          and checked against the float64 recomputation
+ *                          (tests/test_golden.py)
  */
 #ifndef LCORACLE_H
 #define LCORACLE_H

@@ -1,5 +1,7 @@
 """Shared helpers for the GPU parity tests: build a layer, run the HIP path
 through the C ABI, run the oracle on the same bytes, compare."""
+import os
+
 import numpy as np
 
 import lcoracle as O
@@ -35,7 +37,7 @@ def check_routing(gpu: dict, ref: dict, T: int, K: int):
 
 
 def run_and_check(cfg: L.LayerConfig, layer: dict, x: np.ndarray, moe: L.MoeFfn = None,
-                  y_subset=None, threads: int = 8) -> dict:
+                  y_subset=None, threads: int = min(16, os.cpu_count() or 1)) -> dict:
     """Runs the HIP layer on x and checks it against the oracle.  Routing and
     dispatch are compared on the whole batch; y on all tokens, or only on the
     token rows in `y_subset` (each token's output depends on that token alone,

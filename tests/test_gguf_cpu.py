@@ -313,6 +313,21 @@ def test_open_errors(tmp_path):
     assert open_status(p) == "LCMOE_ERR_CORRUPT"
 
 
+@pytest.mark.parametrize("dims", [[0, 4], [4, 0, 2], [0], [3, 5, 0, 7]])
+def test_zero_dimension_tensor(tmp_path, dims):
+    """A zero dimension makes an empty tensor (count 0, 0 bytes, as
+    calculate_tensor_size gives, gguf.rs:307-313): the file opens and the
+    tensor reads back with its dims and no data."""
+    p = tmp_path / "zero.gguf"
+    W.write(p, [], [("z", dims, W.T_F32, b""), ("t", [2], W.T_F32, W.f32([1.0, 2.0]))])
+    assert open_status(p) == "LCMOE_OK"
+    ref = G.GgufRef(p.read_bytes())
+    assert len(ref.raw("z")) == 0
+    with L.GgufFile(p) as f:
+        assert f.get_tensor_info("z")["dims"] == dims
+        assert np.array_equal(np.frombuffer(f.get_tensor_raw("t"), np.float32), [1.0, 2.0])
+
+
 def test_truncation_sweep(tmp_path):
     """Every prefix of a small file: the product reader returns an error
     (never faults) exactly when the reference would fail to read the file

@@ -81,6 +81,10 @@ SMALL = {
     # Q6_K down with a 4-way column split and 4 shared experts
     "q6k-down-e16": small_config(
         "q6dn", 512, 1024, 16, 4, L.ROUTE_SOFTMAX, Q4, Q6, n_shared=1, d_ff_shared=512),
+    # d_model not a multiple of 256 (nor 128): K-quant blocks straddle rows of
+    # gate/up, generic expert kernels and the exact router
+    "q4k-d288-generic": small_config(
+        "d288", 288, 512, 8, 2, L.ROUTE_SOFTMAX_RENORM, Q4, Q4, n_shared=1, d_ff_shared=256),
 }
 
 
@@ -102,7 +106,7 @@ def test_small_layer_parity_many_tokens(name, T):
     cfg = SMALL[name]
     layer = L.synth_layer(cfg, seed=5)
     x = L.synth_x(cfg, T, seed=5, index=T)
-    res = run_and_check(cfg, layer, x, y_subset=[0, 1, T // 2, T - 1])
+    res = run_and_check(cfg, layer, x)
     assert res["rel_l2"] < 1e-3
 
 
@@ -246,8 +250,7 @@ def full_layers():
 def test_full_config_parity(full_layers, c, T):
     cfg, layer, moe = full_layers(c)
     x = L.synth_x(cfg, T, seed=0, index=T)
-    subset = None if T <= 16 else [0, T // 3, T - 1]
-    res = run_and_check(cfg, layer, x, moe=moe, y_subset=subset)
+    res = run_and_check(cfg, layer, x, moe=moe)
     print(f"config {c} T={T}: rel_l2={res['rel_l2']:.2e} touched={int((res['counts'] > 0).sum())}")
 
 
@@ -257,15 +260,14 @@ def test_full_config4_parity(full_layers, T):
     (matrix-core Q6_K path), one shared expert."""
     cfg, layer, moe = full_layers(4)
     x = L.synth_x(cfg, T, seed=0, index=T)
-    subset = None if T == 1 else [0, T // 2, T - 1]
-    res = run_and_check(cfg, layer, x, moe=moe, y_subset=subset)
+    res = run_and_check(cfg, layer, x, moe=moe)
     print(f"config 4 T={T}: rel_l2={res['rel_l2']:.2e} touched={int((res['counts'] > 0).sum())}")
 
 
 def test_full_config3_prefill_parity(full_layers):
     cfg, layer, moe = full_layers(3)
     x = L.synth_x(cfg, 2048, seed=0, index=2048)
-    res = run_and_check(cfg, layer, x, moe=moe, y_subset=[0, 1, 777, 2047])
+    res = run_and_check(cfg, layer, x, moe=moe)
     counts = res["counts"]
     assert counts[:8].sum() > counts[8:].sum()   # the +2.0 bias skews routing
     print(f"config 3 T=2048: rel_l2={res['rel_l2']:.2e} biased-share={counts[:8].sum() / counts.sum():.2f}")
