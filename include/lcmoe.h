@@ -285,6 +285,23 @@ lcmoe_status lcmoe_shard_matmul_split_dev(int32_t type, const float *a_dev, cons
                                           float *c_dev, int32_t m, int32_t k, int32_t n,
                                           int32_t k_split, float *workspace, void *stream);
 
+/* lcmoe_shard_matmul_split_dev without the workspace argument, for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  The k-slice planes live in a static device array of
+ * LCMOE_SHARD_SCRATCH_FLOATS floats (16 MiB) that each GPU holds until the
+ * process ends; a call whose slices need more (S * m * n floats, S the slice
+ * count the k_split rule below gives, S > 1) returns LCMOE_ERR_INVALID_ARG.
+ * The call allocates nothing.  All calls on one GPU share its array: calls
+ * that overlap in time on one GPU (two streams, two threads) race and must
+ * be ordered by the caller.  Same results as lcmoe_shard_matmul_split_dev
+ * with the same k_split. */
+#define LCMOE_SHARD_SCRATCH_FLOATS (4 * 1024 * 1024)
+lcmoe_status lcmoe_shard_matmul_split_noalloc_dev(int32_t type, const float *a_dev,
+                                                  const uint8_t *b_dev, float *c_dev, int32_t m,
+                                                  int32_t k, int32_t n, int32_t k_split,
+                                                  void *stream);
+
 /* ---- device self-tests (need a GPU; used by the parity tests) ---------- */
 
 /* Decode `count` elements of a GGUF tensor with the device decoders and

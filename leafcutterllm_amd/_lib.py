@@ -33,6 +33,7 @@ EXPORTS = (
     "lcmoe_gguf_moe_layer", "lcmoe_set_norm", "lcmoe_forward_norm_residual",
     "lcmoe_forward_norm_residual_dev", "lcmoe_debug_rmsnorm", "lcmoe_shard_matmul",
     "lcmoe_shard_matmul_dev", "lcmoe_shard_matmul_split_dev",
+    "lcmoe_shard_matmul_split_noalloc_dev",
 )
 
 
@@ -104,6 +105,7 @@ def lib() -> C.CDLL:
         "lcmoe_shard_matmul": (i32, [i32, vp, vp, vp, i32, i32, i32]),
         "lcmoe_shard_matmul_dev": (i32, [i32, vp, vp, vp, i32, i32, i32, vp]),
         "lcmoe_shard_matmul_split_dev": (i32, [i32, vp, vp, vp, i32, i32, i32, i32, vp, vp]),
+        "lcmoe_shard_matmul_split_noalloc_dev": (i32, [i32, vp, vp, vp, i32, i32, i32, i32, vp]),
         "lcmoe_forward_norm_residual": (i32, [vp, vp, i32, vp, vp, vp]),
         "lcmoe_forward_norm_residual_dev": (i32, [vp, vp, i32, vp, vp]),
         "lcmoe_gguf_open": (i32, [C.c_char_p, P(vp)]),

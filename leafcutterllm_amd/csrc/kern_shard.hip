@@ -12,10 +12,39 @@
 // column, kShardRows rows of A per block held as independent chains, the
 // weights and A staged through LDS a window of kShardWin k-rows ahead.
 
+#include <mutex>
+
 #include "device_common.h"
 #include "kernels.h"
 
 namespace lcmoe {
+
+// Scratch of lcmoe_shard_matmul_split_noalloc_dev: the k-slice planes
+// [S, m, n].  Every GPU the library runs on holds its own copy until the
+// process ends.  Host code never passes this name to a kernel (on the host it
+// is a stand-in, not a device address); it uses the per-device address that
+// shard_scratch() looks up.
+static __device__ __align__(256) float scratch[kShardScratchFloats];
+
+hipError_t shard_scratch(float **out) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static float *addr[kMaxDevices];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        float *p = nullptr;
+        e = hipGetSymbolAddress((void **)&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        addr[dev] = p;
+    }
+    *out = addr[dev];
+    return hipSuccess;
+}
+
 namespace {
 
 constexpr int kShardCols = 64;   // columns per block: one wave, one lane per column

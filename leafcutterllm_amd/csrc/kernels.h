@@ -6,6 +6,7 @@
 
 #include <cstdint>
 
+#include "../../include/lcmoe.h"
 #include "chains.h"
 
 namespace lcmoe {
@@ -121,14 +122,19 @@ hipError_t launch_combine(const float *Yr, int ks_r, int64_t stride_r, const flo
                           int64_t stride_s, const int32_t *inv, float *topk_w, int T, int K,
                           int S, int d, const CombineRoute &cr, float *y, hipStream_t st,
                           const float *resid = nullptr);
-// out[t] = rms_norm(x[t]) * w, bit-exact with the reference CPU backend
-// (rust/src/backend/cpu.rs:49-60); x, w, out 16-byte aligned, d % 4 == 0.
 // C[m,n] = A[m,k] B[k,n], B in the shard engine's Q8_0 / Q4_0 block layout
 // (qt LCMOE_TYPE_Q8_0 or LCMOE_TYPE_Q4_0); n % 32 == 0, m <= 65535 * 8.
 // S > 1: k in S slices (ceil(k / S) rows each) into ws [S, m, n], then
 // added in slice order into C.
 hipError_t launch_shard_matmul(int qt, const float *a, const uint8_t *b, float *c, int m, int k,
                                int n, hipStream_t st, int S = 1, float *ws = nullptr);
+// The current device's address of the static k-slice scratch
+// (kShardScratchFloats floats, one copy per GPU, kern_shard.hip), looked up
+// once per device; it stands in for ws in launch_shard_matmul.
+constexpr int64_t kShardScratchFloats = LCMOE_SHARD_SCRATCH_FLOATS;
+hipError_t shard_scratch(float **out);
+// out[t] = rms_norm(x[t]) * w, bit-exact with the reference CPU backend
+// (rust/src/backend/cpu.rs:49-60); x, w, out 16-byte aligned, d % 4 == 0.
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int T, int d, float *out,
                           hipStream_t st);
 

@@ -835,6 +835,34 @@ extern "C" lcmoe_status lcmoe_shard_matmul_split_dev(int32_t type, const float *
     return LCMOE_OK;
 }
 
+extern "C" lcmoe_status lcmoe_shard_matmul_split_noalloc_dev(int32_t type, const float *a_dev,
+                                                             const uint8_t *b_dev, float *c_dev,
+                                                             int32_t m, int32_t k, int32_t n,
+                                                             int32_t k_split, void *stream) {
+    clear_error();
+    size_t bb;
+    if (lcmoe_status s = shard_args(type, m, k, n, &bb)) return s;
+    if (k_split < 1 || k_split > 64)
+        return fail(LCMOE_ERR_INVALID_ARG, "k_split=%d outside [1, 64]", k_split);
+    if ((size_t)m * n == 0) return LCMOE_OK;
+    if (!c_dev || (k > 0 && (!a_dev || !b_dev)))
+        return fail(LCMOE_ERR_INVALID_ARG, "a, b or c is NULL");
+    if ((uintptr_t)b_dev & 1) return fail(LCMOE_ERR_INVALID_ARG, "b must be 2-byte aligned");
+    const int ks = k > 0 ? (k + k_split - 1) / k_split : 1;
+    const int S = k > 0 ? (k + ks - 1) / ks : 1;
+    float *ws = nullptr;
+    if (S > 1) {
+        if ((int64_t)S * m * n > kShardScratchFloats)
+            return fail(LCMOE_ERR_INVALID_ARG,
+                        "%d slices of %d x %d need %lld floats of scratch, more than the %lld "
+                        "of the static array (lower k_split)",
+                        S, m, n, (long long)S * m * n, (long long)kShardScratchFloats);
+        HIP_TRY(shard_scratch(&ws));
+    }
+    HIP_TRY(launch_shard_matmul(type, a_dev, b_dev, c_dev, m, k, n, (hipStream_t)stream, S, ws));
+    return LCMOE_OK;
+}
+
 extern "C" lcmoe_status lcmoe_shard_matmul(int32_t type, const float *a, const uint8_t *b,
                                            float *c, int32_t m, int32_t k, int32_t n) {
     clear_error();
