@@ -190,6 +190,81 @@ def shard_matmul_bench(args) -> None:
     }))
 
 
+def e2e_bench(args) -> None:
+    """Config 5: the 24-layer synthetic MoE decoder end to end
+    (lcmoe_model_generate): a 512-token random-id prompt per sequence, then
+    256 greedy tokens, at B = 1 and B = 16.  Prefill runs one sequence per
+    forward (the reference's one-call prompt, engine.rs:54); the 255 decode
+    steps replay one captured HIP graph.  Times come from HIP events on the
+    model's stream; the first generate of each batch size (8 tokens) is the
+    warm-up that also captures its graph."""
+    import numpy as np
+
+    import leafcutterllm_amd as L
+    from leafcutterllm_amd.configs import tensor_size
+
+    mc = L.MODEL_CONFIGS[5]
+    P, n_new = 512, 256
+    batches = [int(b) for b in args.e2e_batches.split(",")]
+    t0 = time.perf_counter()
+    w = L.synth_model(mc, seed=0)
+    t_synth = time.perf_counter() - t0
+    rng = np.random.default_rng(0)
+    per = {}
+    with L.Model(mc.desc(max(batches), P, P + n_new), w) as m:
+        del w
+        for B in batches:
+            prompts = rng.integers(0, mc.vocab, (B, P)).astype(np.int32)
+            m.generate(prompts, 8)
+            t0 = time.perf_counter()
+            out, _ = m.generate(prompts, n_new)
+            wall = time.perf_counter() - t0
+            pre, dec = m.last_timing()
+            per[str(B)] = {
+                "prefill_ms": round(pre, 3), "decode_ms": round(dec, 3),
+                "decode_tokens_per_s": round(B * (n_new - 1) / (dec * 1e-3), 2),
+                "ms_per_decode_step": round(dec / (n_new - 1), 4),
+                "e2e_tokens_per_s": round(B * n_new / ((pre + dec) * 1e-3), 2),
+                "prefill_tokens_per_s": round(B * P / (pre * 1e-3), 1),
+                "wall_s": round(wall, 3),
+                "distinct_ids": int(len(np.unique(out))),
+            }
+    # B = 1 decode step: every weight byte a token touches (one token uses
+    # exactly K routed + S shared experts per layer) plus the KV cache it
+    # reads at the mean context
+    lc = mc.layer
+    d, qd = mc.d_model, mc.n_head * mc.head_dim
+    attn = tensor_size(mc.attn_type, (qd + 2 * mc.n_kv_head * mc.head_dim) * d) \
+        + tensor_size(mc.attn_type, d * qd)
+    moe = (lc.n_expert_used * lc.expert_bytes() + lc.n_shared * lc.shared_bytes()
+           + 4 * d * lc.n_expert)
+    kv = 2 * 2 * mc.n_kv_head * mc.head_dim * (P + n_new / 2)
+    step_bytes = mc.n_layer * (attn + moe + kv) + tensor_size(mc.attn_type, mc.vocab * d)
+    head = per[str(max(batches))]
+    b1 = per.get("1")
+    out = {
+        "metric": "end-to-end greedy decode tokens/s, config 5 (24-layer MoE decoder, Q4_K)",
+        "value": head["decode_tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
+        "steps": n_new - 1, "warmup": 1, "ms_per_step": head["ms_per_decode_step"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 (Q4_K weights; MoE products f16 hi+lo on MFMA; f16 KV cache)",
+        "data": "synthetic (seeded N(0,0.02) weights quantised to Q4_K, random prompt ids)",
+        "config": {"workload": f"config 5: {mc.note}, prompt {P}, {n_new} greedy tokens, "
+                               f"B={max(batches)}", "entry": "lcmoe_model_generate",
+                   "n_layer": mc.n_layer, "d_model": d, "n_head": mc.n_head,
+                   "head_dim": mc.head_dim, "vocab": mc.vocab, "batches": batches},
+        "per_batch": per,
+        "synth_s": round(t_synth, 1),
+    }
+    if b1:
+        gbs = step_bytes / (b1["ms_per_decode_step"] * 1e-3) / 1e9
+        out["roofline"] = {"bound": "hbm", "kernel": "whole B=1 decode step (all launches)",
+                           "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                           "algorithmic_bytes": int(step_bytes)}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -210,6 +285,8 @@ def main():
                     help="only time lcmoe_shard_matmul_dev (TYPE q8 or q4) on one shape")
     ap.add_argument("--shard-split", type=int, default=1, metavar="S",
                     help="with --shard-matmul: time lcmoe_shard_matmul_split_dev with S k-slices")
+    ap.add_argument("--e2e-batches", default="1,16",
+                    help="with --config 5: batch sizes of the end-to-end decode")
     args = ap.parse_args()
 
     if args.copy_probe:
@@ -217,6 +294,10 @@ def main():
         return
     if args.shard_matmul:
         shard_matmul_bench(args)
+        return
+
+    if args.config == 5 and args.gpus == 1:
+        e2e_bench(args)
         return
 
     if args.gpus != 1:

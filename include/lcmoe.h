@@ -251,6 +251,91 @@ int32_t lcmoe_gguf_is_moe_layer(const lcmoe_gguf *g, int32_t layer);
 lcmoe_status lcmoe_gguf_moe_layer(lcmoe_gguf *g, int32_t layer, int32_t max_tokens,
                                   lcmoe_desc *desc, lcmoe_weights *w);
 
+/* ---- end-to-end decoder model (the MoE FFN's caller) ------------------ */
+
+/* The reference engine's decode path around the MoE FFN, on the GPU:
+ * Engine::forward / generate (rust/src/inference/engine.rs:51-132) with the
+ * dense ffn_forward call (engine.rs:114) replaced by this library's MoE
+ * layer.  Per layer: rms_norm (cpu.rs:49-60) -> attention_forward
+ * (attention.rs:37-118: x W_q / W_k / W_v, RoPE, f16 KV cache
+ * (cache/mod.rs:33-78), causal softmax attention, x W_o) -> residual ->
+ * lcmoe_forward_norm_residual_dev (norm, MoE FFN, residual); then the final
+ * rms_norm, the lm_head product of each sequence's last token and greedy
+ * sampling (sample_top_p with temperature 0, sampler.rs:8-10: the LAST of
+ * equal maxima under f32::total_cmp).  Several sequences (a batch) each keep
+ * their own cache. */
+
+/* RoPE positions: the reference rotates token i of each forward call by
+ * position i, restarting at 0 on every call (attention.rs:13-17, called with
+ * the call's seq_len: a decode token is rotated by 0).  ABSOLUTE rotates by
+ * the token's position in its sequence instead. */
+enum { LCMOE_ROPE_PER_CALL = 0, LCMOE_ROPE_ABSOLUTE = 1 };
+
+typedef struct {
+    int32_t n_layer, d_model, n_head, n_kv_head, head_dim, vocab;
+    float rope_theta;      /* rope.freq_base (loader.rs:124-125)          */
+    float norm_eps;        /* 1e-5 in the reference (engine.rs:100, :111) */
+    int32_t rope_positions;/* LCMOE_ROPE_*                                */
+    int32_t attn_type;     /* GGUF type of attn_q/k/v/o, token_embd and
+                              output: LCMOE_TYPE_Q4_K, _Q8_0 or _F32      */
+    int32_t max_batch;     /* sequences decoded together (<= 1024)        */
+    int32_t max_prompt;    /* longest prompt (prefilled one sequence per
+                              call)                                       */
+    int32_t max_ctx;       /* KV cache positions per sequence             */
+    lcmoe_desc moe;        /* every layer's MoE FFN; d_model must match;
+                              max_tokens is set by the model              */
+} lcmoe_model_desc;
+
+/* One decoder layer, GGUF tensors blk.N.* (arch.rs:83-96 names them
+ * input_layernorm / self_attn.* / post_attention_layernorm): matrices are
+ * [out rows, in cols] with blocks along the input, exactly the GGUF bytes;
+ * the norms are f32. */
+typedef struct {
+    const float *attn_norm;                /* [d]                         */
+    const uint8_t *attn_q;                 /* [n_head * head_dim, d]      */
+    const uint8_t *attn_k, *attn_v;        /* [n_kv_head * head_dim, d]   */
+    const uint8_t *attn_o;                 /* [d, n_head * head_dim]      */
+    const float *ffn_norm;                 /* [d]                         */
+    lcmoe_weights moe;                     /* as lcmoe_create takes       */
+} lcmoe_layer_weights;
+
+typedef struct {
+    const uint8_t *token_embd;             /* [vocab, d]                  */
+    const float *output_norm;              /* [d]                         */
+    const uint8_t *output;                 /* lm_head [vocab, d]          */
+    const lcmoe_layer_weights *layers;     /* n_layer of them             */
+} lcmoe_model_weights;
+
+typedef struct lcmoe_model lcmoe_model;
+
+/* Engine::load's resident counterpart: validates, uploads every tensor once
+ * (each layer's MoE through lcmoe_create) and allocates the KV caches of
+ * max_batch sequences.  The caller keeps ownership of the host bytes. */
+lcmoe_status lcmoe_model_create(const lcmoe_model_desc *desc, const lcmoe_model_weights *w,
+                                lcmoe_model **out);
+void lcmoe_model_destroy(lcmoe_model *m);
+/* KVCache::clear (cache/mod.rs:27-31) for every sequence. */
+lcmoe_status lcmoe_model_reset(lcmoe_model *m);
+/* Engine::forward (engine.rs:78-132) for sequences 0 .. B-1, each taking
+ * its T tokens tokens[b * T .. b * T + T) after what its cache holds;
+ * logits [B, vocab] of each sequence's last token.  Host buffers,
+ * synchronous.  T == 1 runs the batch together; T > 1 one sequence at a
+ * time (T <= max_prompt).  An id outside [0, vocab) embeds as zeros
+ * (engine.rs:138). */
+lcmoe_status lcmoe_model_forward(lcmoe_model *m, const int32_t *tokens, int32_t B, int32_t T,
+                                 float *logits);
+/* Engine::generate (engine.rs:51-76) with greedy sampling for B sequences
+ * of P prompt tokens each (prompt [B, P]): reset, prefill each sequence,
+ * then n_new - 1 batched decode steps (one captured HIP graph, replayed).
+ * out [B, n_new] receives the generated ids; n_out[b] (optional) the count
+ * up to and including the first `eos` (the reference stops at id 2; pass -1
+ * to never stop).  P + n_new - 1 <= max_ctx. */
+lcmoe_status lcmoe_model_generate(lcmoe_model *m, const int32_t *prompt, int32_t B, int32_t P,
+                                  int32_t n_new, int32_t eos, int32_t *out, int32_t *n_out);
+/* Device time of the last lcmoe_model_generate: prefill (all sequences)
+ * and decode (all steps), milliseconds, from HIP events on its stream. */
+lcmoe_status lcmoe_model_last_timing(lcmoe_model *m, double *prefill_ms, double *decode_ms);
+
 /* ---- shard-layout quantised GEMM -------------------------------------- */
 
 /* C[m,n] = A[m,k] B[k,n] for the shard engine's quantised matrices: the

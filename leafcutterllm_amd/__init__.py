@@ -5,12 +5,14 @@ package binds it with ctypes and carries the benchmark layer shapes.
 """
 from ._lib import (ROUTE_SIGMOID_GROUP, ROUTE_SOFTMAX, ROUTE_SOFTMAX_RENORM, TYPE_F32,
                    TYPE_Q4_0, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0, Desc, LcmoeError, Weights, lib)
-from .configs import CONFIGS, LayerConfig, synth_layer, synth_x
+from .configs import CONFIGS, MODEL_CONFIGS, LayerConfig, ModelConfig, synth_layer, synth_model, synth_x
 from .gguf import GgufFile
+from .model import Model, ModelDesc
 from .moe import MoeFfn, debug_dequant, debug_rmsnorm, debug_sigmoid, shard_matmul
 
 __all__ = [
-    "CONFIGS", "LayerConfig", "synth_layer", "synth_x", "MoeFfn", "GgufFile", "Desc", "Weights",
+    "CONFIGS", "MODEL_CONFIGS", "LayerConfig", "ModelConfig", "synth_layer", "synth_model",
+    "synth_x", "MoeFfn", "Model", "ModelDesc", "GgufFile", "Desc", "Weights",
     "LcmoeError", "lib", "debug_dequant", "debug_rmsnorm", "debug_sigmoid", "shard_matmul", "TYPE_F32", "TYPE_Q4_0", "TYPE_Q8_0",
     "TYPE_Q4_K", "TYPE_Q6_K", "ROUTE_SOFTMAX_RENORM", "ROUTE_SOFTMAX", "ROUTE_SIGMOID_GROUP",
 ]

@@ -33,7 +33,9 @@ EXPORTS = (
     "lcmoe_gguf_moe_layer", "lcmoe_set_norm", "lcmoe_forward_norm_residual",
     "lcmoe_forward_norm_residual_dev", "lcmoe_debug_rmsnorm", "lcmoe_shard_matmul",
     "lcmoe_shard_matmul_dev", "lcmoe_shard_matmul_split_dev",
-    "lcmoe_shard_matmul_split_noalloc_dev",
+    "lcmoe_shard_matmul_split_noalloc_dev", "lcmoe_model_create", "lcmoe_model_destroy",
+    "lcmoe_model_reset", "lcmoe_model_forward", "lcmoe_model_generate",
+    "lcmoe_model_last_timing",
 )
 
 

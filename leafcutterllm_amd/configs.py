@@ -159,5 +159,87 @@ def small_config(name: str, d: int, F: int, E: int, K: int, route_kind: int, qg:
     return LayerConfig(name, d, F, E, K, route_kind, qg, qd, **kw)
 
 
+# ---- end-to-end decoder model -----------------------------------------------
+
+S_EMBD, S_OUT, S_NORM, S_ATTN = 16, 17, 18, 19  # stream kinds of the model tensors
+
+
+@dataclass
+class ModelConfig:
+    """A decoder model around the MoE layer `layer` (the engine of
+    rust/src/inference/engine.rs:78-132 with an MoE FFN)."""
+    name: str
+    n_layer: int
+    n_head: int
+    n_kv_head: int
+    head_dim: int
+    vocab: int
+    rope_theta: float
+    layer: LayerConfig
+    attn_type: int = TYPE_Q4_K
+    note: str = ""
+
+    @property
+    def d_model(self) -> int:
+        return self.layer.d_model
+
+    def desc(self, max_batch: int, max_prompt: int, max_ctx: int, rope_positions: int = 0,
+             n_layer: int = 0):
+        from .model import ModelDesc
+        d = ModelDesc()
+        d.n_layer = n_layer or self.n_layer
+        d.d_model, d.n_head, d.n_kv_head = self.d_model, self.n_head, self.n_kv_head
+        d.head_dim, d.vocab, d.rope_theta, d.norm_eps = self.head_dim, self.vocab, self.rope_theta, 1e-5
+        d.rope_positions, d.attn_type = rope_positions, self.attn_type
+        d.max_batch, d.max_prompt, d.max_ctx = max_batch, max_prompt, max_ctx
+        d.moe = self.layer.desc(max(max_batch, max_prompt))
+        return d
+
+    def layer_bytes(self) -> int:
+        """Resident bytes of one decoder layer's weights."""
+        d, qd, kvd = self.d_model, self.n_head * self.head_dim, self.n_kv_head * self.head_dim
+        ts = tensor_size
+        attn = ts(self.attn_type, (qd + 2 * kvd) * d) + ts(self.attn_type, d * qd)
+        return attn + self.layer.layer_bytes() + 8 * d
+
+
+MODEL_CONFIGS = {
+    # BASELINE config 5: 24 layers, d_model 2048, 16 heads x 128 with RoPE,
+    # the config-5 MoE layer (60 experts top-4 + 4 shared, d_ff 1408), vocab
+    # 32000, every matrix Q4_K.  RoPE base: the reference's default
+    # (ModelConfig::default, rust/src/model/loader.rs:24-36).
+    5: ModelConfig("e2e-moe-24l-q4_k", 24, 16, 16, 128, 32000, 10000.0, CONFIGS[5],
+                   note="24-layer synthetic MoE decoder, Q4_K"),
+}
+
+
+def synth_model(mc: ModelConfig, seed: int = 0, n_layer: int = 0) -> dict:
+    """Seeded synthetic model weights (N(0, 0.02) matrices quantised to
+    mc.attn_type / the MoE types, norm weights 1 + N(0, 0.02)), keyed as
+    Model and the oracle's engine take them; layer l's MoE is
+    synth_layer(mc.layer, seed * 1000 + l)."""
+    n_layer = n_layer or mc.n_layer
+    d, V = mc.d_model, mc.vocab
+    qd, kvd = mc.n_head * mc.head_dim, mc.n_kv_head * mc.head_dim
+
+    def mat(rows, cols, kind, index):
+        return quantize(mc.attn_type, synth_normal(seed, stream(kind, index), WEIGHT_STD, rows * cols))
+
+    def norm(index):
+        return 1.0 + synth_normal(seed, stream(S_NORM, index), WEIGHT_STD, d)
+
+    layers = []
+    for l in range(n_layer):
+        layers.append({
+            "attn_norm": norm(2 * l), "ffn_norm": norm(2 * l + 1),
+            "attn_q": mat(qd, d, S_ATTN, 4 * l), "attn_k": mat(kvd, d, S_ATTN, 4 * l + 1),
+            "attn_v": mat(kvd, d, S_ATTN, 4 * l + 2), "attn_o": mat(d, qd, S_ATTN, 4 * l + 3),
+            "moe": synth_layer(mc.layer, seed=seed * 1000 + l),
+        })
+    return {"token_embd": mat(V, d, S_EMBD, 0), "output": mat(V, d, S_OUT, 0),
+            "output_norm": norm(1 << 20), "layers": layers}
+
+
 __all__ = ["CONFIGS", "LayerConfig", "synth_layer", "synth_x", "synth_normal", "quantize",
-           "tensor_size", "stream", "small_config", "C"]
+           "tensor_size", "stream", "small_config", "C", "ModelConfig", "MODEL_CONFIGS",
+           "synth_model"]

@@ -138,6 +138,24 @@ hipError_t shard_scratch(float **out);
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int T, int d, float *out,
                           hipStream_t st);
 
+// ---- decoder-layer kernels of the end-to-end engine (kern_engine.hip) ----
+hipError_t launch_embed(int qt, const uint8_t *table, int vocab, int d, const int32_t *tok, int nq,
+                        float *x, hipStream_t st);
+// Y[t, :N] (+= R) = X[t, :K] W^T, W GGUF [N, K] of type qt with K whole blocks
+hipError_t launch_linear(int qt, const uint8_t *W, int N, int K, const float *X, int64_t ldx, int T,
+                         const float *R, float *Y, int64_t ldy, hipStream_t st);
+hipError_t launch_rope_kv(const float *qkv, int nq, int T, int seq0, const int32_t *lens, int H,
+                          int KVH, int hd, const float *freq, int absolute, float *qo,
+                          _Float16 *kc, _Float16 *vc, int ctx, hipStream_t st);
+hipError_t launch_attention(const float *qr, int nq, int T, int seq0, const int32_t *lens, int H,
+                            int KVH, int hd, const _Float16 *kc, const _Float16 *vc, int ctx,
+                            float *part, float *out, hipStream_t st);
+hipError_t launch_argmax(const float *logits, int nseq, int V, int seq0, int32_t *next,
+                         int32_t *out, int out_ld, const int32_t *step, hipStream_t st);
+hipError_t launch_advance(int32_t *lens, int seq0, int nseq, int T, int32_t *step, int dstep,
+                          hipStream_t st);
+int64_t attention_part_floats(int nq, int H, int hd, int ctx);
+
 hipError_t launch_debug_dequant(int qt, const uint8_t *src, int64_t count, float *out,
                                 hipStream_t st);
 hipError_t launch_debug_sigmoid(const float *x, int64_t n, float *out, hipStream_t st);

@@ -1,0 +1,392 @@
+// The end-to-end decoder model (lcmoe_model_*, include/lcmoe.h): the
+// reference engine's forward and greedy generation
+// (rust/src/inference/engine.rs:51-132) on one GPU, with every layer's FFN
+// through the MoE layer (lcmoe_forward_norm_residual_dev).  Weights are
+// resident from lcmoe_model_create; each sequence of a batch keeps its own
+// f16 KV cache.  A decode step reads the cache lengths and the previous
+// tokens from device memory, so its launch sequence never changes: it is
+// captured once into a HIP graph and replayed for every step.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <new>
+#include <vector>
+
+#include "kernels.h"
+#include "lcmoe_internal.h"
+
+using namespace lcmoe;
+
+#define HIP_TRY(expr)                                                                    \
+    do {                                                                                 \
+        hipError_t e_ = (expr);                                                          \
+        if (e_ != hipSuccess)                                                            \
+            return fail(LCMOE_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_));          \
+    } while (0)
+
+struct lcmoe_model {
+    lcmoe_model_desc desc{};
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::vector<void *> allocs;
+    struct Layer {
+        uint8_t *wqkv = nullptr, *wo = nullptr;  // q, k, v rows stacked; o
+        float *attn_norm = nullptr;
+        lcmoe_handle *moe = nullptr;
+    };
+    std::vector<Layer> layers;
+    uint8_t *embd = nullptr, *out_w = nullptr;
+    float *out_norm = nullptr, *freq = nullptr;
+    _Float16 *kc = nullptr, *vc = nullptr;  // [layer][seq][ctx][kv head][head_dim]
+    int32_t *lens = nullptr, *step = nullptr, *tok = nullptr, *next = nullptr, *out_tok = nullptr;
+    float *hidden = nullptr, *xn = nullptr, *qkv = nullptr, *qr = nullptr, *attn = nullptr,
+          *part = nullptr, *logits = nullptr;
+    int tmax = 0;                  // tokens per internal forward
+    std::vector<int32_t> lens_h;   // host mirror of lens (every update goes through here)
+    hipGraphExec_t graph = nullptr;
+    int graph_B = 0;
+    hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};  // start, prefilled, decode, end
+    double prefill_ms = 0, decode_ms = 0;
+};
+
+namespace {
+
+template <class T>
+lcmoe_status alloc_n(lcmoe_model *m, T **p, size_t n) {
+    void *v = nullptr;
+    hipError_t e = hipMalloc(&v, std::max<size_t>(n * sizeof(T), 256));
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        *p = nullptr;
+        return fail(e == hipErrorOutOfMemory ? LCMOE_ERR_OUT_OF_MEMORY : LCMOE_ERR_HIP,
+                    "hipMalloc(%zu): %s", n * sizeof(T), hipGetErrorString(e));
+    }
+    m->allocs.push_back(v);
+    *p = static_cast<T *>(v);
+    return LCMOE_OK;
+}
+
+template <class T>
+lcmoe_status upload(lcmoe_model *m, T **dst, const void *src, size_t bytes) {
+    lcmoe_status st = alloc_n(m, reinterpret_cast<uint8_t **>(dst), bytes);
+    if (st) return st;
+    HIP_TRY(hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice));
+    return LCMOE_OK;
+}
+
+void free_model(lcmoe_model *m) {
+    if (!m) return;
+    (void)hipSetDevice(m->device);
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    if (m->graph) (void)hipGraphExecDestroy(m->graph);
+    for (auto &L : m->layers)
+        if (L.moe) lcmoe_destroy(L.moe);
+    for (void *p : m->allocs) (void)hipFree(p);
+    for (hipEvent_t e : m->ev)
+        if (e) (void)hipEventDestroy(e);
+    if (m->stream) (void)hipStreamDestroy(m->stream);
+    delete m;
+}
+
+bool attn_type_ok(int t) {
+    return t == LCMOE_TYPE_Q4_K || t == LCMOE_TYPE_Q8_0 || t == LCMOE_TYPE_F32;
+}
+
+lcmoe_status validate(const lcmoe_model_desc *d, const lcmoe_model_weights *w) {
+    if (!d || !w || !w->token_embd || !w->output_norm || !w->output || !w->layers)
+        return fail(LCMOE_ERR_INVALID_ARG, "desc, weights or a model tensor is NULL");
+    if (d->n_layer < 1 || d->n_layer > 4096)
+        return fail(LCMOE_ERR_INVALID_ARG, "n_layer=%d outside [1, 4096]", d->n_layer);
+    if (d->d_model != d->moe.d_model)
+        return fail(LCMOE_ERR_INVALID_ARG, "d_model=%d differs from moe.d_model=%d", d->d_model,
+                    d->moe.d_model);
+    if (d->n_head < 1 || d->n_kv_head < 1 || d->n_head % d->n_kv_head)
+        return fail(LCMOE_ERR_INVALID_ARG, "n_head=%d must be a positive multiple of n_kv_head=%d",
+                    d->n_head, d->n_kv_head);
+    if (d->head_dim < 8 || d->head_dim > 256 || d->head_dim % 8)
+        return fail(LCMOE_ERR_INVALID_ARG, "head_dim=%d must be a multiple of 8 in [8, 256]",
+                    d->head_dim);
+    if (d->vocab < 1) return fail(LCMOE_ERR_INVALID_ARG, "vocab=%d", d->vocab);
+    if (!attn_type_ok(d->attn_type))
+        return fail(LCMOE_ERR_UNSUPPORTED, "attn_type=%d (Q4_K, Q8_0 or F32)", d->attn_type);
+    const int64_t bs = block_size(d->attn_type);
+    const int64_t qd = (int64_t)d->n_head * d->head_dim;
+    if (d->d_model % bs || qd % bs || qd % 8 || d->d_model % 8)
+        return fail(LCMOE_ERR_INVALID_ARG,
+                    "d_model=%d and n_head*head_dim=%lld must be whole blocks of %lld", d->d_model,
+                    (long long)qd, (long long)bs);
+    if (!(d->rope_theta > 0.0f) || !std::isfinite(d->rope_theta))
+        return fail(LCMOE_ERR_INVALID_ARG, "rope_theta must be finite and > 0");
+    if (!(d->norm_eps >= 0.0f) || !std::isfinite(d->norm_eps))
+        return fail(LCMOE_ERR_INVALID_ARG, "norm_eps must be finite and >= 0");
+    if (d->rope_positions != LCMOE_ROPE_PER_CALL && d->rope_positions != LCMOE_ROPE_ABSOLUTE)
+        return fail(LCMOE_ERR_INVALID_ARG, "rope_positions=%d", d->rope_positions);
+    if (d->max_batch < 1 || d->max_batch > 1024)
+        return fail(LCMOE_ERR_INVALID_ARG, "max_batch=%d outside [1, 1024]", d->max_batch);
+    if (d->max_ctx < 1 || d->max_prompt < 1 || d->max_prompt > d->max_ctx)
+        return fail(LCMOE_ERR_INVALID_ARG, "need 1 <= max_prompt=%d <= max_ctx=%d", d->max_prompt,
+                    d->max_ctx);
+    if (std::max(d->max_prompt, d->max_batch) > 65536)
+        return fail(LCMOE_ERR_INVALID_ARG, "max_prompt and max_batch must be <= 65536");
+    for (int l = 0; l < d->n_layer; l++) {
+        const lcmoe_layer_weights &L = w->layers[l];
+        if (!L.attn_norm || !L.ffn_norm || !L.attn_q || !L.attn_k || !L.attn_v || !L.attn_o)
+            return fail(LCMOE_ERR_INVALID_ARG, "layer %d: an attention tensor or norm is NULL", l);
+    }
+    return LCMOE_OK;
+}
+
+// Rows [q0, q0 + nq) of the batch forward.  nseq sequences starting at seq0
+// take T tokens each from tok (nseq == 1 or T == 1); their last tokens'
+// logits land in m->logits rows 0 .. nseq-1, the greedy ids in m->next
+// (and, with rec, in m->out_tok at column *m->step); the cache lengths
+// advance by T and *m->step by dstep.
+lcmoe_status forward_dev(lcmoe_model *m, int seq0, int nseq, int T, const int32_t *tok, bool rec,
+                         int dstep) {
+    const lcmoe_model_desc &D = m->desc;
+    const int d = D.d_model, H = D.n_head, KVH = D.n_kv_head, hd = D.head_dim, V = D.vocab;
+    const int nq = nseq * T, qt = D.attn_type, nqkv = (H + 2 * KVH) * hd;
+    const int64_t cache_layer = (int64_t)D.max_batch * D.max_ctx * KVH * hd;
+    hipStream_t st = m->stream;
+    HIP_TRY(launch_embed(qt, m->embd, V, d, tok, nq, m->hidden, st));
+    for (int l = 0; l < D.n_layer; l++) {
+        const auto &L = m->layers[l];
+        _Float16 *kc = m->kc + l * cache_layer, *vc = m->vc + l * cache_layer;
+        HIP_TRY(launch_rmsnorm(m->hidden, L.attn_norm, D.norm_eps, nq, d, m->xn, st));
+        HIP_TRY(launch_linear(qt, L.wqkv, nqkv, d, m->xn, d, nq, nullptr, m->qkv, nqkv, st));
+        HIP_TRY(launch_rope_kv(m->qkv, nq, T, seq0, m->lens, H, KVH, hd, m->freq,
+                               D.rope_positions == LCMOE_ROPE_ABSOLUTE, m->qr, kc, vc, D.max_ctx,
+                               st));
+        HIP_TRY(launch_attention(m->qr, nq, T, seq0, m->lens, H, KVH, hd, kc, vc, D.max_ctx,
+                                 m->part, m->attn, st));
+        // hidden += attn W_o (Tensor::add, engine.rs:106)
+        HIP_TRY(launch_linear(qt, L.wo, d, H * hd, m->attn, H * hd, nq, m->hidden, m->hidden, d,
+                              st));
+        // hidden += ffn(rms_norm(hidden)) (engine.rs:109-115)
+        lcmoe_status s = lcmoe_forward_norm_residual_dev(L.moe, m->hidden, nq, m->hidden, st);
+        if (s) return s;
+    }
+    // the final norm and lm_head of each sequence's last token
+    const float *last = m->hidden + (int64_t)(T - 1) * d;  // nseq == 1, or T == 1
+    HIP_TRY(launch_rmsnorm(last, m->out_norm, D.norm_eps, nseq, d, m->xn, st));
+    HIP_TRY(launch_linear(qt, m->out_w, V, d, m->xn, d, nseq, nullptr, m->logits, V, st));
+    HIP_TRY(launch_argmax(m->logits, nseq, V, seq0, m->next, rec ? m->out_tok : nullptr,
+                          D.max_ctx, m->step, st));
+    HIP_TRY(launch_advance(m->lens, seq0, nseq, T, m->step, dstep, st));
+    return LCMOE_OK;
+}
+
+lcmoe_status set_step(lcmoe_model *m, int32_t v) {
+    HIP_TRY(hipMemcpyAsync(m->step, &v, 4, hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    return LCMOE_OK;
+}
+
+lcmoe_status reset(lcmoe_model *m) {
+    std::fill(m->lens_h.begin(), m->lens_h.end(), 0);
+    HIP_TRY(hipMemcpyAsync(m->lens, m->lens_h.data(), 4 * m->lens_h.size(), hipMemcpyHostToDevice,
+                           m->stream));
+    return set_step(m, 0);
+}
+
+}  // namespace
+
+extern "C" lcmoe_status lcmoe_model_create(const lcmoe_model_desc *desc,
+                                           const lcmoe_model_weights *w, lcmoe_model **out) {
+    clear_error();
+    if (!out) return fail(LCMOE_ERR_INVALID_ARG, "out is NULL");
+    *out = nullptr;
+    lcmoe_status st = validate(desc, w);
+    if (st) return st;
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1) {
+        (void)hipGetLastError();
+        return fail(LCMOE_ERR_HIP, "no HIP device available");
+    }
+    lcmoe_model *m = new (std::nothrow) lcmoe_model();
+    if (!m) return fail(LCMOE_ERR_OUT_OF_MEMORY, "host allocation failed");
+    auto bail = [&](lcmoe_status s) {
+        free_model(m);
+        return s;
+    };
+    m->desc = *desc;
+    const lcmoe_model_desc &D = m->desc;
+    if (hipGetDevice(&m->device) != hipSuccess) return bail(fail(LCMOE_ERR_HIP, "hipGetDevice"));
+    if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess)
+        return bail(fail(LCMOE_ERR_HIP, "hipStreamCreate failed"));
+    for (hipEvent_t &e : m->ev)
+        if (hipEventCreate(&e) != hipSuccess) return bail(fail(LCMOE_ERR_HIP, "hipEventCreate"));
+    const int d = D.d_model, H = D.n_head, KVH = D.n_kv_head, hd = D.head_dim, V = D.vocab;
+    const int qt = D.attn_type;
+    m->tmax = std::max(D.max_prompt, D.max_batch);
+    const size_t row_d = lcmoe_tensor_size(qt, d), row_q = lcmoe_tensor_size(qt, (int64_t)H * hd);
+    // per-pair RoPE frequencies, computed as the reference does (f32 powf)
+    std::vector<float> freq(hd / 2);
+    for (int i = 0; i < hd / 2; i++)
+        freq[i] = 1.0f / std::pow(D.rope_theta, 2.0f * (float)i / (float)hd);
+    if ((st = upload(m, &m->freq, freq.data(), 4 * freq.size()))) return bail(st);
+    if ((st = upload(m, &m->embd, w->token_embd, row_d * V))) return bail(st);
+    if ((st = upload(m, &m->out_w, w->output, row_d * V))) return bail(st);
+    if ((st = upload(m, &m->out_norm, w->output_norm, 4 * (size_t)d))) return bail(st);
+    lcmoe_desc md = D.moe;
+    md.max_tokens = m->tmax;
+    m->layers.resize(D.n_layer);
+    for (int l = 0; l < D.n_layer; l++) {
+        const lcmoe_layer_weights &L = w->layers[l];
+        auto &ML = m->layers[l];
+        const size_t bq = row_d * H * hd, bkv = row_d * KVH * hd;
+        if ((st = alloc_n(m, &ML.wqkv, bq + 2 * bkv))) return bail(st);
+        if (hipMemcpy(ML.wqkv, L.attn_q, bq, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(ML.wqkv + bq, L.attn_k, bkv, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(ML.wqkv + bq + bkv, L.attn_v, bkv, hipMemcpyHostToDevice) != hipSuccess)
+            return bail(fail(LCMOE_ERR_HIP, "layer %d: attention upload failed", l));
+        if ((st = upload(m, &ML.wo, L.attn_o, row_q * d))) return bail(st);
+        if ((st = upload(m, &ML.attn_norm, L.attn_norm, 4 * (size_t)d))) return bail(st);
+        if ((st = lcmoe_create(&md, &L.moe, &ML.moe))) return bail(st);
+        if ((st = lcmoe_set_norm(ML.moe, L.ffn_norm, D.norm_eps))) return bail(st);
+    }
+    const int64_t cache = (int64_t)D.n_layer * D.max_batch * D.max_ctx * KVH * hd;
+    const int64_t T = m->tmax;
+    if ((st = alloc_n(m, &m->kc, cache)) || (st = alloc_n(m, &m->vc, cache)) ||
+        (st = alloc_n(m, &m->lens, D.max_batch)) || (st = alloc_n(m, &m->step, 1)) ||
+        (st = alloc_n(m, &m->tok, T)) || (st = alloc_n(m, &m->next, D.max_batch)) ||
+        (st = alloc_n(m, &m->out_tok, (size_t)D.max_batch * D.max_ctx)) ||
+        (st = alloc_n(m, &m->hidden, T * d)) || (st = alloc_n(m, &m->xn, T * d)) ||
+        (st = alloc_n(m, &m->qkv, T * (H + 2 * KVH) * hd)) || (st = alloc_n(m, &m->qr, T * H * hd)) ||
+        (st = alloc_n(m, &m->attn, T * H * hd)) ||
+        (st = alloc_n(m, &m->part, attention_part_floats((int)T, H, hd, D.max_ctx))) ||
+        (st = alloc_n(m, &m->logits, (size_t)D.max_batch * V)))
+        return bail(st);
+    m->lens_h.assign(D.max_batch, 0);
+    if ((st = reset(m))) return bail(st);
+    *out = m;
+    return LCMOE_OK;
+}
+
+extern "C" void lcmoe_model_destroy(lcmoe_model *m) { free_model(m); }
+
+extern "C" lcmoe_status lcmoe_model_reset(lcmoe_model *m) {
+    clear_error();
+    if (!m) return fail(LCMOE_ERR_INVALID_ARG, "model is NULL");
+    HIP_TRY(hipSetDevice(m->device));
+    return reset(m);
+}
+
+extern "C" lcmoe_status lcmoe_model_forward(lcmoe_model *m, const int32_t *tokens, int32_t B,
+                                            int32_t T, float *logits) {
+    clear_error();
+    if (!m || !tokens || !logits) return fail(LCMOE_ERR_INVALID_ARG, "model, tokens or logits is NULL");
+    const lcmoe_model_desc &D = m->desc;
+    if (B < 1 || B > D.max_batch) return fail(LCMOE_ERR_INVALID_ARG, "B=%d outside [1, %d]", B, D.max_batch);
+    if (T < 1 || T > D.max_prompt) return fail(LCMOE_ERR_INVALID_ARG, "T=%d outside [1, %d]", T, D.max_prompt);
+    for (int b = 0; b < B; b++)
+        if (m->lens_h[b] + T > D.max_ctx)
+            return fail(LCMOE_ERR_INVALID_ARG, "sequence %d: %d cached + %d new > max_ctx=%d", b,
+                        m->lens_h[b], T, D.max_ctx);
+    HIP_TRY(hipSetDevice(m->device));
+    lcmoe_status st;
+    if (T == 1) {
+        HIP_TRY(hipMemcpyAsync(m->tok, tokens, 4 * (size_t)B, hipMemcpyHostToDevice, m->stream));
+        if ((st = forward_dev(m, 0, B, 1, m->tok, false, 0))) return st;
+        HIP_TRY(hipMemcpyAsync(logits, m->logits, 4 * (size_t)B * D.vocab, hipMemcpyDeviceToHost,
+                               m->stream));
+    } else {
+        for (int b = 0; b < B; b++) {
+            HIP_TRY(hipMemcpyAsync(m->tok, tokens + (size_t)b * T, 4 * (size_t)T,
+                                   hipMemcpyHostToDevice, m->stream));
+            if ((st = forward_dev(m, b, 1, T, m->tok, false, 0))) return st;
+            HIP_TRY(hipMemcpyAsync(logits + (size_t)b * D.vocab, m->logits, 4 * (size_t)D.vocab,
+                                   hipMemcpyDeviceToHost, m->stream));
+        }
+    }
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    for (int b = 0; b < B; b++) m->lens_h[b] += T;
+    return LCMOE_OK;
+}
+
+extern "C" lcmoe_status lcmoe_model_generate(lcmoe_model *m, const int32_t *prompt, int32_t B,
+                                             int32_t P, int32_t n_new, int32_t eos, int32_t *out,
+                                             int32_t *n_out) {
+    clear_error();
+    if (!m || !prompt || !out) return fail(LCMOE_ERR_INVALID_ARG, "model, prompt or out is NULL");
+    const lcmoe_model_desc &D = m->desc;
+    if (B < 1 || B > D.max_batch) return fail(LCMOE_ERR_INVALID_ARG, "B=%d outside [1, %d]", B, D.max_batch);
+    if (P < 1 || P > D.max_prompt) return fail(LCMOE_ERR_INVALID_ARG, "P=%d outside [1, %d]", P, D.max_prompt);
+    if (n_new < 1 || P + n_new - 1 > D.max_ctx)
+        return fail(LCMOE_ERR_INVALID_ARG, "n_new=%d: need 1 <= n_new and P + n_new - 1 <= max_ctx=%d",
+                    n_new, D.max_ctx);
+    HIP_TRY(hipSetDevice(m->device));
+    lcmoe_status st;
+    if ((st = reset(m))) return st;
+    hipStream_t s = m->stream;
+    HIP_TRY(hipEventRecord(m->ev[0], s));
+    for (int b = 0; b < B; b++) {  // Engine::generate's prefill, one sequence per call
+        HIP_TRY(hipMemcpyAsync(m->tok, prompt + (size_t)b * P, 4 * (size_t)P,
+                               hipMemcpyHostToDevice, s));
+        if ((st = forward_dev(m, b, 1, P, m->tok, true, 0))) return st;
+    }
+    HIP_TRY(hipEventRecord(m->ev[1], s));
+    if (n_new > 1) {
+        int32_t one = 1;
+        HIP_TRY(hipMemcpyAsync(m->step, &one, 4, hipMemcpyHostToDevice, s));
+        if (!m->graph || m->graph_B != B) {
+            if (m->graph) {
+                HIP_TRY(hipGraphExecDestroy(m->graph));
+                m->graph = nullptr;
+            }
+            HIP_TRY(hipStreamSynchronize(s));
+            hipGraph_t g = nullptr;
+            HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+            st = forward_dev(m, 0, B, 1, m->next, true, 1);
+            hipError_t ec = hipStreamEndCapture(s, &g);
+            if (st) {
+                if (g) (void)hipGraphDestroy(g);
+                return st;
+            }
+            if (ec != hipSuccess) return fail(LCMOE_ERR_HIP, "graph capture: %s", hipGetErrorString(ec));
+            ec = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            if (ec != hipSuccess) {
+                m->graph = nullptr;
+                return fail(LCMOE_ERR_HIP, "graph instantiate: %s", hipGetErrorString(ec));
+            }
+            m->graph_B = B;
+        }
+    }
+    HIP_TRY(hipEventRecord(m->ev[2], s));
+    for (int i = 1; i < n_new; i++) HIP_TRY(hipGraphLaunch(m->graph, s));
+    HIP_TRY(hipEventRecord(m->ev[3], s));
+    for (int b = 0; b < B; b++)
+        HIP_TRY(hipMemcpyAsync(out + (size_t)b * n_new, m->out_tok + (size_t)b * D.max_ctx,
+                               4 * (size_t)n_new, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    float a = 0, c = 0;
+    HIP_TRY(hipEventElapsedTime(&a, m->ev[0], m->ev[1]));
+    HIP_TRY(hipEventElapsedTime(&c, m->ev[2], m->ev[3]));
+    m->prefill_ms = a;
+    m->decode_ms = c;
+    for (int b = 0; b < B; b++) {
+        m->lens_h[b] = P + n_new - 1;
+        if (n_out) {
+            int n = n_new;
+            for (int i = 0; i < n_new; i++)
+                if (out[(size_t)b * n_new + i] == eos) {
+                    n = i + 1;
+                    break;
+                }
+            n_out[b] = n;
+        }
+    }
+    return LCMOE_OK;
+}
+
+extern "C" lcmoe_status lcmoe_model_last_timing(lcmoe_model *m, double *prefill_ms,
+                                                double *decode_ms) {
+    clear_error();
+    if (!m) return fail(LCMOE_ERR_INVALID_ARG, "model is NULL");
+    if (prefill_ms) *prefill_ms = m->prefill_ms;
+    if (decode_ms) *decode_ms = m->decode_ms;
+    return LCMOE_OK;
+}

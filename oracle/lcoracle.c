@@ -941,3 +941,89 @@ int lco_shard_matmul(int type, const float *a, const uint8_t *b, float *c, int m
     free(deq);
     return 0;
 }
+
+/* ====================================================================== */
+/* Decoder-layer pieces around the MoE FFN, for the end-to-end engine      */
+/* (rust/src/inference/engine.rs:78-132).  Same arithmetic as the Rust:     */
+/* every a*b+c rounds twice (-ffp-contract=off), f32 libm calls.           */
+/* ====================================================================== */
+
+/* apply_rotary_emb, rust/src/inference/attention.rs:13-34, on x [seq, heads,
+ * hd]: pair (d, d + hd/2) of token i rotates by angle (pos0 + i) * freq_d,
+ * freq_d = 1 / theta^(2d / hd).  The reference passes pos0 = 0 on every
+ * forward (positions restart at each call: a decode token rotates by 0). */
+void lco_rope(float *x, int seq, int heads, int hd, float theta, int pos0) {
+    for (int i = 0; i < seq; i++)
+        for (int h = 0; h < heads; h++)
+            for (int d = 0; d < hd / 2; d++) {
+                float freq = 1.0f / powf(theta, 2.0f * (float)d / (float)hd);
+                float angle = (float)(pos0 + i) * freq;
+                float cos_a = cosf(angle), sin_a = sinf(angle);
+                size_t base = (size_t)i * heads * hd + (size_t)h * hd;
+                float x1 = x[base + d], x2 = x[base + d + hd / 2];
+                x[base + d] = x1 * cos_a - x2 * sin_a;
+                x[base + d + hd / 2] = x1 * sin_a + x2 * cos_a;
+            }
+}
+
+/* The attention core of attention_forward, attention.rs:56-115, for one
+ * forward of seq tokens whose K/V were just appended to a cache of `total`
+ * positions (so cache_len = total - seq came before): q [seq, heads, hd]
+ * after RoPE; k, v [total, kv_heads, hd] the cache decompressed to f32
+ * (cache/mod.rs:66-78); out [seq, heads * hd].  Head h reads kv head
+ * h / (heads / kv_heads).  Score = (sum_d q*k in order) / sqrt(hd), t past
+ * cache_len + s masked to -inf; softmax as max, sum of exp, then
+ * exp / sum; out = sum_t p_t * v_t in order. */
+void lco_attention_core(const float *q, const float *k, const float *v, int seq, int total,
+                        int heads, int kv_heads, int hd, float *out) {
+    const int groups = heads / kv_heads, cache_len = total - seq;
+    float *scores = (float *)malloc(sizeof(float) * (size_t)(total > 0 ? total : 1));
+    const float sq = sqrtf((float)hd);
+    for (int h = 0; h < heads; h++) {
+        const int kvh = h / groups;
+        for (int s = 0; s < seq; s++) {
+            for (int t = 0; t < total; t++) {
+                if (t > cache_len + s) {
+                    scores[t] = -INFINITY;
+                } else {
+                    float dot = 0.0f;
+                    for (int d = 0; d < hd; d++) {
+                        float p = q[(size_t)s * heads * hd + (size_t)h * hd + d] *
+                                  k[(size_t)t * kv_heads * hd + (size_t)kvh * hd + d];
+                        dot = dot + p;
+                    }
+                    scores[t] = dot / sq;
+                }
+            }
+            float mx = -INFINITY;
+            for (int t = 0; t < total; t++) mx = rust_fmax(mx, scores[t]);
+            float sum = 0.0f;
+            for (int t = 0; t < total; t++) sum = sum + expf(scores[t] - mx);
+            for (int t = 0; t < total; t++) scores[t] = expf(scores[t] - mx) / sum;
+            for (int d = 0; d < hd; d++) {
+                float acc = 0.0f;
+                for (int t = 0; t < total; t++) {
+                    float p = scores[t] * v[(size_t)t * kv_heads * hd + (size_t)kvh * hd + d];
+                    acc = acc + p;
+                }
+                out[(size_t)s * heads * hd + (size_t)h * hd + d] = acc;
+            }
+        }
+    }
+    free(scores);
+}
+
+/* Greedy sampling, sample_top_p with temperature <= 0
+ * (rust/src/inference/sampler.rs:8-10): Iterator::max_by over f32::total_cmp,
+ * which keeps the LAST of equal maxima; total order -NaN < -inf < ... < -0 <
+ * +0 < ... < +inf < +NaN.  Returns 0 for n == 0 (unwrap_or(0)). */
+int lco_argmax_last(const float *x, int n) {
+    int best = -1;
+    int32_t bk = 0;
+    for (int i = 0; i < n; i++) {
+        int32_t b = (int32_t)f2u(x[i]);
+        b ^= (int32_t)(((uint32_t)(b >> 31)) >> 1);
+        if (best < 0 || b >= bk) { best = i; bk = b; }
+    }
+    return best < 0 ? 0 : best;
+}

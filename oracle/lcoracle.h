@@ -42,6 +42,12 @@
  *                          ffn_forward (engine.rs:146-164) bit for bit;
  *                          all-zero experts -> 0; duplicated experts additive;
  *                          routed_scale exact; shared expert adds its FFN
+ *   rope / attention /   : tests/test_oracle_engine.py -- position 0 is the
+ *   argmax                 identity, pair norms kept, angles vs float64,
+ *                          the reference's per-call positions; attention vs a
+ *                          float64 restatement, one key -> its value, causal
+ *                          mask; argmax KAT sampler.rs:57-61, last of ties,
+ *                          total order over +-0 / NaN
  *   golden fixtures      : tests/golden/moe_*.npz (written by
  *                          tests/golden/make_golden.py) reproduced bit for bit
  *                          and checked against the float64 recomputation
@@ -155,6 +161,17 @@ void lco_ffn_dense(const float *x, int m, int d, int F, const float *wg_t,
 void *lco_resident_create(const lco_desc *desc, const lco_weights *w, int threads);
 int lco_resident_forward(void *h, const float *x, int T, float *y, int threads);
 void lco_resident_destroy(void *h);
+
+/* ---- decoder-layer pieces (end-to-end engine, engine.rs:78-132) --------- */
+/* apply_rotary_emb (attention.rs:13-34) with positions pos0 + i (the
+ * reference: pos0 = 0 on every call). */
+void lco_rope(float *x, int seq, int heads, int hd, float theta, int pos0);
+/* attention_forward's core (attention.rs:56-115) over a cache of `total`
+ * positions whose last `seq` are this call's tokens. */
+void lco_attention_core(const float *q, const float *k, const float *v, int seq, int total,
+                        int heads, int kv_heads, int hd, float *out);
+/* greedy sample_top_p (sampler.rs:8-10): max_by(total_cmp), last maximum */
+int lco_argmax_last(const float *x, int n);
 
 #ifdef __cplusplus
 }

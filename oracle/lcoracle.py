@@ -87,6 +87,9 @@ def lib() -> C.CDLL:
             "lco_resident_create": (vp, [C.POINTER(Desc), C.POINTER(Weights), i32]),
             "lco_resident_forward": (i32, [vp, vp, i32, vp, i32]),
             "lco_resident_destroy": (None, [vp]),
+            "lco_rope": (None, [vp, i32, i32, i32, f32, i32]),
+            "lco_attention_core": (None, [vp, vp, vp, i32, i32, i32, i32, i32, vp]),
+            "lco_argmax_last": (i32, [vp, i32]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -329,3 +332,30 @@ def shard_matmul(qtype: int, a: np.ndarray, b: np.ndarray, k: int, n: int) -> np
     if lib().lco_shard_matmul(qtype, _p(a), _p(b), _p(out), m, k, n) != 0:
         raise ValueError("lco_shard_matmul: bad type or shape")
     return out
+
+
+# ---- decoder-layer pieces ------------------------------------------------------
+
+def rope(x: np.ndarray, heads: int, hd: int, theta: float, pos0: int = 0) -> np.ndarray:
+    """apply_rotary_emb (attention.rs:13-34) on x [seq, heads * hd]; returns a copy."""
+    y = np.ascontiguousarray(x, np.float32).copy()
+    lib().lco_rope(_p(y), y.shape[0], heads, hd, theta, pos0)
+    return y
+
+
+def attention_core(q, k, v, heads: int, kv_heads: int, hd: int) -> np.ndarray:
+    """attention_forward's core (attention.rs:56-115): q [seq, heads*hd] after
+    RoPE, k / v [total, kv_heads*hd] the decompressed cache."""
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    seq, total = q.shape[0], k.shape[0]
+    out = np.empty((seq, heads * hd), np.float32)
+    lib().lco_attention_core(_p(q), _p(k), _p(v), seq, total, heads, kv_heads, hd, _p(out))
+    return out
+
+
+def argmax_last(x: np.ndarray) -> int:
+    """Greedy sample_top_p (sampler.rs:8-10): the last maximum under total_cmp."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    return int(lib().lco_argmax_last(_p(x), x.size))

@@ -182,3 +182,28 @@ def test_shard_matmul_split_argument_errors():
     assert lib.lcmoe_shard_matmul_split_dev(8, *args, 0, None, None) == 1    # k_split < 1
     assert lib.lcmoe_shard_matmul_split_dev(8, *args, 65, None, None) == 1   # k_split > 64
     assert lib.lcmoe_shard_matmul_split_dev(8, *args, 4, None, None) == 1    # no workspace
+
+
+def test_model_create_rejects_bad_desc_before_device_work():
+    """lcmoe_model_create validates the descriptor and the tensor pointers
+    first: each case fails the same way with or without a GPU."""
+    from leafcutterllm_amd.configs import ModelConfig, small_config, synth_model
+    from leafcutterllm_amd.model import Model
+
+    mc = ModelConfig("tiny", 1, 4, 2, 64, 32, 10000.0,
+                     small_config("m", 256, 256, 8, 2, L.ROUTE_SOFTMAX, L.TYPE_Q4_K, L.TYPE_Q4_K))
+    w = synth_model(mc, seed=1)
+    cases = [("n_kv_head", 3, "LCMOE_ERR_INVALID_ARG"), ("head_dim", 12, "LCMOE_ERR_INVALID_ARG"),
+             ("attn_type", L.TYPE_Q6_K, "LCMOE_ERR_UNSUPPORTED"), ("d_model", 512, "LCMOE_ERR_INVALID_ARG"),
+             ("max_prompt", 100, "LCMOE_ERR_INVALID_ARG"), ("rope_positions", 2, "LCMOE_ERR_INVALID_ARG"),
+             ("max_batch", 0, "LCMOE_ERR_INVALID_ARG")]
+    for field, value, status in cases:
+        d = mc.desc(2, 16, 32)
+        setattr(d, field, value)
+        with pytest.raises(L.LcmoeError) as e:
+            Model(d, w)
+        assert _lib.STATUS[e.value.status] == status, field
+    w2 = dict(w, layers=[dict(w["layers"][0], attn_v=None)])
+    with pytest.raises(L.LcmoeError) as e:
+        Model(mc.desc(2, 16, 32), w2)
+    assert _lib.STATUS[e.value.status] == "LCMOE_ERR_INVALID_ARG"
