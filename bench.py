@@ -213,6 +213,8 @@ def e2e_bench(args) -> None:
     per = {}
     with L.Model(mc.desc(max(batches), P, P + n_new), w) as m:
         del w
+        if args.no_graph:
+            m.set_decode_graph(False)
         for B in batches:
             prompts = rng.integers(0, mc.vocab, (B, P)).astype(np.int32)
             m.generate(prompts, 8)
@@ -287,6 +289,11 @@ def main():
                     help="with --shard-matmul: time lcmoe_shard_matmul_split_dev with S k-slices")
     ap.add_argument("--e2e-batches", default="1,16",
                     help="with --config 5: batch sizes of the end-to-end decode")
+    ap.add_argument("--layer", action="store_true",
+                    help="with --config 5: time the MoE layer alone instead of the whole decoder")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="with --config 5: eager decode launches instead of the captured graph "
+                         "(for profilers that cannot trace graph launches)")
     args = ap.parse_args()
 
     if args.copy_probe:
@@ -296,7 +303,7 @@ def main():
         shard_matmul_bench(args)
         return
 
-    if args.config == 5 and args.gpus == 1:
+    if args.config == 5 and args.gpus == 1 and not args.layer:
         e2e_bench(args)
         return
 

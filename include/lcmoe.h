@@ -332,6 +332,11 @@ lcmoe_status lcmoe_model_forward(lcmoe_model *m, const int32_t *tokens, int32_t 
  * to never stop).  P + n_new - 1 <= max_ctx. */
 lcmoe_status lcmoe_model_generate(lcmoe_model *m, const int32_t *prompt, int32_t B, int32_t P,
                                   int32_t n_new, int32_t eos, int32_t *out, int32_t *n_out);
+/* Decode steps of lcmoe_model_generate as one captured HIP graph (enable =
+ * 1, the default) or as eager launches (0: for callers that capture the
+ * call into a graph of their own, and for tools that cannot trace
+ * graph-launched kernels).  Results are identical either way. */
+lcmoe_status lcmoe_model_set_decode_graph(lcmoe_model *m, int32_t enable);
 /* Device time of the last lcmoe_model_generate: prefill (all sequences)
  * and decode (all steps), milliseconds, from HIP events on its stream. */
 lcmoe_status lcmoe_model_last_timing(lcmoe_model *m, double *prefill_ms, double *decode_ms);

@@ -35,7 +35,7 @@ EXPORTS = (
     "lcmoe_shard_matmul_dev", "lcmoe_shard_matmul_split_dev",
     "lcmoe_shard_matmul_split_noalloc_dev", "lcmoe_model_create", "lcmoe_model_destroy",
     "lcmoe_model_reset", "lcmoe_model_forward", "lcmoe_model_generate",
-    "lcmoe_model_last_timing",
+    "lcmoe_model_last_timing", "lcmoe_model_set_decode_graph",
 )
 
 

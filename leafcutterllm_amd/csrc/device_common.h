@@ -169,6 +169,82 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// f64 move across lanes by DPP (both 32-bit halves); lanes whose source is
+// outside the pattern, or whose row the mask leaves out, read +0
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), CTRL, ROW_MASK, 0xf, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), CTRL, ROW_MASK, 0xf, true);
+    return __hiloint2double(hi, lo);
+}
+
+// inclusive prefix sum over the 64 lanes (row shifts 1, 2, 4, 8 inside each
+// row of 16, then row broadcasts 15 and 31 across rows): register moves only,
+// no LDS round trips
+__device__ __forceinline__ double wave_incl_scan_f64(double v) {
+    v += dpp_f64<0x111, 0xf>(v);  // row_shr:1
+    v += dpp_f64<0x112, 0xf>(v);  // row_shr:2
+    v += dpp_f64<0x114, 0xf>(v);  // row_shr:4
+    v += dpp_f64<0x118, 0xf>(v);  // row_shr:8
+    v += dpp_f64<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_f64<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+    const int lo = __builtin_amdgcn_readlane(__double2loint(v), lane);
+    const int hi = __builtin_amdgcn_readlane(__double2hiint(v), lane);
+    return __hiloint2double(hi, lo);
+}
+
+// the sum over the 64 lanes, in every lane
+__device__ __forceinline__ double wave_total_f64(double v) {
+    return readlane_f64(wave_incl_scan_f64(v), 63);
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, true);
+}
+
+// the maximum over the 64 lanes, in every lane (0 is the identity); the same
+// row-shift / row-broadcast pattern as wave_incl_scan_f64
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_u32<0x111, 0xf>(v));
+    v = max(v, dpp_u32<0x112, 0xf>(v));
+    v = max(v, dpp_u32<0x114, 0xf>(v));
+    v = max(v, dpp_u32<0x118, 0xf>(v));
+    v = max(v, dpp_u32<0x142, 0xa>(v));
+    v = max(v, dpp_u32<0x143, 0xc>(v));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t max_dpp_u64(uint64_t v) {
+    const uint64_t o = ((uint64_t)dpp_u32<CTRL, ROW_MASK>((uint32_t)(v >> 32)) << 32) |
+                       dpp_u32<CTRL, ROW_MASK>((uint32_t)v);
+    return o > v ? o : v;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    v = max_dpp_u64<0x111, 0xf>(v);
+    v = max_dpp_u64<0x112, 0xf>(v);
+    v = max_dpp_u64<0x114, 0xf>(v);
+    v = max_dpp_u64<0x118, 0xf>(v);
+    v = max_dpp_u64<0x142, 0xa>(v);
+    v = max_dpp_u64<0x143, 0xc>(v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), 63);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// order-preserving unsigned encoding of a non-NaN float, -0 and +0 equal:
+// a < b  <=>  ord_key(a) < ord_key(b); every value encodes above 0
+__device__ __forceinline__ uint32_t ord_key(float f) {
+    const uint32_t u = __float_as_uint(f == 0.0f ? 0.0f : f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
 // Which expert a block of an expert-product launch serves.  Routed launch:
 // slot i < nr serves touched[i] (nothing when i >= number touched) over
 // positions p in [offsets[e], offsets[e] + counts[e]) whose token is

@@ -30,12 +30,6 @@ __device__ __forceinline__ void dec8(const uint8_t *row, int64_t k, float (&w)[8
     Dec<QT>::run(row, k, w);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
@@ -108,57 +102,125 @@ __global__ __launch_bounds__(256) void k_linear(const uint8_t *__restrict__ W, i
     }
 }
 
+// k_linear for Q4_K weights (K a multiple of 256): lane l takes sub-block
+// l % 8 of super-blocks l / 8, l / 8 + 8, ...; per sub-block it loads the
+// super-block header and its pair's 32 quant bytes (three 16-byte loads) and
+// adds (d sc) sum_k x q - (dmin m) sum_k x per token, the decoder's two terms
+// (rust/src/kernels/mod.rs:66-98) factored out of the sum.
+template <int TC>
+__global__ __launch_bounds__(256) void k_linear_q4k(const uint8_t *__restrict__ W,
+                                                    int64_t row_bytes, int N, int K,
+                                                    const float *__restrict__ X, int64_t ldx,
+                                                    int T, const float *R, float *Y, int64_t ldy) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n = blockIdx.x * 4 + wave;
+    if (n >= N) return;
+    const int t0 = blockIdx.y * TC, nt = min(TC, T - t0);
+    const uint8_t *wr = W + (int64_t)n * row_bytes;
+    const int j = lane & 7, nsb = K >> 8, sh = 4 * (j & 1);
+    float acc[TC];
+#pragma unroll
+    for (int t = 0; t < TC; t++) acc[t] = 0.0f;
+    for (int sb = lane >> 3; sb < nsb; sb += 8) {
+        const uint8_t *blk = wr + (int64_t)sb * 144;
+        const uint4 hdr = *reinterpret_cast<const uint4 *>(blk);
+        const uint4 *qp = reinterpret_cast<const uint4 *>(blk + 16 + 32 * (j >> 1));
+        const uint4 qa = qp[0], qb = qp[1];
+        // get_scale_min_k4 (kernels/mod.rs:54-63) from the header words:
+        // scale bytes 0-3 in hdr.y, 4-7 in hdr.z, 8-11 in hdr.w
+        const int jb = 8 * (j & 3);
+        const uint32_t by = (hdr.y >> jb) & 0xff, bz = (hdr.z >> jb) & 0xff, bw = (hdr.w >> jb) & 0xff;
+        const int sc = j < 4 ? (int)(by & 63) : (int)((bw & 15) | ((by >> 6) << 4));
+        const int mn = j < 4 ? (int)(bz & 63) : (int)((bw >> 4) | ((bz >> 6) << 4));
+        const float dl = dh2f(hdr.x & 0xffff) * (float)sc, ml = dh2f(hdr.x >> 16) * (float)mn;
+        const uint32_t qw[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        const int64_t k0 = (int64_t)sb * 256 + 32 * j;
+#pragma unroll
+        for (int t = 0; t < TC; t++) {
+            if (t < nt) {
+                const float4 *xp = reinterpret_cast<const float4 *>(X + (int64_t)(t0 + t) * ldx + k0);
+                float sq = 0.0f, sx = 0.0f;
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const float4 a = xp[u];
+                    const uint32_t w = qw[u] >> sh;
+                    sq = __builtin_fmaf(a.x, (float)(w & 15), sq);
+                    sq = __builtin_fmaf(a.y, (float)((w >> 8) & 15), sq);
+                    sq = __builtin_fmaf(a.z, (float)((w >> 16) & 15), sq);
+                    sq = __builtin_fmaf(a.w, (float)((w >> 24) & 15), sq);
+                    sx = sx + a.x + a.y + a.z + a.w;
+                }
+                acc[t] = __builtin_fmaf(dl, sq, __builtin_fmaf(-ml, sx, acc[t]));
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < TC; t++) {
+        const float s = wave_sum(acc[t]);
+        if (lane == 0 && t < nt) {
+            const int64_t o = (int64_t)(t0 + t) * ldy + n;
+            Y[o] = R ? R[o] + s : s;
+        }
+    }
+}
+
 // q rows [nq][H*hd] (rotated) and the cache rows of this call's tokens from
 // the projections qkv [nq][(H + 2 KVH) hd] (q, then k, then v).  Query q is
 // token i = q % T of sequence b = seq0 + q / T; it lands at cache position
 // lens[b] + i and rotates by position i (per-call positions, as the
 // reference) or lens[b] + i (absolute).  freq[d] = 1 / theta^(2d/hd) comes
-// from the host.
-__global__ __launch_bounds__(256) void k_rope_kv(const float *__restrict__ qkv, int nq, int T,
+// from the host.  Block (q, head): heads [0, H) rotate q, [H, H + KVH)
+// rotate k into the cache, [H + KVH, H + 2 KVH) copy v into it.
+__global__ __launch_bounds__(128) void k_rope_kv(const float *__restrict__ qkv, int nq, int T,
                                                  int seq0, const int32_t *__restrict__ lens, int H,
                                                  int KVH, int hd, const float *__restrict__ freq,
                                                  int absolute, float *__restrict__ qo,
                                                  _Float16 *__restrict__ kc,
                                                  _Float16 *__restrict__ vc, int ctx) {
-    const int q = blockIdx.x;
+    const int q = blockIdx.x, hh = blockIdx.y;
     if (q >= nq) return;
     const int b = seq0 + q / T, i = q % T;
     const int pos = lens[b] + i;
-    const float fp = (float)(absolute ? pos : i);
     const int half = hd / 2, ldq = (H + 2 * KVH) * hd;
-    const float *src = qkv + (int64_t)q * ldq;
+    const float *src = qkv + (int64_t)q * ldq + (int64_t)hh * hd;
     const int64_t crow = ((int64_t)b * ctx + pos) * KVH * hd;
-    // q heads then k heads: one (head, d < hd/2) pair per thread step
-    for (int p = threadIdx.x; p < (H + KVH) * half; p += blockDim.x) {
-        const int hh = p / half, d = p % half;
+    if (hh >= H + KVH) {  // v
+        _Float16 *dst = vc + crow + (int64_t)(hh - H - KVH) * hd;
+        for (int e = threadIdx.x; e < hd; e += blockDim.x) dst[e] = (_Float16)src[e];
+        return;
+    }
+    const float fp = (float)(absolute ? pos : i);
+    for (int d = threadIdx.x; d < half; d += blockDim.x) {
         const float angle = fp * freq[d];
         const float c = cosf(angle), s = sinf(angle);
-        const float x1 = src[hh * hd + d], x2 = src[hh * hd + d + half];
+        const float x1 = src[d], x2 = src[d + half];
         const float y1 = x1 * c - x2 * s, y2 = x1 * s + x2 * c;
         if (hh < H) {
-            qo[(int64_t)q * H * hd + hh * hd + d] = y1;
-            qo[(int64_t)q * H * hd + hh * hd + d + half] = y2;
+            float *dst = qo + (int64_t)q * H * hd + (int64_t)hh * hd;
+            dst[d] = y1;
+            dst[d + half] = y2;
         } else {
-            const int kh = hh - H;
-            kc[crow + kh * hd + d] = (_Float16)y1;
-            kc[crow + kh * hd + d + half] = (_Float16)y2;
+            _Float16 *dst = kc + crow + (int64_t)(hh - H) * hd;
+            dst[d] = (_Float16)y1;
+            dst[d + half] = (_Float16)y2;
         }
     }
-    for (int e = threadIdx.x; e < KVH * hd; e += blockDim.x)
-        vc[crow + e] = (_Float16)src[(H + KVH) * hd + e];
 }
 
 // One 128-position chunk c of the context of query q, head h: the chunk's
 // max score m, sum of exp(score - m) l, and sum of exp(score - m) v (hd
 // values).  Query q (token i of sequence b) sees positions [0, lens[b] + i].
-// One wave; lane j owns positions c*128 + j and c*128 + 64 + j.
-__global__ __launch_bounds__(64) void k_attn_part(const float *__restrict__ qr, int nq, int T,
-                                                  int seq0, const int32_t *__restrict__ lens,
-                                                  int H, int KVH, int hd,
-                                                  const _Float16 *__restrict__ kc,
-                                                  const _Float16 *__restrict__ vc, int ctx,
-                                                  int chunks, float *__restrict__ part) {
-    const int q = blockIdx.x, h = blockIdx.y, c = blockIdx.z, lane = threadIdx.x;
+// 256 threads: scores by two threads per position (half the dims each),
+// then the weighted sum of v by 256 / hd groups of hd threads over
+// interleaved positions, added in LDS.
+__global__ __launch_bounds__(256) void k_attn_part(const float *__restrict__ qr, int nq, int T,
+                                                   int seq0, const int32_t *__restrict__ lens,
+                                                   int H, int KVH, int hd,
+                                                   const _Float16 *__restrict__ kc,
+                                                   const _Float16 *__restrict__ vc, int ctx,
+                                                   int chunks, float *__restrict__ part) {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    const int q = blockIdx.x, h = blockIdx.y, c = blockIdx.z, t = threadIdx.x;
     if (q >= nq) return;
     const int b = seq0 + q / T, i = q % T;
     const int L = lens[b] + i + 1;  // visible positions
@@ -166,53 +228,89 @@ __global__ __launch_bounds__(64) void k_attn_part(const float *__restrict__ qr, 
     float *out = part + (((int64_t)q * H + h) * chunks + c) * (hd + 2);
     const int p0 = c * kAttnChunk;
     if (p0 >= L) {
-        for (int d = lane; d < hd; d += 64) out[d] = 0.0f;
-        if (lane == 0) {
+        for (int d = t; d < hd; d += blockDim.x) out[d] = 0.0f;
+        if (t == 0) {
             out[hd] = -INFINITY;
             out[hd + 1] = 0.0f;
         }
         return;
     }
+    const int np = min(kAttnChunk, L - p0);
     __shared__ float s_q[256];
+    __shared__ float s_half[kAttnChunk];
     __shared__ float s_p[kAttnChunk];
-    for (int d = lane; d < hd; d += 64) s_q[d] = qr[(int64_t)q * H * hd + h * hd + d];
+    __shared__ float s_red[8];
+    __shared__ float s_acc[2048];
+    for (int d = t; d < hd; d += blockDim.x) s_q[d] = qr[(int64_t)q * H * hd + h * hd + d];
     __syncthreads();
-    const float sq = sqrtf((float)hd);
-    float sc[2];
+    const int64_t pstride = (int64_t)KVH * hd;  // elements between positions
+    // scores: position p0 + (t % 128), dims [half * hd/2, half * hd/2 + hd/2);
+    // the row's loads are all issued before the products
+    const int key = t & (kAttnChunk - 1), hf = t >> 7, hd2 = hd / 2;
+    float dot = 0.0f;
+    if (key < np) {
+        const _Float16 *kr = kc + ((int64_t)b * ctx + p0 + key) * pstride + kvh * hd + hf * hd2;
+        h8 kv[16];
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
-        const int pos = p0 + 64 * u + lane;
-        sc[u] = -INFINITY;
-        if (pos < L) {
-            const _Float16 *kr = kc + (((int64_t)b * ctx + pos) * KVH + kvh) * hd;
-            float dot = 0.0f;
-            for (int d = 0; d < hd; d += 8) {
-                typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-                const h8 kv = *reinterpret_cast<const h8 *>(kr + d);
+        for (int u = 0; u < 16; u++)
+            if (8 * u < hd2) kv[u] = *reinterpret_cast<const h8 *>(kr + 8 * u);
 #pragma unroll
-                for (int e = 0; e < 8; e++) dot = __builtin_fmaf(s_q[d + e], (float)kv[e], dot);
+        for (int u = 0; u < 16; u++)
+            if (8 * u < hd2) {
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    dot = __builtin_fmaf(s_q[hf * hd2 + 8 * u + e], (float)kv[u][e], dot);
             }
-            sc[u] = dot / sq;
+    }
+    if (hf) s_half[key] = dot;
+    __syncthreads();
+    float sc = -INFINITY;
+    if (!hf && key < np) sc = (dot + s_half[key]) / sqrtf((float)hd);
+    // block max and sum over the chunk's positions (threads 0-127)
+    float m = wave_max(sc);
+    if ((t & 63) == 0) s_red[t >> 6] = m;
+    __syncthreads();
+    m = fmaxf(s_red[0], s_red[1]);
+    const float p = (!hf && key < np) ? expf(sc - m) : 0.0f;
+    if (!hf) s_p[key] = p;
+    float l = wave_sum(p);
+    __syncthreads();
+    if ((t & 63) == 0) s_red[4 + (t >> 6)] = l;
+    __syncthreads();
+    l = s_red[4] + s_red[5];
+    // weighted sum of v: thread (position group kg, dims 8 dg .. 8 dg + 7)
+    // over positions kg, kg + KG, ... (one 16-byte load each, all issued
+    // first), then the KG groups added in LDS
+    const int DG = hd / 8, KG = 256 / DG, dg = t % DG, kg = t / DG;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (kg < KG) {
+        const _Float16 *vr = vc + ((int64_t)b * ctx + p0) * pstride + kvh * hd + 8 * dg;
+        for (int k0 = kg; k0 < np; k0 += 8 * KG) {
+            h8 vv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (k0 + u * KG < np) vv[u] = *reinterpret_cast<const h8 *>(vr + (k0 + u * KG) * pstride);
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (k0 + u * KG < np) {
+                    const float pk = s_p[k0 + u * KG];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc[e] = __builtin_fmaf(pk, (float)vv[u][e], acc[e]);
+                }
         }
     }
-    const float m = wave_max(fmaxf(sc[0], sc[1]));
-    float p[2];
+    float *s_o = s_acc;  // [KG][hd] partial sums, KG * hd <= 2048
+    if (kg < KG) {
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
-        p[u] = sc[u] == -INFINITY ? 0.0f : expf(sc[u] - m);
-        s_p[64 * u + lane] = p[u];
+        for (int e = 0; e < 8; e++) s_o[kg * hd + 8 * dg + e] = acc[e];
     }
-    const float l = wave_sum(p[0] + p[1]);
     __syncthreads();
-    const int np = min(kAttnChunk, L - p0);
-    for (int d = lane; d < hd; d += 64) {
-        float acc = 0.0f;
-        const _Float16 *vr = vc + (((int64_t)b * ctx + p0) * KVH + kvh) * hd + d;
-        for (int t = 0; t < np; t++)
-            acc = __builtin_fmaf(s_p[t], (float)vr[(int64_t)t * KVH * hd], acc);
-        out[d] = acc;
+    if (t < hd) {
+        float o = 0.0f;
+        for (int j = 0; j < KG; j++) o += s_o[j * hd + t];
+        out[t] = o;
     }
-    if (lane == 0) {
+    if (t == 0) {
         out[hd] = m;
         out[hd + 1] = l;
     }
@@ -335,7 +433,15 @@ hipError_t launch_linear(int qt, const uint8_t *W, int N, int K, const float *X,
     if (T <= 0 || N <= 0) return hipSuccess;
     const int64_t rb = (int64_t)lcmoe_tensor_size(qt, K);
     switch (qt) {
-    case LCMOE_TYPE_Q4_K: linear_tc<LCMOE_TYPE_Q4_K>(W, rb, N, K, X, ldx, T, R, Y, ldy, st); break;
+    case LCMOE_TYPE_Q4_K:
+        // one token: the Q4_K sub-block kernel; batches: the generic kernel,
+        // whose x reads span fewer cache lines per load (measured faster)
+        if (T <= 1)
+            hipLaunchKernelGGL(k_linear_q4k<1>, dim3((N + 3) / 4, 1), dim3(256), 0, st, W, rb, N, K,
+                               X, ldx, T, R, Y, ldy);
+        else
+            linear_tc<LCMOE_TYPE_Q4_K>(W, rb, N, K, X, ldx, T, R, Y, ldy, st);
+        break;
     case LCMOE_TYPE_Q8_0: linear_tc<LCMOE_TYPE_Q8_0>(W, rb, N, K, X, ldx, T, R, Y, ldy, st); break;
     default: linear_tc<LCMOE_TYPE_F32>(W, rb, N, K, X, ldx, T, R, Y, ldy, st);
     }
@@ -346,8 +452,8 @@ hipError_t launch_rope_kv(const float *qkv, int nq, int T, int seq0, const int32
                           int KVH, int hd, const float *freq, int absolute, float *qo,
                           _Float16 *kc, _Float16 *vc, int ctx, hipStream_t st) {
     if (nq <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_rope_kv, dim3(nq), dim3(256), 0, st, qkv, nq, T, seq0, lens, H, KVH, hd,
-                       freq, absolute, qo, kc, vc, ctx);
+    hipLaunchKernelGGL(k_rope_kv, dim3(nq, H + 2 * KVH), dim3(128), 0, st, qkv, nq, T, seq0, lens,
+                       H, KVH, hd, freq, absolute, qo, kc, vc, ctx);
     return hipGetLastError();
 }
 
@@ -356,8 +462,8 @@ hipError_t launch_attention(const float *qr, int nq, int T, int seq0, const int3
                             float *part, float *out, hipStream_t st) {
     if (nq <= 0) return hipSuccess;
     const int chunks = (ctx + kAttnChunk - 1) / kAttnChunk;
-    hipLaunchKernelGGL(k_attn_part, dim3(nq, H, chunks), dim3(64), 0, st, qr, nq, T, seq0, lens, H,
-                       KVH, hd, kc, vc, ctx, chunks, part);
+    hipLaunchKernelGGL(k_attn_part, dim3(nq, H, chunks), dim3(256), 0, st, qr, nq, T, seq0, lens,
+                       H, KVH, hd, kc, vc, ctx, chunks, part);
     hipLaunchKernelGGL(k_attn_combine, dim3(nq, H), dim3(128), 0, st, part, nq, H, hd, chunks, out);
     return hipGetLastError();
 }

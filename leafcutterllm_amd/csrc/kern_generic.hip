@@ -136,29 +136,35 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ Yr, i
                                                  int d, CombineRoute cr, const float *resid,
                                                  float *y) {
     __shared__ float s_w[kMaxK];
+    __shared__ float s_z[kMaxE];
     const int t = blockIdx.y, c4 = blockIdx.x * blockDim.x + threadIdx.x;
     if (cr.logits) {
+        // the scores (logit + bias) of the softmax's items (the K selected
+        // for the renormalised router, all E otherwise) and their exps are
+        // formed in parallel; thread 0 then sums the exps in item order, the
+        // sequential sum of CpuBackend::softmax
+        const float *l = cr.logits + (int64_t)t * cr.E;
+        const int32_t *sel = cr.topk_idx + (int64_t)t * K;
+        const bool renorm = cr.kind == LCMOE_ROUTE_SOFTMAX_RENORM;
+        const int n = renorm ? K : cr.E;
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            const int e = renorm ? sel[i] : i;
+            s_z[i] = cr.bias ? l[e] + cr.bias[e] : l[e];
+        }
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            float mx = -__builtin_inff();
+            for (int i = threadIdx.x; i < n; i += 64) mx = nan_max(mx, s_z[i]);
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) mx = nan_max(mx, __shfl_xor(mx, o, 64));
+            for (int i = threadIdx.x; i < n; i += 64) s_z[i] = expf(s_z[i] - mx);
+        }
+        __syncthreads();
         if (threadIdx.x == 0) {
-            const float *l = cr.logits + (int64_t)t * cr.E;
-            const int32_t *sel = cr.topk_idx + (int64_t)t * K;
-            float mx = -__builtin_inff(), sum = 0.0f;
-            if (cr.kind == LCMOE_ROUTE_SOFTMAX_RENORM) {  // softmax over the K selected
-                for (int k = 0; k < K; k++) {
-                    const int e = sel[k];
-                    mx = nan_max(mx, cr.bias ? l[e] + cr.bias[e] : l[e]);
-                }
-                for (int k = 0; k < K; k++) {
-                    const int e = sel[k];
-                    sum = sum + expf((cr.bias ? l[e] + cr.bias[e] : l[e]) - mx);
-                }
-            } else {  // full-E softmax probabilities of the selected experts
-                for (int e = 0; e < cr.E; e++) mx = nan_max(mx, cr.bias ? l[e] + cr.bias[e] : l[e]);
-                for (int e = 0; e < cr.E; e++)
-                    sum = sum + expf((cr.bias ? l[e] + cr.bias[e] : l[e]) - mx);
-            }
+            float sum = 0.0f;
+            for (int i = 0; i < n; i++) sum = sum + s_z[i];
             for (int k = 0; k < K; k++) {
-                const int e = sel[k];
-                const float w = (expf((cr.bias ? l[e] + cr.bias[e] : l[e]) - mx) / sum) * cr.scale;
+                const float w = (s_z[renorm ? k : sel[k]] / sum) * cr.scale;
                 s_w[k] = w;
                 if (blockIdx.x == 0) topk_w[(int64_t)t * K + k] = w;
             }

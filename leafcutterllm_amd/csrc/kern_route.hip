@@ -637,39 +637,39 @@ __device__ __forceinline__ void logit_bounds(const RouterArgs &a, LogitRegs<NC4>
     constexpr int W = kFastThreads / 64;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int d = a.d, E = a.E, E8 = E & ~7;
+    // up to d = 2048 the next expert's chunk loads while this one is summed
+    // (a second register set; at larger d it would spill)
+    constexpr bool kAhead = NC4 <= 8;
     for (int e = wave; e < E; e += W) {
-        if (e != wave) load_wchunk<NC4>(a, e, R.wv);
-        double l2[2] = {0.0, 0.0}, ab2[2] = {0.0, 0.0};
+        f32x4 wn[kAhead ? NC4 : 1];
+        const bool more = kAhead && e + W < E;
+        if constexpr (kAhead) {
+            if (more) load_wchunk<NC4>(a, e + W, wn);
+        } else {
+            if (e != wave) load_wchunk<NC4>(a, e, R.wv);
+        }
+        double l2[2] = {0.0, 0.0}, ab2[2] = {0.0, 0.0}, qg[NC4];
 #pragma unroll
         for (int g = 0; g < NC4; g++) {  // products are exact in float64
             const f32x4 x = *reinterpret_cast<const f32x4 *>(R.xs + 4 * g), w = R.wv[g];
             const double p0 = (double)x.x * (double)w.x, p1 = (double)x.y * (double)w.y;
             const double p2 = (double)x.z * (double)w.z, p3 = (double)x.w * (double)w.w;
-            l2[g & 1] += (p0 + p1) + (p2 + p3);
+            qg[g] = (p0 + p1) + (p2 + p3);  // group sum, kept for the prefix pass
+            l2[g & 1] += qg[g];
             ab2[g & 1] += (fabs(p0) + fabs(p1)) + (fabs(p2) + fabs(p3));
         }
         const double loc = l2[0] + l2[1];
         double absp = ab2[0] + ab2[1];
-        double incl = loc;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const double v = __shfl_up(incl, off, 64);
-            if (lane >= off) incl += v;
-        }
+        const double incl = wave_incl_scan_f64(loc);
         double run = incl - loc, sg = 0.0;
 #pragma unroll
-        for (int g = 0; g < NC4; g++) {  // group sums again, in order
-            const f32x4 x = *reinterpret_cast<const f32x4 *>(R.xs + 4 * g), w = R.wv[g];
+        for (int g = 0; g < NC4; g++) {  // the prefix before each group, in order
             sg += fabs(run);
-            run += ((double)x.x * (double)w.x + (double)x.y * (double)w.y) +
-                   ((double)x.z * (double)w.z + (double)x.w * (double)w.w);
+            run += qg[g];
         }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            sg += __shfl_xor(sg, off, 64);
-            absp += __shfl_xor(absp, off, 64);
-        }
-        const double total = __shfl(incl, 63, 64);
+        sg = wave_total_f64(sg);
+        absp = wave_total_f64(absp);
+        const double total = readlane_f64(incl, 63);
         if (lane == 0) {
             // float64 rounding of the sums above is covered, with a wide
             // margin, by the 2^-36 * sum|p| term
@@ -679,6 +679,12 @@ __device__ __forceinline__ void logit_bounds(const RouterArgs &a, LogitRegs<NC4>
             if (e >= E8) B += u * (1.0 + u) * g * absp;
             s_a[e] = total;
             s_b[e] = B;
+        }
+        if constexpr (kAhead) {
+            if (more) {
+#pragma unroll
+                for (int i = 0; i < NC4; i++) R.wv[i] = wn[i];
+            }
         }
     }
 }
@@ -701,7 +707,7 @@ __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a, Chain
     __shared__ double s_a[kMaxE], s_b[kMaxE];
     __shared__ float s_z[kMaxE], s_zlo[kMaxE], s_zhi[kMaxE], s_s[kMaxE], s_g[kMaxE];
     __shared__ unsigned char s_ok[kMaxE];
-    __shared__ int s_sel[kMaxK], s_rank[kMaxE];
+    __shared__ int s_sel[kMaxK];
     __shared__ int s_cw[kFastThreads / 64][kMaxE];
     __shared__ int s_off[kMaxE + 1];
     __shared__ int s_flag;
@@ -756,29 +762,41 @@ __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a, Chain
             s_zhi[e] = zhi;
             s_z[e] = zm;
         }
-        __builtin_amdgcn_wave_barrier();
-        int rank = 0;
-        if (valid) {
-            const float k = sel_key(s_z[e]);
-            for (int f = 0; f < E; f++)
-                if (f != e && better(sel_key(s_z[f]), f, k, e)) rank++;
-            s_rank[e] = rank;
-        }
-        __builtin_amdgcn_wave_barrier();
-        // a selected expert must rank certainly before every expert ranked
-        // below it (certainly: interval ends apart, or touching with the
-        // lower index first)
-        if (valid && rank < K) {
-            const float lo_e = s_zlo[e];
-            for (int f = 0; f < E; f++) {
-                if (s_rank[f] <= rank) continue;
-                const float hi_f = s_zhi[f];
-                ok = ok && (lo_e > hi_f || (lo_e == hi_f && e < f));
+        // Selection: K rounds of a wave argmax over 64-bit keys (score in an
+        // order-preserving encoding, then the inverted index: a larger key
+        // is a better expert, ties to the lower index, as better()).
+        const float zm_e = valid ? s_z[e] : 0.0f, lo_e = valid ? s_zlo[e] : 0.0f;
+        const float hi_e = valid ? s_zhi[e] : 0.0f;
+        uint64_t key = valid ? ((uint64_t)ord_key(sel_key(zm_e)) << 32) | (uint32_t)~e : 0;
+        int rank = -1;
+        for (int r = 0; r < K; r++) {
+            const uint64_t best = wave_max_u64(key);
+            const int be = (int)~(uint32_t)best;
+            if (e == be) {
+                rank = r;
+                key = 0;
             }
+        }
+        // Certification: a selected expert must rank certainly before every
+        // expert ranked below it (interval ends apart, or touching with the
+        // lower index first).  Below it: all unselected experts -- whose
+        // highest interval end Mx, and the lowest index among those at Mx,
+        // two wave reductions give -- and the selected experts of later rank.
+        const bool unsel = valid && rank < 0;
+        const uint32_t mx = wave_max_u32(unsel ? ord_key(hi_e) : 0u);
+        const uint32_t fmin = 64u - wave_max_u32(unsel && ord_key(hi_e) == mx ? 64u - e : 0u);
+        if (rank >= 0 && mx != 0) {
+            const uint32_t ol = ord_key(lo_e);
+            ok = ok && (ol > mx || (ol == mx && (uint32_t)e < fmin));
+        }
+        for (int r2 = 1; r2 < K; r2++) {  // the selected expert of rank r2, by ballot
+            const int f = __builtin_ctzll(__ballot(rank == r2));
+            const float hi_f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hi_e), f));
+            if (rank >= 0 && rank < r2) ok = ok && (lo_e > hi_f || (lo_e == hi_f && e < f));
         }
         ok = __all(ok);
         if (lane == 0) s_flag = ok;
-        if (ok && valid && rank < K) {
+        if (ok && rank >= 0) {
             s_sel[rank] = e;
             store_agent(a.topk_idx + (int64_t)t * K + rank, e);
             if (a.T > 1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");

@@ -47,6 +47,7 @@ struct lcmoe_model {
     std::vector<int32_t> lens_h;   // host mirror of lens (every update goes through here)
     hipGraphExec_t graph = nullptr;
     int graph_B = 0;
+    bool use_graph = true;
     hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};  // start, prefilled, decode, end
     double prefill_ms = 0, decode_ms = 0;
 };
@@ -105,8 +106,8 @@ lcmoe_status validate(const lcmoe_model_desc *d, const lcmoe_model_weights *w) {
     if (d->n_head < 1 || d->n_kv_head < 1 || d->n_head % d->n_kv_head)
         return fail(LCMOE_ERR_INVALID_ARG, "n_head=%d must be a positive multiple of n_kv_head=%d",
                     d->n_head, d->n_kv_head);
-    if (d->head_dim < 8 || d->head_dim > 256 || d->head_dim % 8)
-        return fail(LCMOE_ERR_INVALID_ARG, "head_dim=%d must be a multiple of 8 in [8, 256]",
+    if (d->head_dim < 16 || d->head_dim > 256 || d->head_dim % 16)
+        return fail(LCMOE_ERR_INVALID_ARG, "head_dim=%d must be a multiple of 16 in [16, 256]",
                     d->head_dim);
     if (d->vocab < 1) return fail(LCMOE_ERR_INVALID_ARG, "vocab=%d", d->vocab);
     if (!attn_type_ok(d->attn_type))
@@ -331,7 +332,7 @@ extern "C" lcmoe_status lcmoe_model_generate(lcmoe_model *m, const int32_t *prom
     if (n_new > 1) {
         int32_t one = 1;
         HIP_TRY(hipMemcpyAsync(m->step, &one, 4, hipMemcpyHostToDevice, s));
-        if (!m->graph || m->graph_B != B) {
+        if (m->use_graph && (!m->graph || m->graph_B != B)) {
             if (m->graph) {
                 HIP_TRY(hipGraphExecDestroy(m->graph));
                 m->graph = nullptr;
@@ -356,7 +357,13 @@ extern "C" lcmoe_status lcmoe_model_generate(lcmoe_model *m, const int32_t *prom
         }
     }
     HIP_TRY(hipEventRecord(m->ev[2], s));
-    for (int i = 1; i < n_new; i++) HIP_TRY(hipGraphLaunch(m->graph, s));
+    for (int i = 1; i < n_new; i++) {
+        if (m->use_graph) {
+            HIP_TRY(hipGraphLaunch(m->graph, s));
+        } else if ((st = forward_dev(m, 0, B, 1, m->next, true, 1))) {
+            return st;
+        }
+    }
     HIP_TRY(hipEventRecord(m->ev[3], s));
     for (int b = 0; b < B; b++)
         HIP_TRY(hipMemcpyAsync(out + (size_t)b * n_new, m->out_tok + (size_t)b * D.max_ctx,
@@ -379,6 +386,13 @@ extern "C" lcmoe_status lcmoe_model_generate(lcmoe_model *m, const int32_t *prom
             n_out[b] = n;
         }
     }
+    return LCMOE_OK;
+}
+
+extern "C" lcmoe_status lcmoe_model_set_decode_graph(lcmoe_model *m, int32_t enable) {
+    clear_error();
+    if (!m) return fail(LCMOE_ERR_INVALID_ARG, "model is NULL");
+    m->use_graph = enable != 0;
     return LCMOE_OK;
 }
 

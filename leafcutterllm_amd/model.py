@@ -60,6 +60,7 @@ _SIGS = {
                                          C.c_int32, C.c_int32, C.c_void_p, C.c_void_p]),
     "lcmoe_model_last_timing": (C.c_int32, [C.c_void_p, C.POINTER(C.c_double),
                                             C.POINTER(C.c_double)]),
+    "lcmoe_model_set_decode_graph": (C.c_int32, [C.c_void_p, C.c_int32]),
 }
 
 
@@ -138,6 +139,10 @@ class Model:
                                             out.ctypes.data, n.ctypes.data),
               "lcmoe_model_generate")
         return out, n
+
+    def set_decode_graph(self, enable: bool) -> None:
+        check(_bound().lcmoe_model_set_decode_graph(self._h, int(enable)),
+              "lcmoe_model_set_decode_graph")
 
     def last_timing(self):
         a, b = C.c_double(), C.c_double()

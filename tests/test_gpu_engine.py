@@ -132,3 +132,15 @@ def test_config5_two_layer_cut():
                 e = rel(lg[b], refs[b][1][i].astype(np.float64))
                 print(f"config-5 cut step {i} seq {b}: logits rel-L2 {e:.2e}", flush=True)
                 assert e < LOGIT_TOL
+
+
+def test_eager_decode_equals_graph():
+    w = synth_model(TINY, seed=12)
+    prompts = np.array([[4, 8, 15, 16, 23, 42], [1, 1, 2, 3, 5, 8]])
+    with model(TINY, w, E.ROPE_ABSOLUTE) as m:
+        g, _ = m.generate(prompts, 10)
+        m.set_decode_graph(False)
+        e, _ = m.generate(prompts, 10)
+        m.set_decode_graph(True)
+        g2, _ = m.generate(prompts, 10)
+    assert np.array_equal(g, e) and np.array_equal(g, g2)
