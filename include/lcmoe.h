@@ -392,6 +392,26 @@ lcmoe_status lcmoe_shard_matmul_split_noalloc_dev(int32_t type, const float *a_d
                                                   int32_t k, int32_t n, int32_t k_split,
                                                   void *stream);
 
+/* ---- f32 matrix product: the Backend::matmul operator ----------------- */
+
+/* C[m,n] = A[m,k] B[k,n], f32 row-major: Backend::matmul
+ * (rust/src/backend/mod.rs:18-46) for a HIP backend in place of WgpuBackend
+ * (rust/src/backend/wgpu.rs:152-237, whose WGSL shader rounds in its own
+ * order and falls back to the CPU below 256^3).  Bit-identical to
+ * CpuBackend::matmul on x86 (rust/src/backend/cpu.rs:13-23 ->
+ * avx2_matmul, rust/src/kernels/simd.rs:226-249): for the first
+ * 8 * floor(n / 8) columns each output is an in-order fma chain over k from
+ * 0, the n % 8 tail columns add rounded products.  m, k, n >= 0,
+ * m <= 524280.  Host buffers, synchronous (the operands are copied to the
+ * device and C back on every call, as the trait's slice-in / Vec-out
+ * interface has it). */
+lcmoe_status lcmoe_matmul_f32(const float *a, const float *b, float *c, int32_t m, int32_t k,
+                              int32_t n);
+/* Device buffers (4-byte aligned), enqueued on `stream` (NULL: the null
+ * stream); returns without waiting. */
+lcmoe_status lcmoe_matmul_f32_dev(const float *a_dev, const float *b_dev, float *c_dev, int32_t m,
+                                  int32_t k, int32_t n, void *stream);
+
 /* ---- device self-tests (need a GPU; used by the parity tests) ---------- */
 
 /* Decode `count` elements of a GGUF tensor with the device decoders and

@@ -35,7 +35,8 @@ EXPORTS = (
     "lcmoe_shard_matmul_dev", "lcmoe_shard_matmul_split_dev",
     "lcmoe_shard_matmul_split_noalloc_dev", "lcmoe_model_create", "lcmoe_model_destroy",
     "lcmoe_model_reset", "lcmoe_model_forward", "lcmoe_model_generate",
-    "lcmoe_model_last_timing", "lcmoe_model_set_decode_graph",
+    "lcmoe_model_last_timing", "lcmoe_model_set_decode_graph", "lcmoe_matmul_f32",
+    "lcmoe_matmul_f32_dev",
 )
 
 
@@ -108,6 +109,8 @@ def lib() -> C.CDLL:
         "lcmoe_shard_matmul_dev": (i32, [i32, vp, vp, vp, i32, i32, i32, vp]),
         "lcmoe_shard_matmul_split_dev": (i32, [i32, vp, vp, vp, i32, i32, i32, i32, vp, vp]),
         "lcmoe_shard_matmul_split_noalloc_dev": (i32, [i32, vp, vp, vp, i32, i32, i32, i32, vp]),
+        "lcmoe_matmul_f32": (i32, [vp, vp, vp, i32, i32, i32]),
+        "lcmoe_matmul_f32_dev": (i32, [vp, vp, vp, i32, i32, i32, vp]),
         "lcmoe_forward_norm_residual": (i32, [vp, vp, i32, vp, vp, vp]),
         "lcmoe_forward_norm_residual_dev": (i32, [vp, vp, i32, vp, vp]),
         "lcmoe_gguf_open": (i32, [C.c_char_p, P(vp)]),

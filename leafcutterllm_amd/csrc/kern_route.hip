@@ -20,6 +20,7 @@
 #include "chains.h"
 #include "device_common.h"
 #include "kernels.h"
+#include "norm_device.h"
 
 namespace lcmoe {
 namespace {
@@ -689,11 +690,23 @@ __device__ __forceinline__ void logit_bounds(const RouterArgs &a, LogitRegs<NC4>
     }
 }
 
+// columns per LDS pass of the fused norm: small, so that its registers fit
+// beside the router chunk already in flight
+constexpr int kFusedNormChunk = 1024;
+
 template <int NC4>
 __device__ __forceinline__ void logits_and_activations(const RouterArgs &a, int t, float *s_x,
                                                        double *s_a, double *s_b) {
     LogitRegs<NC4> R;
     load_wchunk<NC4>(a, min((int)(threadIdx.x >> 6), a.E - 1), R.wv);
+    if (a.xin) {  // the fused norm, while the router chunks load
+        if ((threadIdx.x >> 6) == 0) {
+            const int64_t row = (int64_t)t * a.d;
+            rmsnorm_wave<kFusedNormChunk>(a.xin + row, a.norm_w, a.norm_eps, a.d, a.xn + row, s_x);
+        }
+        __threadfence_block();
+        __syncthreads();
+    }
     quantise_token<NC4>(a, t, s_x);  // while the router chunks load
     __syncthreads();
     R.xs = s_x + (threadIdx.x & 63) * (4 * NC4 + 4);
@@ -713,8 +726,11 @@ __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a, Chain
     __shared__ int s_flag;
     // x row for the logits (C <= 64 floats per lane), later the fallback's
     // chain stream (one token, 8 experts)
+    // (and first, with the fused norm, its squares: kRmsnormLds floats)
     constexpr int kXFloats = 64 * (64 + 4), kFbFloats = chain_lds_floats(1 + 8, 256);
-    __shared__ __attribute__((aligned(16))) float s_x[kXFloats > kFbFloats ? kXFloats : kFbFloats];
+    constexpr int kS1 = kXFloats > kFbFloats ? kXFloats : kFbFloats;
+    constexpr int kS2 = rmsnorm_lds<kFusedNormChunk>();
+    __shared__ __attribute__((aligned(16))) float s_x[kS1 > kS2 ? kS1 : kS2];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int t = blockIdx.x, d = a.d, E = a.E, K = a.K;
     if (t >= a.T) {

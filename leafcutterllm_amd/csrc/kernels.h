@@ -32,6 +32,12 @@ struct RouterArgs {
     _Float16 *x16, *x16s; // f16 hi/lo pieces and sums for the matrix-core path, or null
     int32_t *counts, *offsets, *perm, *inv, *touched;
     uint32_t *sync;       // [n_token_groups + 1] zero-initialised counters
+    // Fused post-attention RMSNorm (certified fast router only): with xin
+    // set, each token block first writes x[t] = rms_norm(xin[t]) * norm_w
+    // (CpuBackend::rms_norm bit for bit) to xn (== x) and routes from it.
+    const float *xin = nullptr, *norm_w = nullptr;
+    float norm_eps = 0.0f;
+    float *xn = nullptr;
 };
 // The exact router: logits, limbs, top-k, dispatch.
 hipError_t launch_router(const RouterArgs &a, hipStream_t st);
@@ -137,6 +143,11 @@ hipError_t shard_scratch(float **out);
 // (rust/src/backend/cpu.rs:49-60); x, w, out 16-byte aligned, d % 4 == 0.
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int T, int d, float *out,
                           hipStream_t st);
+
+// C[m,n] = A[m,k] B[k,n] in f32, bit-identical to the CPU backend's
+// avx2_matmul order (kern_matmul.hip); m <= 65535 * 8.
+hipError_t launch_matmul_f32(const float *A, const float *B, float *C, int m, int k, int n,
+                             hipStream_t st);
 
 // ---- decoder-layer kernels of the end-to-end engine (kern_engine.hip) ----
 hipError_t launch_embed(int qt, const uint8_t *table, int vocab, int d, const int32_t *tok, int nq,

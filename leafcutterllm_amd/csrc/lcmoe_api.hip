@@ -471,9 +471,14 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
     return LCMOE_OK;
 }
 
-// y = ffn(x), or y = resid + ffn(x) when resid is given (y may be resid)
+// y = ffn(x), or y = resid + ffn(x) when resid is given (y may be resid).
+// With norm_in, x is the handle's norm buffer and receives
+// rms_norm(norm_in) first: inside the certified router's entry (each token
+// block normalises its own row) for matrix-core batches, otherwise as a
+// launch of its own.
 static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, float *y,
-                                    hipStream_t st, const float *resid = nullptr) {
+                                    hipStream_t st, const float *resid = nullptr,
+                                    const float *norm_in = nullptr) {
     const lcmoe_desc &D = h->desc;
     const int d = D.d_model, E = D.n_expert, K = D.n_expert_used, S = D.n_shared;
     // Fused shared experts ride in the routed launches while every routed
@@ -530,8 +535,26 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
     // so the router launch takes a share of the chains; the matrix-core one
     // takes them all.
     ChainArgs ch_r{}, ch_g{};
+    // The norm fuses into the certified router's entry when the exact chains
+    // run wholly in the gate/up launch anyway (matrix-core batches).  For
+    // row-per-lane batches the router launch hosts a share of the chains,
+    // which read x while a fused norm would still be writing it; there the
+    // separate norm launch measured faster (config 2, T = 1: 73 against
+    // 78 us per call).
+    if (norm_in && fast && pr.mfma) {
+        ra.xin = norm_in;
+        ra.norm_w = h->norm_w;
+        ra.norm_eps = h->norm_eps;
+        ra.xn = h->xn;
+    } else if (norm_in) {
+        HIP_TRY(timed(h, st, kSlotNorm, [&] {
+            return launch_rmsnorm(norm_in, h->norm_w, h->norm_eps, T, d, h->xn, st);
+        }));
+    }
     if (fast) {
-        const int kA = pr.mfma ? 0 : (d / 4) & ~255;
+        // the router launch's share of the exact chains reads x, which the
+        // fused norm is still writing there: all chains go to gate/up then
+        const int kA = pr.mfma || ra.xin ? 0 : (d / 4) & ~255;
         if (kA > 0) ch_r = make_chains(x, h->wrt, h->logits, h->chain_part, T, d, E, 0, kA, 8);
         ch_g = make_chains(x, h->wrt, h->logits, h->chain_part, T, d, E, kA, d, 8);
         ra.x16 = mfma ? h->x16 : nullptr;
@@ -640,10 +663,7 @@ extern "C" lcmoe_status lcmoe_set_norm(lcmoe_handle *h, const float *weight, flo
 
 static lcmoe_status enqueue_norm_residual(lcmoe_handle *h, const float *hidden, int32_t T,
                                           float *out, hipStream_t st) {
-    HIP_TRY(timed(h, st, kSlotNorm, [&] {
-        return launch_rmsnorm(hidden, h->norm_w, h->norm_eps, T, h->desc.d_model, h->xn, st);
-    }));
-    return enqueue_forward(h, h->xn, T, out, st, hidden);
+    return enqueue_forward(h, h->xn, T, out, st, hidden, hidden);
 }
 
 extern "C" lcmoe_status lcmoe_forward_norm_residual_dev(lcmoe_handle *h, const float *hidden_dev,
@@ -884,6 +904,48 @@ extern "C" lcmoe_status lcmoe_shard_matmul(int32_t type, const float *a, const u
     for (void *p : {da, db, dc})
         if (p) (void)hipFree(p);
     if (e != hipSuccess) return fail(LCMOE_ERR_HIP, "shard_matmul: %s", hipGetErrorString(e));
+    return LCMOE_OK;
+}
+
+static lcmoe_status matmul_args(int32_t m, int32_t k, int32_t n) {
+    if (m < 0 || k < 0 || n < 0) return fail(LCMOE_ERR_INVALID_ARG, "m=%d k=%d n=%d", m, k, n);
+    if (m > 524280) return fail(LCMOE_ERR_INVALID_ARG, "m=%d exceeds 524280", m);
+    return LCMOE_OK;
+}
+
+extern "C" lcmoe_status lcmoe_matmul_f32_dev(const float *a_dev, const float *b_dev, float *c_dev,
+                                             int32_t m, int32_t k, int32_t n, void *stream) {
+    clear_error();
+    if (lcmoe_status s = matmul_args(m, k, n)) return s;
+    if ((size_t)m * n == 0) return LCMOE_OK;
+    if (!c_dev || (k > 0 && (!a_dev || !b_dev)))
+        return fail(LCMOE_ERR_INVALID_ARG, "a, b or c is NULL");
+    if (((uintptr_t)a_dev | (uintptr_t)b_dev | (uintptr_t)c_dev) & 3)
+        return fail(LCMOE_ERR_INVALID_ARG, "a, b and c must be 4-byte aligned");
+    HIP_TRY(launch_matmul_f32(a_dev, b_dev, c_dev, m, k, n, (hipStream_t)stream));
+    return LCMOE_OK;
+}
+
+extern "C" lcmoe_status lcmoe_matmul_f32(const float *a, const float *b, float *c, int32_t m,
+                                         int32_t k, int32_t n) {
+    clear_error();
+    if (lcmoe_status s = matmul_args(m, k, n)) return s;
+    if ((size_t)m * n == 0) return LCMOE_OK;
+    if (!c || (k > 0 && (!a || !b))) return fail(LCMOE_ERR_INVALID_ARG, "a, b or c is NULL");
+    const size_t ab = sizeof(float) * (size_t)m * k, bb = sizeof(float) * (size_t)k * n,
+                 cb = sizeof(float) * (size_t)m * n;
+    void *da = nullptr, *db = nullptr, *dc = nullptr;
+    hipError_t e = hipMalloc(&da, ab ? ab : 4);
+    if (e == hipSuccess) e = hipMalloc(&db, bb ? bb : 4);
+    if (e == hipSuccess) e = hipMalloc(&dc, cb);
+    if (e == hipSuccess && ab) e = hipMemcpy(da, a, ab, hipMemcpyHostToDevice);
+    if (e == hipSuccess && bb) e = hipMemcpy(db, b, bb, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = launch_matmul_f32((const float *)da, (const float *)db, (float *)dc, m, k, n, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(c, dc, cb, hipMemcpyDeviceToHost);
+    for (void *p : {da, db, dc})
+        if (p) (void)hipFree(p);
+    if (e != hipSuccess) return fail(LCMOE_ERR_HIP, "matmul_f32: %s", hipGetErrorString(e));
     return LCMOE_OK;
 }
 

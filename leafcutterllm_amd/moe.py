@@ -192,3 +192,18 @@ def shard_matmul(qtype: int, a: np.ndarray, b: np.ndarray, k: int, n: int) -> np
     check(lib().lcmoe_shard_matmul(qtype, _ptr(a), _ptr(b), _ptr(out), a.shape[0], k, n),
           "lcmoe_shard_matmul")
     return out
+
+
+def matmul(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Backend::matmul (rust/src/backend/mod.rs:18-46) on the GPU:
+    a [m, k] @ b [k, n] in f32, bit-identical to the x86 CPU backend
+    (lcmoe_matmul_f32)."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    if a.ndim != 2 or b.ndim != 2 or a.shape[1] != b.shape[0]:
+        raise LcmoeError(1, "matmul", f"shapes {a.shape} @ {b.shape}")
+    m, k = a.shape
+    n = b.shape[1]
+    c = np.empty((m, n), np.float32)
+    check(lib().lcmoe_matmul_f32(_ptr(a), _ptr(b), c.ctypes.data, m, k, n), "lcmoe_matmul_f32")
+    return c

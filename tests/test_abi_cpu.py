@@ -19,7 +19,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def header_symbols():
     txt = open(os.path.join(ROOT, "include", "lcmoe.h")).read()
-    return sorted(set(re.findall(r"\b(lcmoe_[a-z_]+)\s*\(", txt)))
+    return sorted(set(re.findall(r"\b(lcmoe_[a-z0-9_]+)\s*\(", txt)))
 
 
 def test_exports_every_declared_symbol():
@@ -207,3 +207,17 @@ def test_model_create_rejects_bad_desc_before_device_work():
     with pytest.raises(L.LcmoeError) as e:
         Model(mc.desc(2, 16, 32), w2)
     assert _lib.STATUS[e.value.status] == "LCMOE_ERR_INVALID_ARG"
+
+
+def test_matmul_f32_argument_errors():
+    """lcmoe_matmul_f32 validates before any device work."""
+    lib = L.lib()
+    a = np.zeros(4, np.float32)
+    for m, k, n in [(-1, 2, 2), (2, -1, 2), (2, 2, -1), (524281, 1, 1)]:
+        st = lib.lcmoe_matmul_f32(a.ctypes.data, a.ctypes.data, a.ctypes.data, m, k, n)
+        assert _lib.STATUS[st] == "LCMOE_ERR_INVALID_ARG", (m, k, n)
+    assert _lib.STATUS[lib.lcmoe_matmul_f32(None, None, a.ctypes.data, 2, 2, 2)] == \
+        "LCMOE_ERR_INVALID_ARG"
+    assert lib.lcmoe_matmul_f32(None, None, None, 0, 5, 3) == 0   # empty: nothing to do
+    st = lib.lcmoe_matmul_f32_dev(6, 4, 4, 1, 1, 1, None)        # misaligned a
+    assert _lib.STATUS[st] == "LCMOE_ERR_INVALID_ARG"

@@ -58,6 +58,12 @@ NORM_CASES = {
                                       L.ROUTE_SIGMOID_GROUP, Q4, Q6, n_shared=1,
                                       d_ff_shared=512, n_group=4, topk_group=2,
                                       bias="plus2_first8"),
+    # the norm fused into the certified router's entry, several norm chunks
+    "d2048-e60-fused": small_config("d2048", 2048, 256, 60, 4, L.ROUTE_SOFTMAX, Q4, Q4,
+                                    n_shared=1, d_ff_shared=256),
+    "d4096-fused": small_config("d4096", 4096, 256, 8, 2, L.ROUTE_SOFTMAX_RENORM, Q4, Q4),
+    # the exact router (d % 128 != 0): the norm as a launch of its own
+    "d288-separate": small_config("d288", 288, 512, 8, 2, L.ROUTE_SOFTMAX_RENORM, Q4, Q4),
 }
 
 
