@@ -423,6 +423,12 @@ lcmoe_status lcmoe_debug_rmsnorm(const float *x, const float *w, float eps, int3
                                  float *out);
 /* The router's sigmoid evaluated on the device, for host/device bit parity. */
 lcmoe_status lcmoe_debug_sigmoid(const float *x, int64_t n, float *out);
+/* Tokens of the handle's last forward whose expert selection the certified
+ * sigmoid-group router left to the exact chain logits (their float64 bounds
+ * could not order the decision); -1 when that forward did not use it.  Waits
+ * for the forward.  No counterpart in the reference: it observes which of
+ * two bit-identical routes ran. */
+lcmoe_status lcmoe_debug_route_fallbacks(lcmoe_handle *h, int32_t *count);
 
 #ifdef __cplusplus
 }

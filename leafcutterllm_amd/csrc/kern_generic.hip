@@ -127,8 +127,9 @@ __global__ __launch_bounds__(256) void k_down(const uint8_t *__restrict__ down, 
 // (column blocks of 1024, tokens); one float4 of columns per thread.  With
 // cr.logits the token's routing weights are first computed from the exact
 // logits and the selection (the expressions of CpuBackend::softmax,
-// rust/src/backend/cpu.rs:66-79: max, sequential sum of exp, divide) and
-// the first column block stores them to topk_w.
+// rust/src/backend/cpu.rs:66-79: max, sequential sum of exp, divide; for
+// the sigmoid-group kind the selected sigmoid scores over their sequential
+// sum, times the scale) and the first column block stores them to topk_w.
 __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ Yr, int ks_r,
                                                  int64_t stride_r, const float *__restrict__ Ys,
                                                  int ks_s, int64_t stride_s,
@@ -139,7 +140,24 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ Yr, i
     __shared__ float s_w[kMaxK];
     __shared__ float s_z[kMaxE];
     const int t = blockIdx.y, c4 = blockIdx.x * blockDim.x + threadIdx.x;
-    if (cr.logits) {
+    if (cr.logits && cr.kind == LCMOE_ROUTE_SIGMOID_GROUP) {
+        // sigmoid scores of the K selected, their sequential sum, the scaled
+        // shares (token_weights' expressions)
+        const float *l = cr.logits + (int64_t)t * cr.E;
+        const int32_t *sel = cr.topk_idx + (int64_t)t * K;
+        if (threadIdx.x < K) s_z[threadIdx.x] = sigmoid_cw(l[sel[threadIdx.x]]);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float sum = 0.0f;
+            for (int k = 0; k < K; k++) sum = sum + s_z[k];
+            for (int k = 0; k < K; k++) {
+                const float w = (s_z[k] / sum) * cr.scale;
+                s_w[k] = w;
+                if (blockIdx.x == 0) topk_w[(int64_t)t * K + k] = w;
+            }
+        }
+        __syncthreads();
+    } else if (cr.logits) {
         // the scores (logit + bias) of the softmax's items (the K selected
         // for the renormalised router, all E otherwise) and their exps are
         // formed in parallel; thread 0 then sums the exps in item order, the

@@ -539,12 +539,15 @@ constexpr int kFastThreads = 512;  // 8 waves: one expert per wave for E = 8
 // columns each, and meet through lane shuffles (NTHR threads, a multiple
 // of 64).  With s_x, the same reads stage the token row into LDS for the
 // logits: lane l's chunk of C = 4*NC4 columns is row l of C + 4 floats,
-// which keeps 8 consecutive lanes' b128 reads on distinct banks.
+// which keeps 8 consecutive lanes' b128 reads on distinct banks.  With
+// nshare > 1 this block takes share `share` of the work (NTHR-thread slices
+// share, share + nshare, ...).
 template <int NC4, int NTHR = kFastThreads>
-__device__ void quantise_token(const RouterArgs &a, int t, float *s_x) {
+__device__ void quantise_token(const RouterArgs &a, int t, float *s_x, int share = 0,
+                               int nshare = 1) {
     constexpr int C = 4 * NC4;
     const int d = a.d, nsb = d / 32;
-    for (int q = threadIdx.x; q < 4 * nsb; q += NTHR) {
+    for (int q = share * NTHR + threadIdx.x; q < 4 * nsb; q += nshare * NTHR) {
         const int sb = q >> 2, part = q & 3, col0 = 32 * sb + 8 * part;
         const f32x4 *v = reinterpret_cast<const f32x4 *>(a.x + (int64_t)t * d + col0);
         const f32x4 v0 = v[0], v1 = v[1];
@@ -853,6 +856,304 @@ __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a, Chain
 }
 
 // ---------------------------------------------------------------------------
+// Certified router for the sigmoid-group kind (lco_route kind 2, the
+// DeepSeek-V3 noaux_tc rule): score s_e = sigmoid(c_e) of the reference chain
+// logit c_e, key z_e = s_e + bias_e; each of the G groups of E/G experts
+// scores the rounded sum of its two largest keys; the topk_group best groups
+// are kept and the K largest keys among their experts selected, ties to the
+// lower index throughout.
+//
+// Grid (E / kSigWaves, T): wave w of block (b, t) bounds the chain logit of
+// expert kSigWaves b + w for token t in float64, as the fast router does
+// (c_e in [S_d - B, S_d + B], hence in [zlo, zhi] as floats); block (0, t)
+// also writes t's activations.  The last block of token t to finish (a
+// per-token counter) certifies it in one wave:
+//   * sigmoid_cw dips below its running maximum by at most one ulp (an
+//     exhaustive check over every float input, oracle/sigmoid_monotone.c),
+//     so s_e lies in [down(sigmoid(zlo)), up(sigmoid(zhi))], and the key in
+//     the rounded sums with the bias (rounding is monotone);
+//   * a group score is monotone in every key, so the group scores of the
+//     low and the high keys bound it;
+//   * the kept groups stand when every kept group's low score beats every
+//     dropped group's high score (or ties it with a lower index);
+//   * the selection stands rank by rank as in the fast router, over the
+//     kept groups' experts.
+// A certified token's selection is final here; the others are marked for
+// the exact chains (k_route_chains) and selection (k_route_select) that
+// follow, which also dispatch every token.  The routing weights come from
+// the exact logits (chains beside the gate/up products) in the combine.
+// ---------------------------------------------------------------------------
+constexpr int kSigWaves = 4;
+
+// d / 256 values with an instantiation (the lane's chunk fully unrolled,
+// so all of its loads are in flight at once)
+__host__ __device__ constexpr bool sig_nc4_ok(int n) {
+    return n == 1 || n == 2 || n == 4 || n == 8 || n == 16 || n == 28 || n == 32;
+}
+
+__device__ __forceinline__ void store_agent_f64(double *p, double v) {
+    __hip_atomic_store(reinterpret_cast<unsigned long long *>(p),
+                       (unsigned long long)__double_as_longlong(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ double load_agent_f64(const double *p) {
+    return __longlong_as_double((long long)__hip_atomic_load(
+        reinterpret_cast<unsigned long long *>(const_cast<double *>(p)), __ATOMIC_RELAXED,
+        __HIP_MEMORY_SCOPE_AGENT));
+}
+
+// float64 chain logit and error bound of (t, e), as logit_bounds(): lane l
+// holds columns [l C, l C + C) (C = 4 NC4) of the token row (read through
+// the cache: every wave of the token reads it) and of the router row in
+// lane-chunk order (a.wlc); written to a.bnd[(t E + e) 2 + {0, 1}].
+template <int NC4>
+__device__ void sig_bounds(const RouterArgs &a, int t, int e) {
+    constexpr int C = 4 * NC4;
+    const int lane = threadIdx.x & 63, d = a.d;
+    const f32x4 *xr = reinterpret_cast<const f32x4 *>(a.x + (int64_t)t * d + lane * C);
+    const f32x4 *wr = reinterpret_cast<const f32x4 *>(a.wlc) + (int64_t)e * NC4 * 64 + lane;
+    f32x4 wv[NC4], xv[NC4];
+#pragma unroll
+    for (int g = 0; g < NC4; g++) {  // the whole chunk in flight
+        wv[g] = wr[64 * g];
+        xv[g] = xr[g];
+    }
+    double l2[2] = {0.0, 0.0}, ab2[2] = {0.0, 0.0}, qg[NC4];
+#pragma unroll
+    for (int g = 0; g < NC4; g++) {  // products are exact in float64
+        const f32x4 x = xv[g], w = wv[g];
+        const double p0 = (double)x.x * (double)w.x, p1 = (double)x.y * (double)w.y;
+        const double p2 = (double)x.z * (double)w.z, p3 = (double)x.w * (double)w.w;
+        qg[g] = (p0 + p1) + (p2 + p3);
+        l2[g & 1] += qg[g];
+        ab2[g & 1] += (fabs(p0) + fabs(p1)) + (fabs(p2) + fabs(p3));
+    }
+    const double loc = l2[0] + l2[1];
+    double absp = ab2[0] + ab2[1];
+    const double incl = wave_incl_scan_f64(loc);
+    double run = incl - loc, sg = 0.0;
+#pragma unroll
+    for (int g = 0; g < NC4; g++) {
+        sg += fabs(run);
+        run += qg[g];
+    }
+    sg = wave_total_f64(sg);
+    absp = wave_total_f64(absp);
+    const double total = readlane_f64(incl, 63);
+    if (lane == 0) {
+        const double u = 0x1p-24, gm = 1.0 + 1.01 * (double)d * u;
+        const double sabs = 4.0 * sg + 4.0 * absp;
+        double B = u * gm * sabs + 0x1p-36 * absp + (double)d * 0x1p-149;
+        if (e >= (a.E & ~7)) B += u * (1.0 + u) * gm * absp;
+        store_agent_f64(a.bnd + ((int64_t)t * a.E + e) * 2, total);
+        store_agent_f64(a.bnd + ((int64_t)t * a.E + e) * 2 + 1, B);
+    }
+}
+
+// Certification of token t by one wave (E <= 256, G <= 64);
+// s_lo / s_hi / s_m: E floats each (the low, high and point keys), s_g:
+// 3 x 64 group scores, s_sel: K.  Writes topk_idx[t] when certified and
+// flag[t] (0 certified, 1 for the exact path).
+__device__ void sig_certify(const RouterArgs &a, int t, float *s_lo, float *s_hi, float *s_m,
+                            float *s_g, int *s_sel) {
+    const int lane = threadIdx.x & 63, E = a.E, K = a.K, NI = (E + 63) / 64;
+    const RouteParams &rp = a.rp;
+    const int G = rp.n_group, gs = E / G;
+    bool ok = true;
+    double Sv[4], Bv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {  // all of this lane's bounds in flight
+        const int e = min(lane + 64 * i, E - 1);
+        Sv[i] = load_agent_f64(a.bnd + ((int64_t)t * E + e) * 2);
+        Bv[i] = load_agent_f64(a.bnd + ((int64_t)t * E + e) * 2 + 1);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int e = lane + 64 * i;
+        if (i >= NI || e >= E) break;
+        const double S = Sv[i], B = Bv[i];
+        const double lo = S - B, hi = S + B;
+        const bool fin = __builtin_isfinite(lo) && __builtin_isfinite(hi);
+        ok = ok && fin;
+        const float zlo = fin ? ceil_f32(lo) : 0.0f, zhi = fin ? floor_f32(hi) : 0.0f;
+        const float zm = fin ? (float)S : 0.0f;
+        // sigmoid_cw's dips are at most one ulp: widen by one step each way
+        // (scores lie in [0, 1])
+        float klo = sigmoid_cw(zlo), khi = next_up(sigmoid_cw(zhi)), km = sigmoid_cw(zm);
+        klo = klo > 0.0f ? next_down(klo) : 0.0f;
+        if (rp.has_bias) {
+            const float b = a.bias[e];
+            klo = klo + b;
+            khi = khi + b;
+            km = km + b;
+        }
+        // finite keys order as values (a NaN bias goes to the exact path)
+        ok = ok && __builtin_isfinite(klo) && __builtin_isfinite(khi) && __builtin_isfinite(km);
+        s_lo[e] = klo;
+        s_hi[e] = khi;
+        s_m[e] = km;
+    }
+    chain_detail::wave_lds_sync();
+    // group scores of the three key sets: the rounded sum of the group's two
+    // largest keys (select_token's expression; only the values matter, and
+    // the keys are finite when they count).  Groups of a power-of-two size up
+    // to 64 are lane segments of each 64-expert slice: a butterfly over the
+    // segment merges (largest, second) pairs.
+    if (gs <= 64 && (gs & (gs - 1)) == 0) {
+        for (int arr = 0; arr < 3; arr++) {
+            const float *v = arr == 0 ? s_lo : arr == 1 ? s_hi : s_m;
+            for (int i = 0; i < NI; i++) {
+                const int e = lane + 64 * i;
+                float k1 = e < E ? v[e] : -__builtin_inff(), k2 = -__builtin_inff();
+                for (int off = 1; off < gs; off <<= 1) {
+                    const float o1 = __shfl_xor(k1, off, 64), o2 = __shfl_xor(k2, off, 64);
+                    const float hi1 = fmaxf(k1, o1), lo1 = fminf(k1, o1);
+                    k2 = fmaxf(lo1, fmaxf(k2, o2));
+                    k1 = hi1;
+                }
+                if (e < E && (lane & (gs - 1)) == 0)
+                    s_g[64 * arr + e / gs] = gs >= 2 ? k1 + k2 : k1;
+            }
+        }
+    } else if (lane < G) {
+        for (int arr = 0; arr < 3; arr++) {
+            const float *v = arr == 0 ? s_lo : arr == 1 ? s_hi : s_m;
+            float k1 = -__builtin_inff(), k2 = -__builtin_inff();
+            int e1 = INT_MAX, e2 = INT_MAX;
+            for (int i = 0; i < gs; i++) {
+                const int e = lane * gs + i;
+                const float k = sel_key(v[e]);
+                if (better(k, e, k1, e1)) {
+                    k2 = k1;
+                    e2 = e1;
+                    k1 = k;
+                    e1 = e;
+                } else if (better(k, e, k2, e2)) {
+                    k2 = k;
+                    e2 = e;
+                }
+            }
+            s_g[64 * arr + lane] = gs >= 2 ? v[e1] + v[min(e2, E - 1)] : v[e1];
+        }
+    }
+    chain_detail::wave_lds_sync();
+    // kept groups by the point scores, topk_group rounds of a wave argmax
+    const bool gv = lane < G;
+    const float glo = gv ? s_g[lane] : 0.0f, ghi = gv ? s_g[64 + lane] : 0.0f;
+    uint64_t gkey = gv ? ((uint64_t)ord_key(sel_key(s_g[128 + lane])) << 32) | (uint32_t)~lane : 0;
+    bool kept = false;
+    for (int r = 0; r < rp.topk_group; r++) {
+        const uint64_t best = wave_max_u64(gkey);
+        if (gv && lane == (int)~(uint32_t)best) {
+            kept = true;
+            gkey = 0;
+        }
+    }
+    // every kept group above every dropped one: the dropped groups' highest
+    // score Mx and the lowest index at it, two wave reductions
+    {
+        const bool dropped = gv && !kept;
+        const uint32_t mx = wave_max_u32(dropped ? ord_key(ghi) : 0u);
+        const uint32_t fmin = 64u - wave_max_u32(dropped && ord_key(ghi) == mx ? 64u - lane : 0u);
+        if (kept && mx != 0) {
+            const uint32_t ol = ord_key(glo);
+            ok = ok && (ol > mx || (ol == mx && (uint32_t)lane < fmin));
+        }
+    }
+    const uint64_t kmask = __ballot(kept);
+    // K rounds of a wave argmax over the kept groups' experts (point keys)
+    uint64_t ek[4];
+    int rank[4];
+    bool cand[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int e = lane + 64 * i;
+        cand[i] = i < NI && e < E && ((kmask >> (e / gs)) & 1ull);
+        ek[i] = cand[i] ? ((uint64_t)ord_key(sel_key(s_m[e])) << 32) | (uint32_t)~e : 0;
+        rank[i] = -1;
+    }
+    for (int r = 0; r < K; r++) {
+        uint64_t mine = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) mine = ek[i] > mine ? ek[i] : mine;
+        const uint64_t best = wave_max_u64(mine);
+        const int be = (int)~(uint32_t)best;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (lane + 64 * i == be) {
+                rank[i] = r;
+                ek[i] = 0;
+            }
+        if (lane == 0) s_sel[r] = be;
+    }
+    chain_detail::wave_lds_sync();
+    // each selected expert certainly above every unselected candidate ...
+    {
+        uint32_t ml = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (cand[i] && rank[i] < 0) ml = max(ml, ord_key(s_hi[lane + 64 * i]));
+        const uint32_t mx = wave_max_u32(ml);
+        uint32_t fl = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = lane + 64 * i;
+            if (cand[i] && rank[i] < 0 && ord_key(s_hi[e]) == mx) fl = max(fl, (uint32_t)(E - e));
+        }
+        const uint32_t fmin = (uint32_t)E - wave_max_u32(fl);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = lane + 64 * i;
+            if (rank[i] >= 0 && mx != 0) {
+                const uint32_t ol = ord_key(s_lo[e]);
+                ok = ok && (ol > mx || (ol == mx && (uint32_t)e < fmin));
+            }
+        }
+    }
+    // ... and above every selected expert of a later rank
+    for (int r2 = 1; r2 < K; r2++) {
+        const int f = s_sel[r2];
+        const float hf = s_hi[f];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = lane + 64 * i;
+            if (rank[i] >= 0 && rank[i] < r2) {
+                const float le = s_lo[e];
+                ok = ok && (le > hf || (le == hf && e < f));
+            }
+        }
+    }
+    ok = __all(ok);
+    if (ok) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (rank[i] >= 0) store_agent(a.topk_idx + (int64_t)t * K + rank[i], lane + 64 * i);
+    }
+    if (lane == 0) store_agent(a.flag + t, ok ? 0 : 1);
+}
+
+template <int NC4>
+__global__ __launch_bounds__(64 * kSigWaves) void k_route_sig(RouterArgs a) {
+    __shared__ float s_f[3 * kMaxE + 3 * 64];  // certification: keys, group scores
+    __shared__ int s_last;
+    const int t = blockIdx.y, tid = threadIdx.x, wave = tid >> 6;
+    sig_bounds<NC4>(a, t, blockIdx.x * kSigWaves + wave);
+    // the token's activations, a slice per block
+    quantise_token<1, 64 * kSigWaves>(a, t, nullptr, blockIdx.x, gridDim.x);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's bounds have landed
+    __syncthreads();
+    if (tid == 0) s_last = atomicAdd(&a.tsync[t], 1u) == gridDim.x - 1;
+    __syncthreads();
+    if (!s_last) return;
+    // the last block of token t: every bound of t is stored
+    if (wave == 0) {
+        __shared__ int s_sel[kMaxK];
+        if (tid == 0) a.tsync[t] = 0;
+        sig_certify(a, t, s_f, s_f + a.E, s_f + 2 * a.E, s_f + 3 * a.E, s_sel);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Chain router: exact logits for every (token, expert) as chain tiles
 // (chains.h), spread over the whole chip, then selection and dispatch.  It
 // serves the sigmoid-group kind, more than 64 experts, and batches whose
@@ -877,7 +1178,14 @@ __global__ __launch_bounds__(64 * kChainWaves) void k_route_chains(RouterArgs a,
     __shared__ __attribute__((aligned(16))) float s_lds[kChainWaves][kChainLds];
     if ((int)blockIdx.x < chain_blocks) {
         const int wave = threadIdx.x >> 6, tile = blockIdx.x * kChainWaves + wave;
-        if (tile < ch.tiles) {
+        // after the certified sigmoid router: only tokens it marked
+        bool need = true;
+        if (a.flag && tile < ch.tiles) {
+            const int t0 = (tile / ((ch.E + 7) / 8)) * ch.nt;
+            need = false;
+            for (int t = t0; t < min(t0 + ch.nt, ch.T); t++) need = need || a.flag[t] != 0;
+        }
+        if (tile < ch.tiles && need) {
             if (ch.nt == 1)  // fewer than 8 tokens: 1-token tiles, 256-column chunks
                 chain_tile<1, 256, 2>(ch, tile, s_lds[wave]);
             else
@@ -896,9 +1204,17 @@ __global__ __launch_bounds__(64 * kSelWaves) void k_route_select(RouterArgs a) {
     __shared__ int s_off[kMaxE + 1];
     __shared__ int s_flag;
     const int tid = threadIdx.x, wave = tid >> 6, t = blockIdx.x * kSelWaves + wave;
-    if (t < a.T) select_token(a, t, s_z[wave], s_s[wave], s_g[wave], s_ok[wave], s_sel[wave]);
+    // after the certified sigmoid router: only the tokens it marked
+    const bool sel = t < a.T && (!a.flag || a.flag[t] != 0);
+    if (sel) select_token(a, t, s_z[wave], s_s[wave], s_g[wave], s_ok[wave], s_sel[wave]);
     if (a.T == 1) {
-        if (wave == 0) dispatch_one(a, s_sel[0]);
+        if (wave == 0) {
+            if (!sel) {  // certified: the selection is in topk_idx
+                if ((tid & 63) < a.K) s_sel[0][tid & 63] = load_agent(a.topk_idx + (tid & 63));
+                chain_detail::wave_lds_sync();
+            }
+            dispatch_one(a, s_sel[0]);
+        }
         return;
     }
     __threadfence();  // every selection released at device scope before the count
@@ -989,6 +1305,36 @@ hipError_t launch_route_fast(const RouterArgs &a, const ChainArgs &ch, hipStream
     }
     hipLaunchKernelGGL(k_route_fast, dim3(a.T + cb), dim3(kFastThreads), 0, st, a, c);
     return hipGetLastError();
+}
+
+bool route_sig_ok(const RouterArgs &a) {
+    const int G = a.rp.n_group;
+    return a.rp.kind == LCMOE_ROUTE_SIGMOID_GROUP && a.wlc && a.bnd && a.tsync && a.flag &&
+           a.E % kSigWaves == 0 && a.E <= 256 && a.d % 256 == 0 && sig_nc4_ok(a.d / 256) && G >= 1 &&
+           G <= 64 && a.E % G == 0 && a.K <= kMaxK && route_chains_ok(a);
+}
+
+hipError_t launch_route_sig(const RouterArgs &a, hipStream_t st) {
+    if (!route_sig_ok(a)) return hipErrorInvalidValue;
+    static_assert(64 % kSigWaves == 0, "blocks of whole expert groups");
+    const dim3 grid(a.E / kSigWaves, a.T), block(64 * kSigWaves);
+    switch (a.d / 256) {
+    case 1: hipLaunchKernelGGL(k_route_sig<1>, grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL(k_route_sig<2>, grid, block, 0, st, a); break;
+    case 4: hipLaunchKernelGGL(k_route_sig<4>, grid, block, 0, st, a); break;
+    case 8: hipLaunchKernelGGL(k_route_sig<8>, grid, block, 0, st, a); break;
+    case 16: hipLaunchKernelGGL(k_route_sig<16>, grid, block, 0, st, a); break;
+    case 28: hipLaunchKernelGGL(k_route_sig<28>, grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL(k_route_sig<32>, grid, block, 0, st, a); break;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    // the exact chains and selection for the marked tokens; the activations
+    // are written already
+    RouterArgs b = a;
+    b.xh = nullptr;
+    b.x16 = nullptr;
+    return launch_route_chains(b, st);
 }
 
 hipError_t launch_debug_sigmoid(const float *x, int64_t n, float *out, hipStream_t st) {

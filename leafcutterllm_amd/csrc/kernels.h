@@ -38,6 +38,13 @@ struct RouterArgs {
     const float *xin = nullptr, *norm_w = nullptr;
     float norm_eps = 0.0f;
     float *xn = nullptr;
+    // Certified sigmoid-group router: float64 logit and bound per (t, e),
+    // per-token block counters, and per-token fallback marks (1: the exact
+    // chains decide this token); the chain and select launches that follow
+    // it serve only the marked tokens when `flag` is set.
+    double *bnd = nullptr;      // [T, E, 2]
+    uint32_t *tsync = nullptr;  // [T] zero-initialised
+    int32_t *flag = nullptr;    // [T]
 };
 // The exact router: logits, limbs, top-k, dispatch.
 hipError_t launch_router(const RouterArgs &a, hipStream_t st);
@@ -52,6 +59,14 @@ hipError_t launch_route_chains(const RouterArgs &a, hipStream_t st);
 // and of the routed gate/up launch (the rest).
 bool route_fast_ok(const RouterArgs &a);
 hipError_t launch_route_fast(const RouterArgs &a, const ChainArgs &ch, hipStream_t st);
+// Certified router for the sigmoid-group kind (E <= 256, E % 4 == 0,
+// d / 256 in {1, 2, 4, 8, 16, 28, 32}, n_group <= 64): float64 logit bounds, then
+// certification of the group and expert selection per token; a.bnd, a.tsync
+// and a.flag set.  Writes topk_idx and the activations; the exact chains
+// (launch_route_chains with a.flag) and selection then serve only tokens the
+// bounds could not certify, and dispatch every token.
+bool route_sig_ok(const RouterArgs &a);
+hipError_t launch_route_sig(const RouterArgs &a, hipStream_t st);
 int router_token_groups(int T, int d, int E);
 
 // See SlotArgs (device_common.h): nr routed slots, then S fused shared

@@ -36,6 +36,12 @@ const char *kSlotNames[kNumSlots] = {"router", "act16", "gateup", "gateup_shared
 constexpr int kMaxKSplit = 4;
 // largest T * E * d served by the certified per-token router
 constexpr int64_t kFastRouterElems = (int64_t)1 << 24;
+// largest T * E * d served by the certified sigmoid-group router.  It
+// re-reads the router matrix per token, and a token its bounds cannot settle
+// (about 2% at DeepSeek-V3 shapes) makes the forward wait for the exact
+// chains: past about 24 tokens at those shapes the chain router alone is
+// the faster one.
+constexpr int64_t kSigRouterElems = (int64_t)1 << 25;
 
 struct ExpertSet {  // one family of experts (routed or shared)
     int n = 0, F = 0, qt_gu = 0, qt_dn = 0;
@@ -83,7 +89,12 @@ struct lcmoe_handle {
             *inv = nullptr, *touched = nullptr;
     float *topk_w = nullptr;
     uint32_t *sync = nullptr;
+    // certified sigmoid-group router: bounds, per-token counters and marks
+    double *sig_bnd = nullptr;
+    uint32_t *sig_sync = nullptr;
+    int32_t *sig_flag = nullptr;
     int last_T = -1;
+    bool last_sig = false;  // the last forward used the certified sigmoid-group router
     hipStream_t last_stream = nullptr;
     bool timing = false;
     struct Pending { int slot; hipEvent_t a, b; };
@@ -375,6 +386,14 @@ extern "C" lcmoe_status lcmoe_create(const lcmoe_desc *desc, const lcmoe_weights
     if ((st = alloc_n(h, &h->sync, nsync))) return bail(st);
     if (hipMemset(h->sync, 0, sizeof(uint32_t) * nsync) != hipSuccess)
         return bail(fail(LCMOE_ERR_HIP, "workspace clear failed"));
+    if (D.route_kind == LCMOE_ROUTE_SIGMOID_GROUP) {
+        if ((st = alloc_n(h, &h->sig_bnd, 2 * Tm * E))) return bail(st);
+        if ((st = alloc_n(h, &h->sig_sync, Tm))) return bail(st);
+        if ((st = alloc_n(h, &h->sig_flag, Tm))) return bail(st);
+        if (hipMemset(h->sig_sync, 0, sizeof(uint32_t) * Tm) != hipSuccess ||
+            hipMemset(h->sig_flag, 0, sizeof(int32_t) * Tm) != hipSuccess)
+            return bail(fail(LCMOE_ERR_HIP, "workspace clear failed"));
+    }
     *out = h;
     return LCMOE_OK;
 }
@@ -526,6 +545,13 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
     // kFastRouterElems multiply-adds per forward the chain router, which
     // reads each router row once per 8 tokens, is the faster one
     const bool fast = route_fast_ok(ra) && (int64_t)T * E * d <= kFastRouterElems;
+    // the sigmoid-group kind's certified router (its weights, like the fast
+    // router's, come from the chains beside gate/up and the combine)
+    RouterArgs rs = ra;
+    rs.bnd = h->sig_bnd;
+    rs.tsync = h->sig_sync;
+    rs.flag = h->sig_flag;
+    const bool sig = !fast && route_sig_ok(rs) && (int64_t)T * E * d <= kSigRouterElems;
     // With the certified fast router, selection, dispatch and activations
     // come from it; the exact chains of the routing weights run in extra
     // blocks beside them, and the combine turns the chains into weights.  The
@@ -559,6 +585,10 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
         ch_g = make_chains(x, h->wrt, h->logits, h->chain_part, T, d, E, kA, d, 8);
         ra.x16 = mfma ? h->x16 : nullptr;
         HIP_TRY(timed(h, st, kSlotRouter, [&] { return launch_route_fast(ra, ch_r, st); }));
+    } else if (sig) {
+        ch_g = make_chains(x, h->wrt, h->logits, h->chain_part, T, d, E, 0, d, 8);
+        rs.x16 = mfma ? h->x16 : nullptr;
+        HIP_TRY(timed(h, st, kSlotRouter, [&] { return launch_route_sig(rs, st); }));
     } else if (route_chains_ok(ra)) {
         ra.x16 = mfma ? h->x16 : nullptr;
         HIP_TRY(timed(h, st, kSlotRouter, [&] { return launch_route_chains(ra, st); }));
@@ -576,7 +606,7 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
         return s;
     const int ks_r = pr.ks, ks_s = ps.ks;
     CombineRoute cr{};
-    if (fast)
+    if (fast || sig)
         cr = CombineRoute{h->logits, h->topk_idx, D.has_bias ? h->bias : nullptr, D.route_kind,
                           E, D.routed_scale};
     HIP_TRY(timed(h, st, kSlotCombine, [&] {
@@ -589,6 +619,7 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
     }));
     h->last_T = T;
     h->last_stream = st;
+    h->last_sig = sig;
     return LCMOE_OK;
 }
 
@@ -966,6 +997,21 @@ extern "C" lcmoe_status lcmoe_debug_rmsnorm(const float *x, const float *w, floa
     for (void *p : {a, b, c})
         if (p) (void)hipFree(p);
     if (e != hipSuccess) return fail(LCMOE_ERR_HIP, "debug_rmsnorm: %s", hipGetErrorString(e));
+    return LCMOE_OK;
+}
+
+extern "C" lcmoe_status lcmoe_debug_route_fallbacks(lcmoe_handle *h, int32_t *count) {
+    clear_error();
+    if (!h || !count) return fail(LCMOE_ERR_INVALID_ARG, "handle or count is NULL");
+    *count = -1;
+    if (!h->last_sig || h->last_T <= 0) return LCMOE_OK;
+    HIP_TRY(hipSetDevice(h->device));
+    HIP_TRY(hipStreamSynchronize(h->last_stream));
+    std::vector<int32_t> f((size_t)h->last_T);
+    HIP_TRY(hipMemcpy(f.data(), h->sig_flag, sizeof(int32_t) * f.size(), hipMemcpyDeviceToHost));
+    int32_t n = 0;
+    for (int32_t v : f) n += v != 0;
+    *count = n;
     return LCMOE_OK;
 }
 

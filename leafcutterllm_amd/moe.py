@@ -128,6 +128,13 @@ class MoeFfn:
             "topk_idx", "topk_w", "counts", "offsets", "perm", "inv"))), "lcmoe_get_dispatch")
         return out
 
+    def route_fallbacks(self) -> int:
+        """Tokens of the last forward that the certified sigmoid-group router
+        left to the exact chain logits; -1 when that forward did not use it."""
+        n = np.zeros(1, np.int32)
+        check(lib().lcmoe_debug_route_fallbacks(self._h, _ptr(n)), "lcmoe_debug_route_fallbacks")
+        return int(n[0])
+
     def set_timing(self, on: bool) -> None:
         check(lib().lcmoe_set_timing(self._h, 1 if on else 0), "lcmoe_set_timing")
 

@@ -581,6 +581,48 @@ float lco_expf_cw(float x) {
 
 float lco_sigmoid_cw(float x) { return 1.0f / (1.0f + lco_expf_cw(-x)); }
 
+/* The largest dip of lco_sigmoid_cw below its running maximum, in units in
+ * the last place: max over x <= y of bits(s(x)) - bits(s(y)) (s >= 0, so
+ * bit patterns order as values), over every non-NaN float taken in
+ * increasing order, -inf .. -0, +0 .. +inf.  A certified router may treat
+ * the function as monotone within this many ulps.  The ordered inputs are
+ * cut into chunks; a dip across chunks is the maximum before a chunk minus
+ * a value inside it. */
+#define LCO_NFLOAT 4278190082ull /* 2 * (0x7f800000 + 1) */
+static float lco_ordered_float(uint64_t n) {
+    return n <= 0x7f800000ull ? u2f((uint32_t)(0xff800000ull - n))
+                              : u2f((uint32_t)(n - 0x7f800001ull));
+}
+int64_t lco_sigmoid_max_dip(int threads) {
+    enum { NCH = 256 };
+    static uint32_t cmax[NCH], cmin[NCH];
+    static int64_t cdip[NCH];
+    if (threads < 1) threads = 1;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
+    for (int c = 0; c < NCH; c++) {
+        const uint64_t n0 = LCO_NFLOAT * (uint64_t)c / NCH, n1 = LCO_NFLOAT * (uint64_t)(c + 1) / NCH;
+        uint32_t run = 0, mn = 0xffffffffu;
+        int64_t dip = 0;
+        for (uint64_t n = n0; n < n1; n++) {
+            const uint32_t b = f2u(lco_sigmoid_cw(lco_ordered_float(n)));
+            if (b > run) run = b;
+            if (b < mn) mn = b;
+            if ((int64_t)run - (int64_t)b > dip) dip = (int64_t)run - (int64_t)b;
+        }
+        cmax[c] = run;
+        cmin[c] = mn;
+        cdip[c] = dip;
+    }
+    int64_t dip = 0;
+    uint32_t before = 0;
+    for (int c = 0; c < NCH; c++) {
+        if (cdip[c] > dip) dip = cdip[c];
+        if ((int64_t)before - (int64_t)cmin[c] > dip) dip = (int64_t)before - (int64_t)cmin[c];
+        if (cmax[c] > before) before = cmax[c];
+    }
+    return dip;
+}
+
 /* ====================================================================== */
 /* Routing.  The reference has no router; the rules below are this          */
 /* project's written semantics (router logits reuse Tensor::matmul,          */

@@ -135,6 +135,9 @@ int lco_shard_matmul(int type, const float *a, const uint8_t *b, float *c, int m
 void lco_softmax(const float *x, float *y, int n);
 float lco_expf_cw(float x);
 float lco_sigmoid_cw(float x);
+/* largest dip of lco_sigmoid_cw below its running maximum over all non-NaN
+ * floats, in ulps (exhaustive; `threads` OpenMP threads) */
+int64_t lco_sigmoid_max_dip(int threads);
 
 /* ---- routing ---------------------------------------------------------- */
 void lco_router_logits(const float *x, const float *w, float *l, int T, int d, int E);

@@ -78,6 +78,7 @@ def lib() -> C.CDLL:
             "lco_softmax": (None, [vp, vp, i32]),
             "lco_expf_cw": (f32, [f32]),
             "lco_sigmoid_cw": (f32, [f32]),
+            "lco_sigmoid_max_dip": (C.c_int64, [i32]),
             "lco_router_logits": (None, [vp, vp, vp, i32, i32, i32]),
             "lco_route": (i32, [C.POINTER(Desc), vp, vp, i32, vp, vp]),
             "lco_dispatch": (i32, [vp, i32, i32, i32, vp, vp, vp, vp]),
@@ -199,6 +200,12 @@ def expf_cw(x: np.ndarray) -> np.ndarray:
 def sigmoid_cw(x: np.ndarray) -> np.ndarray:
     f = lib().lco_sigmoid_cw
     return np.array([f(float(v)) for v in np.asarray(x, np.float32).ravel()], np.float32)
+
+
+def sigmoid_max_dip(threads: int = 8) -> int:
+    """Exhaustive: the largest dip of sigmoid_cw below its running maximum
+    over every non-NaN float, in ulps (lco_sigmoid_max_dip)."""
+    return int(lib().lco_sigmoid_max_dip(threads))
 
 
 def router_logits(x: np.ndarray, w: np.ndarray) -> np.ndarray:

@@ -205,6 +205,73 @@ def test_router_fallback_with_chain_split(T):
         assert np.all(np.argmax(idx[rows] == 0, axis=1) < np.argmax(idx[rows] == 1, axis=1))
 
 
+# ------------------------------------------ certified sigmoid-group router --
+
+SIG_CFG = small_config("sig64", 512, 256, 64, 8, L.ROUTE_SIGMOID_GROUP, Q4, Q6, n_shared=1,
+                       d_ff_shared=256, n_group=8, topk_group=4, routed_scale=2.5,
+                       bias="normal0.1")
+
+
+@pytest.mark.parametrize("T", [1, 5, 32, 100])
+def test_sigmoid_certified_router(T):
+    """float64 bounds settle the group and expert selection of (nearly) every
+    token; routing, dispatch and weights equal the oracle's exact chains."""
+    layer = L.synth_layer(SIG_CFG, seed=31)
+    x = L.synth_x(SIG_CFG, T, seed=31, index=T)
+    with L.MoeFfn(SIG_CFG.desc(T), layer) as moe:
+        res = run_and_check(SIG_CFG, layer, x, moe=moe)
+        fb = moe.route_fallbacks()
+    assert res["rel_l2"] < 1e-3
+    assert 0 <= fb <= max(1, T // 8), fb
+
+
+@pytest.mark.parametrize("T", [1, 7, 40])
+def test_sigmoid_router_exact_ties_fall_back(T):
+    """Experts 0 and 1 (group 0) share a router row and a +1 bias: their keys
+    tie exactly and lead every token, so no float64 bound can order them and
+    every token takes the exact chains, which rank 0 before 1."""
+    layer = L.synth_layer(SIG_CFG, seed=32)
+    r = layer["router"].copy()
+    r[:, 1] = r[:, 0]
+    layer["router"] = r
+    b = layer["bias"].copy()
+    b[0] = b[1] = 1.0
+    layer["bias"] = b
+    x = L.synth_x(SIG_CFG, T, seed=32, index=T)
+    with L.MoeFfn(SIG_CFG.desc(T), layer) as moe:
+        res = run_and_check(SIG_CFG, layer, x, moe=moe)
+        assert moe.route_fallbacks() == T
+    idx = res["topk_idx"].reshape(T, SIG_CFG.n_expert_used)
+    assert np.all(idx[:, 0] == 0) and np.all(idx[:, 1] == 1)
+
+
+def test_sigmoid_router_mixed_tokens():
+    """Every third token is the one-hot x = e_0, whose logits are row 0 of
+    the router: experts 0 and 1 share the top logit 50 and the bias, an exact
+    tie for the exact chains to settle; the other tokens (x[0] = 0) certify.
+    The chain and select launches serve exactly the marked tokens, and every
+    token is dispatched."""
+    T = 24
+    layer = L.synth_layer(SIG_CFG, seed=33)
+    r = layer["router"].copy()
+    r[0, :2] = 50.0
+    layer["router"] = r
+    b = layer["bias"].copy()
+    b[1] = b[0]
+    layer["bias"] = b
+    x = L.synth_x(SIG_CFG, T, seed=33, index=T)
+    x[:, 0] = 0.0
+    tied = np.arange(T) % 3 == 0
+    x[tied] = 0.0
+    x[tied, 0] = 1.0
+    with L.MoeFfn(SIG_CFG.desc(T), layer) as moe:
+        res = run_and_check(SIG_CFG, layer, x, moe=moe)
+        fb = moe.route_fallbacks()
+    idx = res["topk_idx"].reshape(T, SIG_CFG.n_expert_used)
+    assert np.all(idx[tied, 0] == 0) and np.all(idx[tied, 1] == 1)
+    assert int(tied.sum()) <= fb <= int(tied.sum()) + max(1, T // 8), fb
+
+
 def test_e1_k1_reduces_to_dense_ffn():
     """E = 1, K = 1, renormalised: weight exactly 1.0 and the layer is the
     dense SwiGLU ffn_forward (engine.rs:146-164) of the one expert."""
@@ -254,14 +321,19 @@ def test_full_config_parity(full_layers, c, T):
     print(f"config {c} T={T}: rel_l2={res['rel_l2']:.2e} touched={int((res['counts'] > 0).sum())}")
 
 
-@pytest.mark.parametrize("T", [1, 32, 256])
+@pytest.mark.parametrize("T", [1, 4, 32, 256])
 def test_full_config4_parity(full_layers, T):
     """DeepSeek-V3 shape: sigmoid-group router over 256 experts, Q6_K down
     (matrix-core Q6_K path), one shared expert."""
     cfg, layer, moe = full_layers(4)
     x = L.synth_x(cfg, T, seed=0, index=T)
     res = run_and_check(cfg, layer, x, moe=moe)
-    print(f"config 4 T={T}: rel_l2={res['rel_l2']:.2e} touched={int((res['counts'] > 0).sum())}")
+    fb = moe.route_fallbacks()
+    # decode batches route through the certified sigmoid-group router (T * E
+    # * d within its limit), larger ones through the exact chains alone
+    assert fb == -1 if T > 18 else 0 <= fb <= max(1, T // 8), fb
+    print(f"config 4 T={T}: rel_l2={res['rel_l2']:.2e} touched={int((res['counts'] > 0).sum())} "
+          f"uncertified={fb}")
 
 
 def test_full_config3_prefill_parity(full_layers):

@@ -395,3 +395,17 @@ def test_routed_scale_and_shared_expert_add():
                             "gate": lay["gate_sh"], "up": lay["up_sh"], "down": lay["down_sh"]},
                            x)["y"]
     assert rel_l2(ysh, y1.astype(np.float64) + shared) < 1e-6
+
+
+def test_sigmoid_cw_dips_at_most_one_ulp():
+    """The certified sigmoid-group router treats sigmoid_cw as monotone up to
+    one ulp: its scores bound s(c) for c in [zlo, zhi] by one ulp below
+    s(zlo) and above s(zhi).  Exhaustively, over every non-NaN float32 input
+    in increasing order, the function never falls more than one ulp below
+    its running maximum; and it does dip (so the widening is needed): the two
+    adjacent inputs below step down by exactly one ulp."""
+    lo = np.float32(0.0614658967)
+    hi = np.nextafter(lo, np.float32(1.0))
+    s = O.sigmoid_cw(np.array([lo, hi], np.float32))
+    assert s.view(np.uint32)[0] - s.view(np.uint32)[1] == 1
+    assert O.sigmoid_max_dip(8) == 1
