@@ -249,7 +249,8 @@ def e2e_bench(args) -> None:
         "value": head["decode_tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
         "steps": n_new - 1, "warmup": 1, "ms_per_step": head["ms_per_decode_step"],
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f32 (Q4_K weights; MoE products f16 hi+lo on MFMA; f16 KV cache)",
+        "dtype": ("f32 (Q4_K weights; MoE products exact int8 dot4 on 15-bit activation limbs "
+                  "when T*K <= E, f16 hi+lo activations on MFMA above; f16 KV cache)"),
         "data": "synthetic (seeded N(0,0.02) weights quantised to Q4_K, random prompt ids)",
         "config": {"workload": f"config 5: {mc.note}, prompt {P}, {n_new} greedy tokens, "
                                f"B={max(batches)}", "entry": "lcmoe_model_generate",
@@ -281,6 +282,8 @@ def main():
                          "the layer and the residual add) instead of lcmoe_forward_dev")
     ap.add_argument("--kernel-events", type=int, default=1,
                     help="time each kernel with HIP events in a second timed region")
+    ap.add_argument("--read-probe", action="store_true",
+                    help="only measure the HBM streaming-read rate over 64 MiB - 1 GiB slices")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run device-to-device copies of this size (FETCH_SIZE calibration)")
     ap.add_argument("--shard-matmul", default="", metavar="TYPE,M,K,N",
@@ -296,6 +299,12 @@ def main():
                          "(for profilers that cannot trace graph launches)")
     args = ap.parse_args()
 
+    if args.read_probe:
+        import leafcutterllm_amd as LP
+        print(json.dumps({"stream_read_GBps": {str(m): round(LP.read_bandwidth(m, reps=16), 1)
+                                               for m in (64, 128, 256, 512, 1024)},
+                          "peak_GBps": HBM_PEAK_GBS}), flush=True)
+        return
     if args.copy_probe:
         copy_probe(args.copy_probe)
         return
@@ -405,6 +414,8 @@ def main():
 
     head = per_batch[args.tokens]
     T = args.tokens
+    qname = {L.TYPE_Q8_0: "Q8_0", L.TYPE_Q4_K: "Q4_K", L.TYPE_Q6_K: "Q6_K", L.TYPE_F32: "F32"}
+    gq = qname[cfg.qtype_gate]
     gu_flops = 4 * cfg.d_model * cfg.d_ff * T * cfg.n_expert_used
     gu_weight_bytes = (head["gateup_bytes"] - 4 * T * cfg.d_model
                        - 4 * T * cfg.n_expert_used * cfg.d_ff)
@@ -413,7 +424,7 @@ def main():
         # are bound by the f16 dense MFMA peak, not by streaming the weights
         roof = {
             "bound": "mfma",
-            "kernel": "routed gate/up launch (k_mfma_gateup: Q4_K dequant + gate/up + SwiGLU)",
+            "kernel": f"routed gate/up launch (k_mfma_gateup: {gq} dequant + gate/up + SwiGLU)",
             "achieved": round(gu_flops / (head["gateup_ms"] * 1e-3) / 1e12, 2),
             "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(gu_flops / (head["gateup_ms"] * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
@@ -426,7 +437,7 @@ def main():
     else:
         roof = {
             "bound": "hbm",
-            "kernel": "gate/up launch (fused Q4_K dequant + gate/up products + SwiGLU)",
+            "kernel": f"gate/up launch (fused {gq} dequant + gate/up products + SwiGLU)",
             "achieved": round(head["gateup_GBps"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -435,7 +446,6 @@ def main():
             "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
             "algorithmic_bytes": round(head["gateup_bytes"]),
         }
-    qname = {L.TYPE_Q8_0: "Q8_0", L.TYPE_Q4_K: "Q4_K", L.TYPE_Q6_K: "Q6_K", L.TYPE_F32: "F32"}
     qdesc = qname[cfg.qtype_gate] + ("" if cfg.qtype_down == cfg.qtype_gate
                                      else f" gate/up, {qname[cfg.qtype_down]} down")
     metric = ("MoE-layer tokens/s + % HBM roofline, Mixtral-shape Q4_K, batch 1-64"
@@ -453,7 +463,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 (f16 hi+lo activation halves x exact f16 sc*q weights on MFMA, f32 accumulate)",
+        "dtype": ("f32 in/out; expert products on exact weights (f16 sc*q) with f16 hi+lo "
+                  "activations (~22 bits) on MFMA when T*K > E, exact int8 dot4 on 15-bit "
+                  "two-limb activations when T*K <= E; f32 accumulate"),
         "data": ("synthetic (seeded splitmix64 N(0,1) activations, N(0,0.02) weights quantised "
                  f"to {qdesc})"),
         "config": {
@@ -475,6 +487,14 @@ def main():
     }
     for m in moes:
         m.close()
+    if roof["bound"] == "hbm":
+        # the practical ceiling beside the 8 TB/s peak: a plain streaming read
+        # of slices the size of the dominant launch's bytes (past the MALL)
+        sl = max(16, min(1024, int(round(roof["algorithmic_bytes"] / 2 ** 24)) * 16))
+        bw = L.read_bandwidth(sl, reps=8)
+        roof["stream_read_GBps"] = round(bw, 1)
+        roof["stream_read_slice_MiB"] = sl
+        roof["frac_of_stream"] = round(roof["achieved"] / bw, 4)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(cfg, layer, sweep, args.tokens)
     print(json.dumps(out), flush=True)

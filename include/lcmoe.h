@@ -423,6 +423,13 @@ lcmoe_status lcmoe_debug_rmsnorm(const float *x, const float *w, float eps, int3
                                  float *out);
 /* The router's sigmoid evaluated on the device, for host/device bit parity. */
 lcmoe_status lcmoe_debug_sigmoid(const float *x, int64_t n, float *out);
+/* HBM streaming-read rate: reads `slice_bytes` (a multiple of 16 MiB, at
+ * most 1 GiB) of a 4 GiB device buffer per launch with a plain 16-byte-load
+ * kernel, each launch a different slice (past the 256 MB MALL), `reps`
+ * launches after two unmeasured ones; *gbps = bytes / mean launch time by
+ * HIP events.  The practical ceiling the expert kernels are compared with.
+ * No counterpart in the reference. */
+lcmoe_status lcmoe_debug_read_bandwidth(int64_t slice_bytes, int32_t reps, double *gbps);
 /* Tokens of the handle's last forward whose expert selection the certified
  * sigmoid-group router left to the exact chain logits (their float64 bounds
  * could not order the decision); -1 when that forward did not use it.  Waits

@@ -36,7 +36,7 @@ EXPORTS = (
     "lcmoe_shard_matmul_split_noalloc_dev", "lcmoe_model_create", "lcmoe_model_destroy",
     "lcmoe_model_reset", "lcmoe_model_forward", "lcmoe_model_generate",
     "lcmoe_model_last_timing", "lcmoe_model_set_decode_graph", "lcmoe_matmul_f32",
-    "lcmoe_matmul_f32_dev", "lcmoe_debug_route_fallbacks",
+    "lcmoe_matmul_f32_dev", "lcmoe_debug_route_fallbacks", "lcmoe_debug_read_bandwidth",
 )
 
 
@@ -104,6 +104,7 @@ def lib() -> C.CDLL:
         "lcmoe_debug_dequant": (i32, [i32, vp, i64, vp]),
         "lcmoe_debug_sigmoid": (i32, [vp, i64, vp]),
         "lcmoe_debug_route_fallbacks": (i32, [vp, vp]),
+        "lcmoe_debug_read_bandwidth": (i32, [i64, i32, vp]),
         "lcmoe_debug_rmsnorm": (i32, [vp, vp, f32, i32, i32, vp]),
         "lcmoe_set_norm": (i32, [vp, vp, f32]),
         "lcmoe_shard_matmul": (i32, [i32, vp, vp, vp, i32, i32, i32]),

@@ -300,6 +300,35 @@ hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int T, int 
     return hipGetLastError();
 }
 
+// Streaming-read probe: block b reads its contiguous share of `n` 16-byte
+// words, eight loads in flight per lane, and folds them into a word that is
+// stored only if it matches a value no input produces here (the loads stay
+// live, nothing is written).
+__global__ __launch_bounds__(256) void k_stream_read(const uint4 *__restrict__ p, int64_t n,
+                                                     uint32_t *__restrict__ sink) {
+    const int64_t per = (n + gridDim.x - 1) / gridDim.x, b0 = per * blockIdx.x;
+    const int64_t b1 = b0 + per < n ? b0 + per : n;
+    uint32_t acc = 0;
+    for (int64_t i = b0 + threadIdx.x; i < b1; i += 256 * 8) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int64_t j = i + 256 * u;
+            v[u] = j < b1 ? p[j] : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;
+}
+
+hipError_t launch_stream_read(const void *p, int64_t bytes, int blocks, uint32_t *sink,
+                              hipStream_t st) {
+    hipLaunchKernelGGL(k_stream_read, dim3(blocks), dim3(256), 0, st,
+                       reinterpret_cast<const uint4 *>(p), bytes / 16, sink);
+    return hipGetLastError();
+}
+
 hipError_t launch_debug_dequant(int qt, const uint8_t *src, int64_t count, float *out,
                                 hipStream_t st) {
     int64_t groups = count / 8;

@@ -185,6 +185,10 @@ int64_t attention_part_floats(int nq, int H, int hd, int ctx);
 hipError_t launch_debug_dequant(int qt, const uint8_t *src, int64_t count, float *out,
                                 hipStream_t st);
 hipError_t launch_debug_sigmoid(const float *x, int64_t n, float *out, hipStream_t st);
+// Streaming-read probe over `bytes` (a multiple of 16) at p; sink: `blocks`
+// words, written only on an impossible match.
+hipError_t launch_stream_read(const void *p, int64_t bytes, int blocks, uint32_t *sink,
+                              hipStream_t st);
 
 // RPL64 eligibility: Q4_K, rows tile by 64, columns are whole super-blocks.
 inline bool rpl64_ok(int qt, int64_t rows, int64_t cols) {

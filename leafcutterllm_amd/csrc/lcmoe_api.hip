@@ -1000,6 +1000,44 @@ extern "C" lcmoe_status lcmoe_debug_rmsnorm(const float *x, const float *w, floa
     return LCMOE_OK;
 }
 
+extern "C" lcmoe_status lcmoe_debug_read_bandwidth(int64_t slice_bytes, int32_t reps,
+                                                   double *gbps) {
+    clear_error();
+    const int64_t total = (int64_t)4 << 30, mib16 = (int64_t)16 << 20;
+    if (!gbps || reps < 1 || slice_bytes < mib16 || slice_bytes % mib16 ||
+        slice_bytes > ((int64_t)1 << 30))
+        return fail(LCMOE_ERR_INVALID_ARG, "slice of 16 MiB multiples up to 1 GiB, reps >= 1");
+    int dev = 0, cus = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    const int blocks = 4 * std::max(cus, 1);
+    void *buf = nullptr, *sink = nullptr;
+    hipEvent_t a = nullptr, b = nullptr;
+    hipError_t e = hipMalloc(&buf, total);
+    if (e == hipSuccess) e = hipMalloc(&sink, sizeof(uint32_t) * blocks);
+    if (e == hipSuccess) e = hipMemset(buf, 1, total);
+    if (e == hipSuccess) e = hipEventCreate(&a);
+    if (e == hipSuccess) e = hipEventCreate(&b);
+    const int64_t nslice = total / slice_bytes;
+    float ms = 0.0f;
+    for (int r = 0; e == hipSuccess && r < reps + 2; r++) {
+        if (r == 2) e = hipEventRecord(a, nullptr);
+        if (e == hipSuccess)
+            e = launch_stream_read((const char *)buf + (r % nslice) * slice_bytes, slice_bytes,
+                                   blocks, (uint32_t *)sink, nullptr);
+    }
+    if (e == hipSuccess) e = hipEventRecord(b, nullptr);
+    if (e == hipSuccess) e = hipEventSynchronize(b);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    if (buf) (void)hipFree(buf);
+    if (sink) (void)hipFree(sink);
+    if (e != hipSuccess) return fail(LCMOE_ERR_HIP, "read probe: %s", hipGetErrorString(e));
+    *gbps = (double)slice_bytes * reps / (ms * 1e-3) / 1e9;
+    return LCMOE_OK;
+}
+
 extern "C" lcmoe_status lcmoe_debug_route_fallbacks(lcmoe_handle *h, int32_t *count) {
     clear_error();
     if (!h || !count) return fail(LCMOE_ERR_INVALID_ARG, "handle or count is NULL");

@@ -201,6 +201,15 @@ def shard_matmul(qtype: int, a: np.ndarray, b: np.ndarray, k: int, n: int) -> np
     return out
 
 
+def read_bandwidth(slice_mib: int, reps: int = 8) -> float:
+    """HBM streaming-read rate in GB/s over distinct `slice_mib` MiB slices
+    (lcmoe_debug_read_bandwidth)."""
+    out = np.zeros(1, np.float64)
+    check(lib().lcmoe_debug_read_bandwidth(slice_mib << 20, reps, _ptr(out)),
+          "lcmoe_debug_read_bandwidth")
+    return float(out[0])
+
+
 def matmul(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     """Backend::matmul (rust/src/backend/mod.rs:18-46) on the GPU:
     a [m, k] @ b [k, n] in f32, bit-identical to the x86 CPU backend

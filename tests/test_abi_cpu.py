@@ -221,3 +221,15 @@ def test_matmul_f32_argument_errors():
     assert lib.lcmoe_matmul_f32(None, None, None, 0, 5, 3) == 0   # empty: nothing to do
     st = lib.lcmoe_matmul_f32_dev(6, 4, 4, 1, 1, 1, None)        # misaligned a
     assert _lib.STATUS[st] == "LCMOE_ERR_INVALID_ARG"
+
+
+def test_read_bandwidth_argument_errors():
+    """lcmoe_debug_read_bandwidth validates its slice and repeat count before
+    touching a device."""
+    lib = L.lib()
+    out = np.zeros(1, np.float64)
+    mib = 1 << 20
+    for slice_bytes, reps in [(8 * mib, 4), (24 * mib, 4), (2048 * mib, 4), (64 * mib, 0)]:
+        st = lib.lcmoe_debug_read_bandwidth(slice_bytes, reps, out.ctypes.data)
+        assert _lib.STATUS[st] == "LCMOE_ERR_INVALID_ARG", (slice_bytes, reps)
+    assert _lib.STATUS[lib.lcmoe_debug_read_bandwidth(64 * mib, 4, None)] == "LCMOE_ERR_INVALID_ARG"
