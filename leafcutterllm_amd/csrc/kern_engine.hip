@@ -17,6 +17,8 @@
 // step is the same launch sequence every time (it is captured once into a
 // HIP graph and replayed).
 
+#include <algorithm>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -388,6 +390,26 @@ __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ logit
     }
 }
 
+// Y[t, :N] = (R[t] +) sum over slices z in order of part[z][t, :N]; one
+// float4 of columns per thread, grid (column blocks of 1024, T)
+__global__ __launch_bounds__(256) void k_linear_reduce(const float *__restrict__ part, int ks,
+                                                       int64_t stride, int N, const float *R,
+                                                       float *Y, int64_t ldy) {
+    const int t = blockIdx.y, c4 = blockIdx.x * 256 + threadIdx.x;
+    if (4 * c4 >= N) return;
+    const float4 *p = reinterpret_cast<const float4 *>(part + (int64_t)t * N) + c4;
+    float4 s = p[0];
+    for (int z = 1; z < ks; z++) {
+        const float4 u = p[z * stride / 4];
+        s.x = s.x + u.x; s.y = s.y + u.y; s.z = s.z + u.z; s.w = s.w + u.w;
+    }
+    if (R) {  // hidden + attn W_o (Tensor::add, engine.rs:106); R may be Y
+        const float4 r = reinterpret_cast<const float4 *>(R + (int64_t)t * ldy)[c4];
+        s.x = r.x + s.x; s.y = r.y + s.y; s.z = r.z + s.z; s.w = r.w + s.w;
+    }
+    reinterpret_cast<float4 *>(Y + (int64_t)t * ldy)[c4] = s;
+}
+
 // lens[seq0 .. seq0 + nseq) += T; *step += dstep
 __global__ void k_advance(int32_t *lens, int seq0, int nseq, int T, int32_t *step, int dstep) {
     const int b = threadIdx.x;
@@ -445,6 +467,47 @@ hipError_t launch_linear(int qt, const uint8_t *W, int N, int K, const float *X,
     case LCMOE_TYPE_Q8_0: linear_tc<LCMOE_TYPE_Q8_0>(W, rb, N, K, X, ldx, T, R, Y, ldy, st); break;
     default: linear_tc<LCMOE_TYPE_F32>(W, rb, N, K, X, ldx, T, R, Y, ldy, st);
     }
+    return hipGetLastError();
+}
+
+// One 32-token pass per block (pass groups of the down kernel); K split
+// while the grid holds fewer than 256 blocks (one CU each), at least one
+// super-block per slice.
+static void linear_mfma_plan(int N, int K, int T, int &chunks, int &ks) {
+    chunks = std::min(64, std::max(1, (T + 31) / 32));
+    const int base = (N / 64 + 3) / 4 * chunks, NB = K / 256;
+    ks = 1;
+    while (ks * 2 <= NB && base * ks < 256) ks *= 2;
+}
+
+// the largest partials buffer any batch of up to T rows needs
+int64_t linear_mfma_part_floats(int N, int K, int T) {
+    int64_t most = 0;
+    for (int t = 2; t <= T; t++) {
+        int chunks, ks;
+        linear_mfma_plan(N, K, t, chunks, ks);
+        most = std::max(most, (int64_t)ks * t * N);
+    }
+    return most;
+}
+
+hipError_t launch_linear_mfma(const uint8_t *Wr, int N, int K, const float *X, int T,
+                              const float *R, float *Y, int64_t ldy, _Float16 *x16, _Float16 *xs,
+                              float *part, hipStream_t st) {
+    if (T <= 0 || N <= 0) return hipSuccess;
+    if (!linear_mfma_ok(N, K) || ldy % 4) return hipErrorInvalidValue;
+    int chunks, ks;
+    linear_mfma_plan(N, K, T, chunks, ks);
+    hipError_t e = launch_act16(X, T, K, x16, xs, st);
+    if (e != hipSuccess) return e;
+    // one slot of T tokens (the shared-expert form of the slot arguments)
+    const SlotArgsHost sa{nullptr, nullptr, nullptr, nullptr, 1, 1, T, 1, 1, 0, INT32_MAX, 1, 32};
+    const bool direct = ks == 1 && !R && ldy == N;
+    const int64_t stride = (int64_t)T * N;
+    e = launch_mfma_down(Wr, 0, x16, xs, sa, 1, chunks, N, K, ks, direct ? Y : part, stride, st);
+    if (e != hipSuccess || direct) return e;
+    hipLaunchKernelGGL(k_linear_reduce, dim3((N / 4 + 255) / 256, T), dim3(256), 0, st, part, ks,
+                       stride, N, R, Y, ldy);
     return hipGetLastError();
 }
 

@@ -170,6 +170,18 @@ hipError_t launch_embed(int qt, const uint8_t *table, int vocab, int d, const in
 // Y[t, :N] (+= R) = X[t, :K] W^T, W GGUF [N, K] of type qt with K whole blocks
 hipError_t launch_linear(int qt, const uint8_t *W, int N, int K, const float *X, int64_t ldx, int T,
                          const float *R, float *Y, int64_t ldy, hipStream_t st);
+// Matrix-core linear for batches: Y[t, :N] (= or R[t] +) X[t, :K] W^T for
+// Q4_K W [N, K] in the RPL64 layout (linear_mfma_ok), X rows contiguous
+// (ld K).  X goes to f16 hi/lo pieces in x16 / xs (T * K * 2 and
+// T * K / 16 halves), the product runs on the matrix-core down kernel (one
+// slot holding all T tokens), K split into ks slices when that fills the
+// GPU better; part (linear_mfma_part_floats(N, K, most rows)) takes the slices' partials,
+// which a reduce adds in slice order (then R) into Y (row stride ldy).
+inline bool linear_mfma_ok(int64_t N, int64_t K) { return N % 64 == 0 && K % 256 == 0; }
+int64_t linear_mfma_part_floats(int N, int K, int T);
+hipError_t launch_linear_mfma(const uint8_t *Wr, int N, int K, const float *X, int T,
+                              const float *R, float *Y, int64_t ldy, _Float16 *x16, _Float16 *xs,
+                              float *part, hipStream_t st);
 hipError_t launch_rope_kv(const float *qkv, int nq, int T, int seq0, const int32_t *lens, int H,
                           int KVH, int hd, const float *freq, int absolute, float *qo,
                           _Float16 *kc, _Float16 *vc, int ctx, hipStream_t st);

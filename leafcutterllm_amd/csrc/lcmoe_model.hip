@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 #include <new>
 #include <vector>
 
@@ -33,11 +34,16 @@ struct lcmoe_model {
     std::vector<void *> allocs;
     struct Layer {
         uint8_t *wqkv = nullptr, *wo = nullptr;  // q, k, v rows stacked; o
+        // the same Q4_K matrices in the RPL64 layout for the matrix-core
+        // linears of batches (null where the shapes do not fit)
+        uint8_t *wqkv_r = nullptr, *wo_r = nullptr;
         float *attn_norm = nullptr;
         lcmoe_handle *moe = nullptr;
     };
     std::vector<Layer> layers;
-    uint8_t *embd = nullptr, *out_w = nullptr;
+    uint8_t *embd = nullptr, *out_w = nullptr, *out_r = nullptr;
+    _Float16 *x16 = nullptr, *xs16 = nullptr;  // activations of the matrix-core linears
+    float *lpart = nullptr;                    // their K-slice partials
     float *out_norm = nullptr, *freq = nullptr;
     _Float16 *kc = nullptr, *vc = nullptr;  // [layer][seq][ctx][kv head][head_dim]
     int32_t *lens = nullptr, *step = nullptr, *tok = nullptr, *next = nullptr, *out_tok = nullptr;
@@ -151,20 +157,27 @@ lcmoe_status forward_dev(lcmoe_model *m, int seq0, int nseq, int T, const int32_
     const int nq = nseq * T, qt = D.attn_type, nqkv = (H + 2 * KVH) * hd;
     const int64_t cache_layer = (int64_t)D.max_batch * D.max_ctx * KVH * hd;
     hipStream_t st = m->stream;
+    // Y (= or R +) X W^T over `rows` rows of X (ld K): the matrix-core linear
+    // for batches of rows when W has its RPL64 copy, else launch_linear
+    auto linear = [&](const uint8_t *W, const uint8_t *Wr, int N, int K, const float *X, int rows,
+                      const float *R, float *Y, int64_t ldy) {
+        if (Wr && rows >= 2)
+            return launch_linear_mfma(Wr, N, K, X, rows, R, Y, ldy, m->x16, m->xs16, m->lpart, st);
+        return launch_linear(qt, W, N, K, X, K, rows, R, Y, ldy, st);
+    };
     HIP_TRY(launch_embed(qt, m->embd, V, d, tok, nq, m->hidden, st));
     for (int l = 0; l < D.n_layer; l++) {
         const auto &L = m->layers[l];
         _Float16 *kc = m->kc + l * cache_layer, *vc = m->vc + l * cache_layer;
         HIP_TRY(launch_rmsnorm(m->hidden, L.attn_norm, D.norm_eps, nq, d, m->xn, st));
-        HIP_TRY(launch_linear(qt, L.wqkv, nqkv, d, m->xn, d, nq, nullptr, m->qkv, nqkv, st));
+        HIP_TRY(linear(L.wqkv, L.wqkv_r, nqkv, d, m->xn, nq, nullptr, m->qkv, nqkv));
         HIP_TRY(launch_rope_kv(m->qkv, nq, T, seq0, m->lens, H, KVH, hd, m->freq,
                                D.rope_positions == LCMOE_ROPE_ABSOLUTE, m->qr, kc, vc, D.max_ctx,
                                st));
         HIP_TRY(launch_attention(m->qr, nq, T, seq0, m->lens, H, KVH, hd, kc, vc, D.max_ctx,
                                  m->part, m->attn, st));
         // hidden += attn W_o (Tensor::add, engine.rs:106)
-        HIP_TRY(launch_linear(qt, L.wo, d, H * hd, m->attn, H * hd, nq, m->hidden, m->hidden, d,
-                              st));
+        HIP_TRY(linear(L.wo, L.wo_r, d, H * hd, m->attn, nq, m->hidden, m->hidden, d));
         // hidden += ffn(rms_norm(hidden)) (engine.rs:109-115)
         lcmoe_status s = lcmoe_forward_norm_residual_dev(L.moe, m->hidden, nq, m->hidden, st);
         if (s) return s;
@@ -172,7 +185,7 @@ lcmoe_status forward_dev(lcmoe_model *m, int seq0, int nseq, int T, const int32_
     // the final norm and lm_head of each sequence's last token
     const float *last = m->hidden + (int64_t)(T - 1) * d;  // nseq == 1, or T == 1
     HIP_TRY(launch_rmsnorm(last, m->out_norm, D.norm_eps, nseq, d, m->xn, st));
-    HIP_TRY(launch_linear(qt, m->out_w, V, d, m->xn, d, nseq, nullptr, m->logits, V, st));
+    HIP_TRY(linear(m->out_w, m->out_r, V, d, m->xn, nseq, nullptr, m->logits, V));
     HIP_TRY(launch_argmax(m->logits, nseq, V, seq0, m->next, rec ? m->out_tok : nullptr,
                           D.max_ctx, m->step, st));
     HIP_TRY(launch_advance(m->lens, seq0, nseq, T, m->step, dstep, st));
@@ -231,6 +244,20 @@ extern "C" lcmoe_status lcmoe_model_create(const lcmoe_model_desc *desc,
     if ((st = upload(m, &m->embd, w->token_embd, row_d * V))) return bail(st);
     if ((st = upload(m, &m->out_w, w->output, row_d * V))) return bail(st);
     if ((st = upload(m, &m->out_norm, w->output_norm, 4 * (size_t)d))) return bail(st);
+    // RPL64 copies of the Q4_K linears for the matrix-core path of batches
+    const bool q4 = qt == LCMOE_TYPE_Q4_K;
+    const int nqkv = (H + 2 * KVH) * hd;
+    const bool r_qkv = q4 && linear_mfma_ok(nqkv, d), r_o = q4 && linear_mfma_ok(d, H * hd),
+               r_out = q4 && linear_mfma_ok(V, d);
+    std::vector<uint8_t> host, rpl;
+    auto upload_rpl = [&](uint8_t **dst, const uint8_t *src, int64_t rows, int64_t cols) {
+        const size_t bytes = lcmoe_tensor_size(qt, cols) * rows;
+        rpl.resize(bytes);
+        repack_rpl64_q4k(src, rpl.data(), rows, cols);
+        return upload(m, dst, rpl.data(), bytes);
+    };
+    if (r_out && (st = upload_rpl(&m->out_r, static_cast<const uint8_t *>(w->output), V, d)))
+        return bail(st);
     lcmoe_desc md = D.moe;
     md.max_tokens = m->tmax;
     m->layers.resize(D.n_layer);
@@ -244,6 +271,15 @@ extern "C" lcmoe_status lcmoe_model_create(const lcmoe_model_desc *desc,
             hipMemcpy(ML.wqkv + bq + bkv, L.attn_v, bkv, hipMemcpyHostToDevice) != hipSuccess)
             return bail(fail(LCMOE_ERR_HIP, "layer %d: attention upload failed", l));
         if ((st = upload(m, &ML.wo, L.attn_o, row_q * d))) return bail(st);
+        if (r_qkv) {
+            host.resize(bq + 2 * bkv);
+            std::memcpy(host.data(), L.attn_q, bq);
+            std::memcpy(host.data() + bq, L.attn_k, bkv);
+            std::memcpy(host.data() + bq + bkv, L.attn_v, bkv);
+            if ((st = upload_rpl(&ML.wqkv_r, host.data(), nqkv, d))) return bail(st);
+        }
+        if (r_o && (st = upload_rpl(&ML.wo_r, static_cast<const uint8_t *>(L.attn_o), d, H * hd)))
+            return bail(st);
         if ((st = upload(m, &ML.attn_norm, L.attn_norm, 4 * (size_t)d))) return bail(st);
         if ((st = lcmoe_create(&md, &L.moe, &ML.moe))) return bail(st);
         if ((st = lcmoe_set_norm(ML.moe, L.ffn_norm, D.norm_eps))) return bail(st);
@@ -260,6 +296,16 @@ extern "C" lcmoe_status lcmoe_model_create(const lcmoe_model_desc *desc,
         (st = alloc_n(m, &m->part, attention_part_floats((int)T, H, hd, D.max_ctx))) ||
         (st = alloc_n(m, &m->logits, (size_t)D.max_batch * V)))
         return bail(st);
+    if (r_qkv || r_o || r_out) {
+        const int64_t kmax = std::max<int64_t>(d, (int64_t)H * hd);
+        int64_t part = 0;
+        if (r_qkv) part = std::max(part, linear_mfma_part_floats(nqkv, d, (int)T));
+        if (r_o) part = std::max(part, linear_mfma_part_floats(d, H * hd, (int)T));
+        if (r_out) part = std::max(part, linear_mfma_part_floats(V, d, D.max_batch));
+        if ((st = alloc_n(m, &m->x16, 2 * T * kmax)) || (st = alloc_n(m, &m->xs16, T * kmax / 16)) ||
+            (st = alloc_n(m, &m->lpart, part)))
+            return bail(st);
+    }
     m->lens_h.assign(D.max_batch, 0);
     if ((st = reset(m))) return bail(st);
     *out = m;
