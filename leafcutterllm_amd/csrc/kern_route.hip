@@ -1217,7 +1217,12 @@ __global__ __launch_bounds__(64 * kSelWaves) void k_route_select(RouterArgs a) {
         }
         return;
     }
-    __threadfence();  // every selection released at device scope before the count
+    // the selections were published with coherent stores (store_agent) and
+    // dispatch_block reads them with coherent loads: once every wave's
+    // stores have completed the count may advance, with no L2 write-back or
+    // invalidate (a device-scope fence in each of the T / 8 blocks costs
+    // tens of us)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
         const unsigned old = atomicAdd(&a.sync[0], 1u);
@@ -1225,7 +1230,6 @@ __global__ __launch_bounds__(64 * kSelWaves) void k_route_select(RouterArgs a) {
     }
     __syncthreads();
     if (!s_flag) return;
-    __threadfence();
     dispatch_block<64 * kSelWaves>(a, s_cw, s_off);
     if (tid == 0) a.sync[0] = 0;
 }
