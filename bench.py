@@ -26,15 +26,23 @@ MALL_BYTES = 256 << 20
 
 
 def algorithmic_bytes(cfg, counts, T):
-    """Per-call bytes: quant blocks of every touched expert (gate, up, down),
-    the f32 router, x in and y out.  Intermediates excluded."""
+    """Per-call bytes: quant blocks of every touched and every shared expert
+    (gate, up, down), the f32 router, x in and y out (intermediates
+    excluded); the routed gate/up launch's bytes (touched experts' gate and
+    up, x, H); and the shared experts' gate/up bytes, which that launch also
+    reads when they ride in it."""
     from leafcutterllm_amd.configs import tensor_size
     touched = int(sum(1 for c in counts if c > 0))
     gu = 2 * tensor_size(cfg.qtype_gate, cfg.d_ff * cfg.d_model)
     dn = tensor_size(cfg.qtype_down, cfg.d_model * cfg.d_ff)
-    layer = touched * (gu + dn) + 4 * cfg.d_model * cfg.n_expert + 8 * T * cfg.d_model
+    S, FS = cfg.n_shared, cfg.d_ff_shared
+    gu_sh = S * 2 * tensor_size(cfg.qtype_gate, FS * cfg.d_model) if S else 0
+    dn_sh = S * tensor_size(cfg.qtype_down, cfg.d_model * FS) if S else 0
+    layer = (touched * (gu + dn) + gu_sh + dn_sh + 4 * cfg.d_model * cfg.n_expert
+             + 8 * T * cfg.d_model)
     gateup = touched * gu + 4 * T * cfg.d_model + 4 * T * cfg.n_expert_used * cfg.d_ff
-    return layer, gateup, touched
+    shared_gateup = gu_sh + 4 * T * S * FS
+    return layer, gateup, shared_gateup, touched
 
 
 def cpu_baseline(cfg, layer, sweep, head_T, budget_s=5.0):
@@ -359,11 +367,12 @@ def main():
     for T in sweep:
         # realised routing of every replica's input -> algorithmic bytes
         call_bytes, gu_bytes, touched = [], [], []
+        sh_bytes = 0
         for r in range(R):
             step(r, T)
             stream.synchronize()
             counts = moes[r].dispatch()["counts"]
-            b, g, n = algorithmic_bytes(cfg, counts, T)
+            b, g, sh_bytes, n = algorithmic_bytes(cfg, counts, T)
             call_bytes.append(b)
             gu_bytes.append(g)
             touched.append(n)
@@ -398,6 +407,12 @@ def main():
         kern = timed_region(True)[1] if args.kernel_events else {}
         bytes_per_step = sum(call_bytes[i % R] for i in range(args.steps)) / args.steps
         gu_per_launch = sum(gu_bytes[i % R] for i in range(args.steps)) / args.steps
+        # shared experts timed without a launch of their own ride in the
+        # routed gate/up launch
+        shared_in_routed = (cfg.n_shared > 0 and bool(kern)
+                            and kern.get("gateup_shared", (0.0, 0))[1] == 0)
+        if shared_in_routed:
+            gu_per_launch += sh_bytes
         gu = kern.get("gateup", (0.0, 0))
         gu_ms = gu[0] / gu[1] if gu[1] else float("nan")
         per_batch[T] = {
@@ -409,6 +424,7 @@ def main():
             "gateup_ms": gu_ms,
             "gateup_bytes": gu_per_launch,
             "gateup_GBps": gu_per_launch / (gu_ms * 1e-3) / 1e9 if gu_ms == gu_ms else float("nan"),
+            "shared_in_routed_launch": shared_in_routed,
             "kernel_ms": {k: v[0] / max(1, v[1]) for k, v in kern.items()},
         }
 
@@ -417,14 +433,19 @@ def main():
     qname = {L.TYPE_Q8_0: "Q8_0", L.TYPE_Q4_K: "Q4_K", L.TYPE_Q6_K: "Q6_K", L.TYPE_F32: "F32"}
     gq = qname[cfg.qtype_gate]
     gu_flops = 4 * cfg.d_model * cfg.d_ff * T * cfg.n_expert_used
+    if head["shared_in_routed_launch"]:
+        gu_flops += 4 * cfg.d_model * cfg.d_ff_shared * T * cfg.n_shared
     gu_weight_bytes = (head["gateup_bytes"] - 4 * T * cfg.d_model
-                       - 4 * T * cfg.n_expert_used * cfg.d_ff)
+                       - 4 * T * cfg.n_expert_used * cfg.d_ff
+                       - (4 * T * cfg.n_shared * cfg.d_ff_shared
+                          if head["shared_in_routed_launch"] else 0))
     if gu_flops / (MFMA_F16_PEAK_TFLOPS * 1e12) > gu_weight_bytes / (HBM_PEAK_GBS * 1e9):
         # past the ridge point (prefill-sized batches): the gate/up products
         # are bound by the f16 dense MFMA peak, not by streaming the weights
         roof = {
             "bound": "mfma",
-            "kernel": f"routed gate/up launch (k_mfma_gateup: {gq} dequant + gate/up + SwiGLU)",
+            "kernel": (f"routed{' + shared' if head['shared_in_routed_launch'] else ''} gate/up "
+                       f"launch (k_mfma_gateup: {gq} dequant + gate/up + SwiGLU)"),
             "achieved": round(gu_flops / (head["gateup_ms"] * 1e-3) / 1e12, 2),
             "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(gu_flops / (head["gateup_ms"] * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),

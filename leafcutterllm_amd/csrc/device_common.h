@@ -257,7 +257,10 @@ struct SlotArgs {
     const int32_t *perm, *counts, *offsets, *touched;
     int E, K, T, shared;
     int nr, S, sbase, ns, sl;
+    const int32_t *pslots;  // pass slots (RouterArgs::pass_slots) or null
 };
+
+constexpr int kPassTokens = 32;  // tokens per pass slot
 
 __device__ __forceinline__ bool slot_info(const SlotArgs &sa, int slot, int &e, int &p0, int &n) {
     if (sa.shared) {
@@ -273,6 +276,14 @@ __device__ __forceinline__ bool slot_info(const SlotArgs &sa, int slot, int &e, 
         p0 = sa.sbase + s * sa.T + c * sa.sl;
         n = min(sa.sl, sa.T - c * sa.sl);
         return n > 0;
+    }
+    if (sa.pslots) {  // one 32-token pass of one expert
+        if (slot >= sa.pslots[0]) return false;
+        const int v = sa.pslots[1 + slot], pass = v >> 8;
+        e = v & 255;
+        p0 = sa.offsets[e] + kPassTokens * pass;
+        n = min(kPassTokens, sa.counts[e] - kPassTokens * pass);
+        return true;
     }
     if (slot >= sa.touched[sa.E]) return false;
     e = sa.touched[slot];

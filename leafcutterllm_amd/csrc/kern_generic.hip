@@ -260,7 +260,7 @@ template <int QT> struct DownK { static constexpr auto fn = k_down<QT>; };
 template <int QT> struct DeqK { static constexpr auto fn = k_debug_dequant<QT>; };
 
 SlotArgs dev_slots(const SlotArgsHost &s) {
-    return SlotArgs{s.perm, s.counts, s.offsets, s.touched, s.E, s.K, s.T, s.shared, s.nr, s.S, s.sbase, s.ns, s.sl};
+    return SlotArgs{s.perm, s.counts, s.offsets, s.touched, s.E, s.K, s.T, s.shared, s.nr, s.S, s.sbase, s.ns, s.sl, s.pslots};
 }
 
 }  // namespace

@@ -1279,7 +1279,7 @@ __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int 
 }
 
 SlotArgs dev_slots(const SlotArgsHost &s) {
-    return SlotArgs{s.perm, s.counts, s.offsets, s.touched, s.E, s.K, s.T, s.shared, s.nr, s.S, s.sbase, s.ns, s.sl};
+    return SlotArgs{s.perm, s.counts, s.offsets, s.touched, s.E, s.K, s.T, s.shared, s.nr, s.S, s.sbase, s.ns, s.sl, s.pslots};
 }
 
 }  // namespace

@@ -192,20 +192,28 @@ __device__ void select_token(const RouterArgs &a, int t, float *s_z, float *s_s,
     }
 }
 
+// Inclusive scan across the wave
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int u = __shfl_up(v, off, 64);
+        if (lane >= off) v += u;
+    }
+    return v;
+}
+
 // Exclusive scan of s_off[0..E) (per-expert counts) into offsets by one
-// wave, writing offsets[0..E], touched[] and s_off[E] = total.
+// wave, writing offsets[0..E], touched[] and s_off[E] = total, and with
+// a.pass_slots the pass slots: expert e's ceil(count / 32) passes, in
+// expert order, after the count of them.
 __device__ void scan_experts(const RouterArgs &a, int *s_off) {
     const int lane = threadIdx.x & 63, E = a.E;
-    int run = 0, nt = 0;
+    int run = 0, nt = 0, np = 0;
     for (int e0 = 0; e0 < E; e0 += 64) {
         const int e = e0 + lane;
         const int c = e < E ? s_off[e] : 0;
-        int incl = c;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const int v = __shfl_up(incl, off, 64);
-            if (lane >= off) incl += v;
-        }
+        const int incl = wave_incl_scan(c);
         const uint64_t m = __ballot(c > 0);
         if (e < E) {
             s_off[e] = run + incl - c;
@@ -214,11 +222,19 @@ __device__ void scan_experts(const RouterArgs &a, int *s_off) {
         if (c > 0) a.touched[nt + __popcll(m & ((1ull << lane) - 1ull))] = e;
         run += __shfl(incl, 63, 64);
         nt += __popcll(m);
+        if (a.pass_slots) {
+            const int passes = (c + kPassTokens - 1) / kPassTokens;
+            const int pincl = wave_incl_scan(passes);
+            for (int j = 0; j < passes; j++)
+                a.pass_slots[1 + np + pincl - passes + j] = j * 256 + e;
+            np += __shfl(pincl, 63, 64);
+        }
     }
     if (lane == 0) {
         s_off[E] = run;
         a.offsets[E] = run;
         a.touched[E] = nt;
+        if (a.pass_slots) a.pass_slots[0] = np;
     }
 }
 
@@ -319,12 +335,14 @@ __device__ void dispatch_one(const RouterArgs &a, const int *sel) {
             a.perm[pos] = kpos;
             a.inv[kpos] = pos;
             a.touched[pos] = e;
+            if (a.pass_slots) a.pass_slots[1 + pos] = e;  // one pass per expert
         }
         run += __popcll(m);
     }
     if (lane == 0) {
         a.offsets[E] = run;
         a.touched[E] = run;
+        if (a.pass_slots) a.pass_slots[0] = run;
     }
 }
 

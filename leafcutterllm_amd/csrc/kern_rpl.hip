@@ -555,7 +555,7 @@ hipError_t launch_rpl_gateup(const uint8_t *gate, const uint8_t *up, int64_t est
                              const SlotArgsHost &sa, int slots, int d, int F, float *Hf, int8_t *hh,
                              int8_t *hl, float *hs, float *hm, _Float16 *h16, _Float16 *hs16,
                              const ChainArgs &ch, hipStream_t st, bool q8) {
-    SlotArgs s{sa.perm, sa.counts, sa.offsets, sa.touched, sa.E, sa.K, sa.T, sa.shared, sa.nr, sa.S, sa.sbase, sa.ns, sa.sl};
+    SlotArgs s{sa.perm, sa.counts, sa.offsets, sa.touched, sa.E, sa.K, sa.T, sa.shared, sa.nr, sa.S, sa.sbase, sa.ns, sa.sl, sa.pslots};
     ChainArgs c = ch;
     if (c.tiles) {
         if (c.k0 % 256 || c.k1 % 256) return hipErrorInvalidValue;
@@ -575,7 +575,7 @@ hipError_t launch_rpl_down(const uint8_t *down, int64_t estride, const int8_t *h
                            const int8_t *hl, const float *hs, const float *hm,
                            const SlotArgsHost &sa, int slots, int d, int F, int ksplit, float *Y,
                            int64_t split_stride, hipStream_t st, int fmt) {
-    SlotArgs s{sa.perm, sa.counts, sa.offsets, sa.touched, sa.E, sa.K, sa.T, sa.shared, sa.nr, sa.S, sa.sbase, sa.ns, sa.sl};
+    SlotArgs s{sa.perm, sa.counts, sa.offsets, sa.touched, sa.E, sa.K, sa.T, sa.shared, sa.nr, sa.S, sa.sbase, sa.ns, sa.sl, sa.pslots};
     const dim3 grid(d / 64, slots, ksplit);
     if (fmt == 1)
         hipLaunchKernelGGL(k_rpl_down<1>, grid, dim3(256), 0, st, down, estride, hh, hl, hs, hm, s,

@@ -31,6 +31,10 @@ struct RouterArgs {
     float *xs, *xm;       // [T, d/32] scale and quantised-sum
     _Float16 *x16, *x16s; // f16 hi/lo pieces and sums for the matrix-core path, or null
     int32_t *counts, *offsets, *perm, *inv, *touched;
+    // pass slots, or null: [0] = their number P, then per slot v < P the
+    // entry pass * 256 + e, the 32-token passes of every touched expert in
+    // expert order (written by the batch dispatch)
+    int32_t *pass_slots = nullptr;
     uint32_t *sync;       // [n_token_groups + 1] zero-initialised counters
     // Fused post-attention RMSNorm (certified fast router only): with xin
     // set, each token block first writes x[t] = rms_norm(xin[t]) * norm_w
@@ -76,6 +80,9 @@ struct SlotArgsHost {
     const int32_t *perm, *counts, *offsets, *touched;
     int E, K, T, shared;
     int nr, S, sbase, ns, sl;
+    // routed slot v < nr is pass slot v (one 32-token pass of one expert)
+    // when set (RouterArgs::pass_slots)
+    const int32_t *pslots = nullptr;
 };
 
 // Generic decode path on GGUF-layout tensors (any supported type, any

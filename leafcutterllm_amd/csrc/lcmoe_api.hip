@@ -87,6 +87,7 @@ struct lcmoe_handle {
     _Float16 *x16 = nullptr, *x16s = nullptr;
     int32_t *topk_idx = nullptr, *counts = nullptr, *offsets = nullptr, *perm = nullptr,
             *inv = nullptr, *touched = nullptr;
+    int32_t *pass_slots = nullptr;  // RouterArgs::pass_slots
     float *topk_w = nullptr;
     uint32_t *sync = nullptr;
     // certified sigmoid-group router: bounds, per-token counters and marks
@@ -103,6 +104,13 @@ struct lcmoe_handle {
     double t_ms[kNumSlots] = {};
     int64_t t_n[kNumSlots] = {};
 };
+
+// Pass slots a forward of T tokens can need: sum over the touched experts of
+// ceil(count / 32) < T K / 32 + touched.
+static int64_t max_pass_slots(const lcmoe_desc &D, int64_t T) {
+    const int64_t A = T * D.n_expert_used;
+    return (A + 31) / 32 + std::min<int64_t>(D.n_expert, A);
+}
 
 namespace {
 
@@ -382,6 +390,7 @@ extern "C" lcmoe_status lcmoe_create(const lcmoe_desc *desc, const lcmoe_weights
     if ((st = alloc_n(h, &h->perm, A))) return bail(st);
     if ((st = alloc_n(h, &h->inv, A))) return bail(st);
     if ((st = alloc_n(h, &h->touched, E + 1))) return bail(st);
+    if ((st = alloc_n(h, &h->pass_slots, 1 + max_pass_slots(D, Tm)))) return bail(st);
     const int nsync = router_token_groups((int)Tm, (int)d, (int)E) + 1;
     if ((st = alloc_n(h, &h->sync, nsync))) return bail(st);
     if (hipMemset(h->sync, 0, sizeof(uint32_t) * nsync) != hipSuccess)
@@ -403,11 +412,13 @@ extern "C" void lcmoe_destroy(lcmoe_handle *h) { free_handle(h); }
 // Which product kernels serve an expert family this forward.
 struct Plan {
     bool mfma;
+    bool passes;  // routed slots are pass slots (one 32-token pass each)
     int slots, ks;
     int chunks;  // blocks sharing one matrix-core slot's 32-token passes
     int sl, ns;  // fused shared experts: tokens per slot, slots per expert
     int per_slot;  // average tokens per slot
 };
+
 
 // fused: the routed plan also carries the fused shared experts (slots
 // p.slots .. p.slots + n_shared - 1, all T tokens each)
@@ -433,6 +444,15 @@ static Plan plan_set(lcmoe_handle *h, const ExpertSet &s, bool shared, int T, in
         shared ? T : ((int64_t)T * D.n_expert_used + p.slots - 1) / std::max(1, p.slots);
     p.chunks = p.mfma ? (int)std::min<int64_t>(64, std::max<int64_t>(1, (per_slot + 31) / 32)) : 1;
     p.per_slot = (int)std::min<int64_t>(per_slot, INT32_MAX);
+    // Routed experts averaging more than one pass: one block per 32-token
+    // pass of each touched expert (pass slots from the dispatch), so skewed
+    // routing spreads its busy experts over the grid instead of leaving
+    // their passes to a fixed number of blocks each.
+    p.passes = p.mfma && !shared && p.chunks > 1 && h->pass_slots;
+    if (p.passes) {
+        p.slots = (int)max_pass_slots(D, T);
+        p.chunks = 1;
+    }
     // fused shared experts: slices of the tokens one slot takes (the passes
     // of its chunk blocks, or one row-per-lane pass)
     p.sl = p.mfma ? 32 * p.chunks : 4;
@@ -453,7 +473,8 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
     const int d = D.d_model, K = D.n_expert_used, E = D.n_expert;
     const int A = D.max_tokens * K;  // routed positions; fused shared ones follow
     SlotArgsHost sa{h->perm, h->counts, h->offsets, h->touched, E, K, T, shared ? 1 : 0,
-                    pl.slots, fused, fused ? A : INT32_MAX, std::max(1, pl.ns), pl.sl};
+                    pl.slots, fused, fused ? A : INT32_MAX, std::max(1, pl.ns), pl.sl,
+                    pl.passes ? h->pass_slots : nullptr};
     const int slots = pl.slots + fused * pl.ns;
     // H between the products in the form the down kernel reads: f16 pieces
     // for the matrix-core downs, int8 limbs for the row-per-lane ones (Q4_K
@@ -508,7 +529,7 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
     const bool together = Sf > 0 && pr0.chunks == 1;
     const int fused = together ? Sf : 0;
     const Plan pr = together ? plan_set(h, h->routed, false, T, Sf) : pr0;
-    const Plan off{false, 0, 1, 1, 4, 0, 0};
+    const Plan off{false, false, 0, 1, 1, 4, 0, 0};
     const Plan pf = Sf > 0 && !together ? plan_set(h, h->routed, false, T, Sf, true) : off;
     const Plan ps = S > 0 && !h->fused ? plan_set(h, h->shared, true, T) : off;
     const bool sep_f = Sf > 0 && !together;
@@ -540,6 +561,7 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
     ra.perm = h->perm;
     ra.inv = h->inv;
     ra.touched = h->touched;
+    ra.pass_slots = pr.passes ? h->pass_slots : nullptr;
     ra.sync = h->sync;
     // the fast router reads the whole router matrix once per token: past
     // kFastRouterElems multiply-adds per forward the chain router, which
