@@ -1151,16 +1151,27 @@ __device__ void sig_certify(const RouterArgs &a, int t, float *s_lo, float *s_hi
 }
 
 template <int NC4>
-__global__ __launch_bounds__(64 * kSigWaves) void k_route_sig(RouterArgs a) {
+__global__ __launch_bounds__(64 * kSigWaves) void k_route_sig(RouterArgs a, ChainArgs ch) {
     __shared__ float s_f[3 * kMaxE + 3 * 64];  // certification: keys, group scores
     __shared__ int s_last;
     const int t = blockIdx.y, tid = threadIdx.x, wave = tid >> 6;
+    const int nsig = a.E / kSigWaves;  // bound blocks per token
+    if ((int)blockIdx.x >= nsig) {
+        // blocks past them (row 0): the first column range of the exact
+        // chains, wave 0, one tile at a time
+        if (t == 0 && wave == 0) {
+            __shared__ __attribute__((aligned(16))) float s_chain[chain_lds_floats(1 + 8, 256)];
+            for (int tile = blockIdx.x - nsig; tile < ch.tiles; tile += gridDim.x - nsig)
+                chain_tile<1, 256, 1>(ch, tile, s_chain);
+        }
+        return;
+    }
     sig_bounds<NC4>(a, t, blockIdx.x * kSigWaves + wave);
     // the token's activations, a slice per block
-    quantise_token<1, 64 * kSigWaves>(a, t, nullptr, blockIdx.x, gridDim.x);
+    quantise_token<1, 64 * kSigWaves>(a, t, nullptr, blockIdx.x, nsig);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's bounds have landed
     __syncthreads();
-    if (tid == 0) s_last = atomicAdd(&a.tsync[t], 1u) == gridDim.x - 1;
+    if (tid == 0) s_last = atomicAdd(&a.tsync[t], 1u) == (unsigned)nsig - 1;
     __syncthreads();
     if (!s_last) return;
     // the last block of token t: every bound of t is stored
@@ -1336,18 +1347,25 @@ bool route_sig_ok(const RouterArgs &a) {
            G <= 64 && a.E % G == 0 && a.K <= kMaxK && route_chains_ok(a);
 }
 
-hipError_t launch_route_sig(const RouterArgs &a, hipStream_t st) {
+hipError_t launch_route_sig(const RouterArgs &a, const ChainArgs &ch, hipStream_t st) {
     if (!route_sig_ok(a)) return hipErrorInvalidValue;
     static_assert(64 % kSigWaves == 0, "blocks of whole expert groups");
-    const dim3 grid(a.E / kSigWaves, a.T), block(64 * kSigWaves);
+    ChainArgs c = ch;
+    int cb = 0;
+    if (c.tiles) {  // one-token tiles, 256-column chunks
+        if (c.k0 % 256 || c.k1 % 256) return hipErrorInvalidValue;
+        c = with_nt(ch, 1);
+        cb = c.tiles < 64 ? c.tiles : 64;
+    }
+    const dim3 grid(a.E / kSigWaves + cb, a.T), block(64 * kSigWaves);
     switch (a.d / 256) {
-    case 1: hipLaunchKernelGGL(k_route_sig<1>, grid, block, 0, st, a); break;
-    case 2: hipLaunchKernelGGL(k_route_sig<2>, grid, block, 0, st, a); break;
-    case 4: hipLaunchKernelGGL(k_route_sig<4>, grid, block, 0, st, a); break;
-    case 8: hipLaunchKernelGGL(k_route_sig<8>, grid, block, 0, st, a); break;
-    case 16: hipLaunchKernelGGL(k_route_sig<16>, grid, block, 0, st, a); break;
-    case 28: hipLaunchKernelGGL(k_route_sig<28>, grid, block, 0, st, a); break;
-    default: hipLaunchKernelGGL(k_route_sig<32>, grid, block, 0, st, a); break;
+    case 1: hipLaunchKernelGGL(k_route_sig<1>, grid, block, 0, st, a, c); break;
+    case 2: hipLaunchKernelGGL(k_route_sig<2>, grid, block, 0, st, a, c); break;
+    case 4: hipLaunchKernelGGL(k_route_sig<4>, grid, block, 0, st, a, c); break;
+    case 8: hipLaunchKernelGGL(k_route_sig<8>, grid, block, 0, st, a, c); break;
+    case 16: hipLaunchKernelGGL(k_route_sig<16>, grid, block, 0, st, a, c); break;
+    case 28: hipLaunchKernelGGL(k_route_sig<28>, grid, block, 0, st, a, c); break;
+    default: hipLaunchKernelGGL(k_route_sig<32>, grid, block, 0, st, a, c); break;
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

@@ -70,7 +70,7 @@ hipError_t launch_route_fast(const RouterArgs &a, const ChainArgs &ch, hipStream
 // (launch_route_chains with a.flag) and selection then serve only tokens the
 // bounds could not certify, and dispatch every token.
 bool route_sig_ok(const RouterArgs &a);
-hipError_t launch_route_sig(const RouterArgs &a, hipStream_t st);
+hipError_t launch_route_sig(const RouterArgs &a, const ChainArgs &ch, hipStream_t st);
 int router_token_groups(int T, int d, int E);
 
 // See SlotArgs (device_common.h): nr routed slots, then S fused shared
