@@ -431,10 +431,11 @@ lcmoe_status lcmoe_debug_sigmoid(const float *x, int64_t n, float *out);
  * No counterpart in the reference. */
 lcmoe_status lcmoe_debug_read_bandwidth(int64_t slice_bytes, int32_t reps, double *gbps);
 /* Tokens of the handle's last forward whose expert selection the certified
- * sigmoid-group router left to the exact chain logits (their float64 bounds
- * could not order the decision); -1 when that forward did not use it.  Waits
- * for the forward.  No counterpart in the reference: it observes which of
- * two bit-identical routes ran. */
+ * router with parallel float64 bounds (the sigmoid-group kind's, and the
+ * softmax kinds' at one token with 32 or more experts) left to the exact
+ * chain logits (their bounds could not order the decision); -1 when that
+ * forward did not use it.  Waits for the forward.  No counterpart in the
+ * reference: it observes which of two bit-identical routes ran. */
 lcmoe_status lcmoe_debug_route_fallbacks(lcmoe_handle *h, int32_t *count);
 
 #ifdef __cplusplus

@@ -874,32 +874,38 @@ __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a, Chain
 }
 
 // ---------------------------------------------------------------------------
-// Certified router for the sigmoid-group kind (lco_route kind 2, the
-// DeepSeek-V3 noaux_tc rule): score s_e = sigmoid(c_e) of the reference chain
-// logit c_e, key z_e = s_e + bias_e; each of the G groups of E/G experts
-// scores the rounded sum of its two largest keys; the topk_group best groups
-// are kept and the K largest keys among their experts selected, ties to the
-// lower index throughout.
+// Certified router with parallel bounds.  The sigmoid-group kind (lco_route
+// kind 2, the DeepSeek-V3 noaux_tc rule): score s_e = sigmoid(c_e) of the
+// reference chain logit c_e, key z_e = s_e + bias_e; each of the G groups
+// of E/G experts scores the rounded sum of its two largest keys; the
+// topk_group best groups are kept and the K largest keys among their
+// experts selected, ties to the lower index throughout.  The softmax kinds
+// (at one token, for wide routers): key z_e = c_e + bias_e, the K largest
+// over all experts (one group, kept).
 //
-// Grid (E / kSigWaves, T): wave w of block (b, t) bounds the chain logit of
-// expert kSigWaves b + w for token t in float64, as the fast router does
-// (c_e in [S_d - B, S_d + B], hence in [zlo, zhi] as floats); block (0, t)
-// also writes t's activations.  The last block of token t to finish (a
-// per-token counter) certifies it in one wave:
+// Grid (E / kSigWaves [+ chain blocks], T): wave w of block (b, t) bounds
+// the chain logit of expert kSigWaves b + w for token t in float64, as the
+// fast router does (c_e in [S_d - B, S_d + B], hence in [zlo, zhi] as
+// floats); the blocks also write t's activations, a slice each.  The last
+// block of token t to finish (a per-token counter) certifies it in one wave:
 //   * sigmoid_cw dips below its running maximum by at most one ulp (an
-//     exhaustive check over every float input, oracle/sigmoid_monotone.c),
-//     so s_e lies in [down(sigmoid(zlo)), up(sigmoid(zhi))], and the key in
-//     the rounded sums with the bias (rounding is monotone);
+//     exhaustive check over every float input, lco_sigmoid_max_dip in the
+//     oracle), so s_e lies in [down(sigmoid(zlo)), up(sigmoid(zhi))], and
+//     the key in the rounded sums with the bias (rounding is monotone; for
+//     the softmax kinds the key interval is [zlo + b, zhi + b] directly);
 //   * a group score is monotone in every key, so the group scores of the
 //     low and the high keys bound it;
 //   * the kept groups stand when every kept group's low score beats every
 //     dropped group's high score (or ties it with a lower index);
 //   * the selection stands rank by rank as in the fast router, over the
 //     kept groups' experts.
-// A certified token's selection is final here; the others are marked for
-// the exact chains (k_route_chains) and selection (k_route_select) that
-// follow, which also dispatch every token.  The routing weights come from
-// the exact logits (chains beside the gate/up products) in the combine.
+// A certified token's selection is final here.  With one token the
+// certifying wave also runs the exact path for an uncertified token (the
+// chains over all d columns, select_token) and the dispatch; with more, the
+// uncertified tokens are marked for the exact chains (k_route_chains) and
+// selection (k_route_select) that follow, which also dispatch every token.
+// The routing weights come from the exact logits (chains beside the
+// bounds and the gate/up products) in the combine.
 // ---------------------------------------------------------------------------
 constexpr int kSigWaves = 4;
 
@@ -971,12 +977,15 @@ __device__ void sig_bounds(const RouterArgs &a, int t, int e) {
 // Certification of token t by one wave (E <= 256, G <= 64);
 // s_lo / s_hi / s_m: E floats each (the low, high and point keys), s_g:
 // 3 x 64 group scores, s_sel: K.  Writes topk_idx[t] when certified and
-// flag[t] (0 certified, 1 for the exact path).
-__device__ void sig_certify(const RouterArgs &a, int t, float *s_lo, float *s_hi, float *s_m,
+// flag[t] (0 certified, 1 for the exact path); returns the verdict, with the
+// selection in s_sel when certified.  The softmax kinds select the K largest
+// keys z = c + bias over all experts (select_token): one group, kept.
+__device__ bool sig_certify(const RouterArgs &a, int t, float *s_lo, float *s_hi, float *s_m,
                             float *s_g, int *s_sel) {
     const int lane = threadIdx.x & 63, E = a.E, K = a.K, NI = (E + 63) / 64;
     const RouteParams &rp = a.rp;
-    const int G = rp.n_group, gs = E / G;
+    const bool grouped = rp.kind == LCMOE_ROUTE_SIGMOID_GROUP;
+    const int G = grouped ? rp.n_group : 1, gs = E / G;
     bool ok = true;
     double Sv[4], Bv[4];
 #pragma unroll
@@ -995,11 +1004,16 @@ __device__ void sig_certify(const RouterArgs &a, int t, float *s_lo, float *s_hi
         ok = ok && fin;
         const float zlo = fin ? ceil_f32(lo) : 0.0f, zhi = fin ? floor_f32(hi) : 0.0f;
         const float zm = fin ? (float)S : 0.0f;
-        // sigmoid_cw's dips are at most one ulp: widen by one step each way
-        // (scores lie in [0, 1])
-        float klo = sigmoid_cw(zlo), khi = next_up(sigmoid_cw(zhi)), km = sigmoid_cw(zm);
-        klo = klo > 0.0f ? next_down(klo) : 0.0f;
-        if (rp.has_bias) {
+        float klo = zlo, khi = zhi, km = zm;
+        if (grouped) {
+            // sigmoid_cw's dips are at most one ulp: widen by one step each
+            // way (scores lie in [0, 1])
+            klo = sigmoid_cw(zlo);
+            khi = next_up(sigmoid_cw(zhi));
+            km = sigmoid_cw(zm);
+            klo = klo > 0.0f ? next_down(klo) : 0.0f;
+        }
+        if (rp.has_bias) {  // rounding to nearest is monotone
             const float b = a.bias[e];
             klo = klo + b;
             khi = khi + b;
@@ -1012,73 +1026,76 @@ __device__ void sig_certify(const RouterArgs &a, int t, float *s_lo, float *s_hi
         s_m[e] = km;
     }
     chain_detail::wave_lds_sync();
-    // group scores of the three key sets: the rounded sum of the group's two
-    // largest keys (select_token's expression; only the values matter, and
-    // the keys are finite when they count).  Groups of a power-of-two size up
-    // to 64 are lane segments of each 64-expert slice: a butterfly over the
-    // segment merges (largest, second) pairs.
-    if (gs <= 64 && (gs & (gs - 1)) == 0) {
-        for (int arr = 0; arr < 3; arr++) {
-            const float *v = arr == 0 ? s_lo : arr == 1 ? s_hi : s_m;
-            for (int i = 0; i < NI; i++) {
-                const int e = lane + 64 * i;
-                float k1 = e < E ? v[e] : -__builtin_inff(), k2 = -__builtin_inff();
-                for (int off = 1; off < gs; off <<= 1) {
-                    const float o1 = __shfl_xor(k1, off, 64), o2 = __shfl_xor(k2, off, 64);
-                    const float hi1 = fmaxf(k1, o1), lo1 = fminf(k1, o1);
-                    k2 = fmaxf(lo1, fmaxf(k2, o2));
-                    k1 = hi1;
-                }
-                if (e < E && (lane & (gs - 1)) == 0)
-                    s_g[64 * arr + e / gs] = gs >= 2 ? k1 + k2 : k1;
-            }
-        }
-    } else if (lane < G) {
-        for (int arr = 0; arr < 3; arr++) {
-            const float *v = arr == 0 ? s_lo : arr == 1 ? s_hi : s_m;
-            float k1 = -__builtin_inff(), k2 = -__builtin_inff();
-            int e1 = INT_MAX, e2 = INT_MAX;
-            for (int i = 0; i < gs; i++) {
-                const int e = lane * gs + i;
-                const float k = sel_key(v[e]);
-                if (better(k, e, k1, e1)) {
-                    k2 = k1;
-                    e2 = e1;
-                    k1 = k;
-                    e1 = e;
-                } else if (better(k, e, k2, e2)) {
-                    k2 = k;
-                    e2 = e;
+    uint64_t kmask = ~0ull;  // kept groups (one for the softmax kinds)
+    if (grouped) {
+        // group scores of the three key sets: the rounded sum of the group's
+        // two largest keys (select_token's expression; only the values
+        // matter, and the keys are finite when they count).  Groups of a
+        // power-of-two size up to 64 are lane segments of each 64-expert
+        // slice: a butterfly over the segment merges (largest, second) pairs.
+        if (gs <= 64 && (gs & (gs - 1)) == 0) {
+            for (int arr = 0; arr < 3; arr++) {
+                const float *v = arr == 0 ? s_lo : arr == 1 ? s_hi : s_m;
+                for (int i = 0; i < NI; i++) {
+                    const int e = lane + 64 * i;
+                    float k1 = e < E ? v[e] : -__builtin_inff(), k2 = -__builtin_inff();
+                    for (int off = 1; off < gs; off <<= 1) {
+                        const float o1 = __shfl_xor(k1, off, 64), o2 = __shfl_xor(k2, off, 64);
+                        const float hi1 = fmaxf(k1, o1), lo1 = fminf(k1, o1);
+                        k2 = fmaxf(lo1, fmaxf(k2, o2));
+                        k1 = hi1;
+                    }
+                    if (e < E && (lane & (gs - 1)) == 0)
+                        s_g[64 * arr + e / gs] = gs >= 2 ? k1 + k2 : k1;
                 }
             }
-            s_g[64 * arr + lane] = gs >= 2 ? v[e1] + v[min(e2, E - 1)] : v[e1];
+        } else if (lane < G) {
+            for (int arr = 0; arr < 3; arr++) {
+                const float *v = arr == 0 ? s_lo : arr == 1 ? s_hi : s_m;
+                float k1 = -__builtin_inff(), k2 = -__builtin_inff();
+                int e1 = INT_MAX, e2 = INT_MAX;
+                for (int i = 0; i < gs; i++) {
+                    const int e = lane * gs + i;
+                    const float k = sel_key(v[e]);
+                    if (better(k, e, k1, e1)) {
+                        k2 = k1;
+                        e2 = e1;
+                        k1 = k;
+                        e1 = e;
+                    } else if (better(k, e, k2, e2)) {
+                        k2 = k;
+                        e2 = e;
+                    }
+                }
+                s_g[64 * arr + lane] = gs >= 2 ? v[e1] + v[min(e2, E - 1)] : v[e1];
+            }
         }
-    }
-    chain_detail::wave_lds_sync();
-    // kept groups by the point scores, topk_group rounds of a wave argmax
-    const bool gv = lane < G;
-    const float glo = gv ? s_g[lane] : 0.0f, ghi = gv ? s_g[64 + lane] : 0.0f;
-    uint64_t gkey = gv ? ((uint64_t)ord_key(sel_key(s_g[128 + lane])) << 32) | (uint32_t)~lane : 0;
-    bool kept = false;
-    for (int r = 0; r < rp.topk_group; r++) {
-        const uint64_t best = wave_max_u64(gkey);
-        if (gv && lane == (int)~(uint32_t)best) {
-            kept = true;
-            gkey = 0;
+        chain_detail::wave_lds_sync();
+        // kept groups by the point scores, topk_group rounds of a wave argmax
+        const bool gv = lane < G;
+        const float glo = gv ? s_g[lane] : 0.0f, ghi = gv ? s_g[64 + lane] : 0.0f;
+        uint64_t gkey = gv ? ((uint64_t)ord_key(sel_key(s_g[128 + lane])) << 32) | (uint32_t)~lane : 0;
+        bool kept = false;
+        for (int r = 0; r < rp.topk_group; r++) {
+            const uint64_t best = wave_max_u64(gkey);
+            if (gv && lane == (int)~(uint32_t)best) {
+                kept = true;
+                gkey = 0;
+            }
         }
-    }
-    // every kept group above every dropped one: the dropped groups' highest
-    // score Mx and the lowest index at it, two wave reductions
-    {
-        const bool dropped = gv && !kept;
-        const uint32_t mx = wave_max_u32(dropped ? ord_key(ghi) : 0u);
-        const uint32_t fmin = 64u - wave_max_u32(dropped && ord_key(ghi) == mx ? 64u - lane : 0u);
-        if (kept && mx != 0) {
-            const uint32_t ol = ord_key(glo);
-            ok = ok && (ol > mx || (ol == mx && (uint32_t)lane < fmin));
+        // every kept group above every dropped one: the dropped groups' highest
+        // score Mx and the lowest index at it, two wave reductions
+        {
+            const bool dropped = gv && !kept;
+            const uint32_t mx = wave_max_u32(dropped ? ord_key(ghi) : 0u);
+            const uint32_t fmin = 64u - wave_max_u32(dropped && ord_key(ghi) == mx ? 64u - lane : 0u);
+            if (kept && mx != 0) {
+                const uint32_t ol = ord_key(glo);
+                ok = ok && (ol > mx || (ol == mx && (uint32_t)lane < fmin));
+            }
         }
+        kmask = __ballot(kept);
     }
-    const uint64_t kmask = __ballot(kept);
     // K rounds of a wave argmax over the kept groups' experts (point keys)
     uint64_t ek[4];
     int rank[4];
@@ -1148,11 +1165,14 @@ __device__ void sig_certify(const RouterArgs &a, int t, float *s_lo, float *s_hi
             if (rank[i] >= 0) store_agent(a.topk_idx + (int64_t)t * K + rank[i], lane + 64 * i);
     }
     if (lane == 0) store_agent(a.flag + t, ok ? 0 : 1);
+    return ok;
 }
 
 template <int NC4>
 __global__ __launch_bounds__(64 * kSigWaves) void k_route_sig(RouterArgs a, ChainArgs ch) {
     __shared__ float s_f[3 * kMaxE + 3 * 64];  // certification: keys, group scores
+    // one wave's chain stream: the chain blocks', or the one-token fallback's
+    __shared__ __attribute__((aligned(16))) float s_chain[chain_lds_floats(1 + 8, 256)];
     __shared__ int s_last;
     const int t = blockIdx.y, tid = threadIdx.x, wave = tid >> 6;
     const int nsig = a.E / kSigWaves;  // bound blocks per token
@@ -1160,7 +1180,6 @@ __global__ __launch_bounds__(64 * kSigWaves) void k_route_sig(RouterArgs a, Chai
         // blocks past them (row 0): the first column range of the exact
         // chains, wave 0, one tile at a time
         if (t == 0 && wave == 0) {
-            __shared__ __attribute__((aligned(16))) float s_chain[chain_lds_floats(1 + 8, 256)];
             for (int tile = blockIdx.x - nsig; tile < ch.tiles; tile += gridDim.x - nsig)
                 chain_tile<1, 256, 1>(ch, tile, s_chain);
         }
@@ -1178,7 +1197,22 @@ __global__ __launch_bounds__(64 * kSigWaves) void k_route_sig(RouterArgs a, Chai
     if (wave == 0) {
         __shared__ int s_sel[kMaxK];
         if (tid == 0) a.tsync[t] = 0;
-        sig_certify(a, t, s_f, s_f + a.E, s_f + 2 * a.E, s_f + 3 * a.E, s_sel);
+        const bool ok = sig_certify(a, t, s_f, s_f + a.E, s_f + 2 * a.E, s_f + 3 * a.E, s_sel);
+        if (a.T > 1) return;  // the chains, selection and dispatch launches follow
+        // one token: this wave finishes the routing itself (no launches
+        // follow): for an uncertified token the exact chains over all d
+        // columns and the exact selection, then the dispatch from LDS
+        if (!ok) {
+            const ChainArgs ca = make_chains(a.x, a.wrt, a.logits, nullptr, a.T, a.d, a.E, 0,
+                                             a.d, 1);
+            for (int g = 0; g < ca.tiles; g++) chain_tile<1, 256, 1>(ca, g, s_chain);
+            __threadfence_block();
+            float *s_z = s_f, *s_s = s_f + kMaxE, *s_g = s_f + 2 * kMaxE;
+            unsigned char *s_ok = reinterpret_cast<unsigned char *>(s_f + 3 * kMaxE);
+            select_token(a, t, s_z, s_s, s_g, s_ok, s_sel);
+            chain_detail::wave_lds_sync();
+        }
+        dispatch_one(a, s_sel);
     }
 }
 
@@ -1342,9 +1376,11 @@ hipError_t launch_route_fast(const RouterArgs &a, const ChainArgs &ch, hipStream
 
 bool route_sig_ok(const RouterArgs &a) {
     const int G = a.rp.n_group;
-    return a.rp.kind == LCMOE_ROUTE_SIGMOID_GROUP && a.wlc && a.bnd && a.tsync && a.flag &&
-           a.E % kSigWaves == 0 && a.E <= 256 && a.d % 256 == 0 && sig_nc4_ok(a.d / 256) && G >= 1 &&
-           G <= 64 && a.E % G == 0 && a.K <= kMaxK && route_chains_ok(a);
+    const bool groups = a.rp.kind != LCMOE_ROUTE_SIGMOID_GROUP ||
+                        (G >= 1 && G <= 64 && a.E % G == 0);
+    return a.wlc && a.bnd && a.tsync && a.flag && a.E % kSigWaves == 0 && a.E <= 256 &&
+           a.d % 256 == 0 && sig_nc4_ok(a.d / 256) && groups && a.K <= kMaxK &&
+           route_chains_ok(a);
 }
 
 hipError_t launch_route_sig(const RouterArgs &a, const ChainArgs &ch, hipStream_t st) {
@@ -1368,7 +1404,7 @@ hipError_t launch_route_sig(const RouterArgs &a, const ChainArgs &ch, hipStream_
     default: hipLaunchKernelGGL(k_route_sig<32>, grid, block, 0, st, a, c); break;
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || a.T == 1) return e;  // one token: the launch dispatched it
     // the exact chains and selection for the marked tokens; the activations
     // are written already
     RouterArgs b = a;

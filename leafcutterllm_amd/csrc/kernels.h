@@ -63,12 +63,15 @@ hipError_t launch_route_chains(const RouterArgs &a, hipStream_t st);
 // and of the routed gate/up launch (the rest).
 bool route_fast_ok(const RouterArgs &a);
 hipError_t launch_route_fast(const RouterArgs &a, const ChainArgs &ch, hipStream_t st);
-// Certified router for the sigmoid-group kind (E <= 256, E % 4 == 0,
-// d / 256 in {1, 2, 4, 8, 16, 28, 32}, n_group <= 64): float64 logit bounds, then
-// certification of the group and expert selection per token; a.bnd, a.tsync
-// and a.flag set.  Writes topk_idx and the activations; the exact chains
-// (launch_route_chains with a.flag) and selection then serve only tokens the
-// bounds could not certify, and dispatch every token.
+// Certified router with parallel float64 logit bounds (E <= 256, E % 4 == 0,
+// d / 256 in {1, 2, 4, 8, 16, 28, 32}; the sigmoid-group kind with
+// n_group <= 64, or a softmax kind): E / 4 blocks per token bound the
+// logits, the last certifies the (group and) expert selection; a.bnd,
+// a.tsync and a.flag set.  Writes topk_idx and the activations.  One token:
+// the certifying block also runs the exact fallback and the dispatch.  More:
+// the exact chains (launch_route_chains with a.flag) and selection then
+// serve only tokens the bounds could not certify, and dispatch every token.
+// ch: a first column range of the exact chains, run in blocks beside them.
 bool route_sig_ok(const RouterArgs &a);
 hipError_t launch_route_sig(const RouterArgs &a, const ChainArgs &ch, hipStream_t st);
 int router_token_groups(int T, int d, int E);

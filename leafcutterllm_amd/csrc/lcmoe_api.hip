@@ -42,6 +42,10 @@ constexpr int64_t kFastRouterElems = (int64_t)1 << 24;
 // chains: past about 24 tokens at those shapes the chain router alone is
 // the faster one.
 constexpr int64_t kSigRouterElems = (int64_t)1 << 25;
+// Softmax routers this wide take the parallel-bounds certified router at one
+// token (config 5, E = 60: the fast router's one block reads 491 KB of
+// router weights alone).
+constexpr int kParallelBoundsMinE = 32;
 
 struct ExpertSet {  // one family of experts (routed or shared)
     int n = 0, F = 0, qt_gu = 0, qt_dn = 0;
@@ -95,7 +99,7 @@ struct lcmoe_handle {
     uint32_t *sig_sync = nullptr;
     int32_t *sig_flag = nullptr;
     int last_T = -1;
-    bool last_sig = false;  // the last forward used the certified sigmoid-group router
+    bool last_sig = false;  // the last forward used the parallel-bounds certified router
     hipStream_t last_stream = nullptr;
     bool timing = false;
     struct Pending { int slot; hipEvent_t a, b; };
@@ -395,7 +399,7 @@ extern "C" lcmoe_status lcmoe_create(const lcmoe_desc *desc, const lcmoe_weights
     if ((st = alloc_n(h, &h->sync, nsync))) return bail(st);
     if (hipMemset(h->sync, 0, sizeof(uint32_t) * nsync) != hipSuccess)
         return bail(fail(LCMOE_ERR_HIP, "workspace clear failed"));
-    if (D.route_kind == LCMOE_ROUTE_SIGMOID_GROUP) {
+    if (D.route_kind == LCMOE_ROUTE_SIGMOID_GROUP || E >= kParallelBoundsMinE) {
         if ((st = alloc_n(h, &h->sig_bnd, 2 * Tm * E))) return bail(st);
         if ((st = alloc_n(h, &h->sig_sync, Tm))) return bail(st);
         if ((st = alloc_n(h, &h->sig_flag, Tm))) return bail(st);
@@ -566,13 +570,18 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
     // the fast router reads the whole router matrix once per token: past
     // kFastRouterElems multiply-adds per forward the chain router, which
     // reads each router row once per 8 tokens, is the faster one
-    const bool fast = route_fast_ok(ra) && (int64_t)T * E * d <= kFastRouterElems;
-    // the sigmoid-group kind's certified router (its weights, like the fast
-    // router's, come from the chains beside gate/up and the combine)
+    // the certified router with parallel float64 bounds (E / 4 blocks per
+    // token, the last one certifying): the sigmoid-group kind's, and at one
+    // token the softmax kinds' when E >= kParallelBoundsMinE (the fast
+    // router's single block would read the whole router matrix alone).  Its
+    // weights, like the fast router's, come from the chains and the combine.
     RouterArgs rs = ra;
     rs.bnd = h->sig_bnd;
     rs.tsync = h->sig_sync;
     rs.flag = h->sig_flag;
+    const bool par = T == 1 && E >= kParallelBoundsMinE &&
+                     D.route_kind != LCMOE_ROUTE_SIGMOID_GROUP && route_sig_ok(rs);
+    const bool fast = !par && route_fast_ok(ra) && (int64_t)T * E * d <= kFastRouterElems;
     const bool sig = !fast && route_sig_ok(rs) && (int64_t)T * E * d <= kSigRouterElems;
     // With the certified fast router, selection, dispatch and activations
     // come from it; the exact chains of the routing weights run in extra

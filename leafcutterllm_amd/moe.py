@@ -129,7 +129,8 @@ class MoeFfn:
         return out
 
     def route_fallbacks(self) -> int:
-        """Tokens of the last forward that the certified sigmoid-group router
+        """Tokens of the last forward that the parallel-bounds certified
+        router (sigmoid-group kind; softmax kinds at one token with E >= 32)
         left to the exact chain logits; -1 when that forward did not use it."""
         n = np.zeros(1, np.int32)
         check(lib().lcmoe_debug_route_fallbacks(self._h, _ptr(n)), "lcmoe_debug_route_fallbacks")

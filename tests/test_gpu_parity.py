@@ -272,6 +272,44 @@ def test_sigmoid_router_mixed_tokens():
     assert int(tied.sum()) <= fb <= int(tied.sum()) + max(1, T // 8), fb
 
 
+WIDE_CFG = small_config("wide64", 512, 256, 64, 4, L.ROUTE_SOFTMAX_RENORM, Q4, Q4, n_shared=1,
+                        d_ff_shared=256)
+
+
+@pytest.mark.parametrize("kind", [L.ROUTE_SOFTMAX_RENORM, L.ROUTE_SOFTMAX])
+def test_wide_softmax_router_one_token(kind):
+    """E >= 32 at one token: the softmax kinds take the parallel-bounds
+    certified router, which certifies (nearly) every token and, in the same
+    launch, dispatches; routing, dispatch and weights equal the oracle's."""
+    cfg = small_config("wide64", 512, 256, 64, 4, kind, Q4, Q4, n_shared=1, d_ff_shared=256)
+    layer = L.synth_layer(cfg, seed=41)
+    for i in range(6):
+        x = L.synth_x(cfg, 1, seed=41, index=i)
+        with L.MoeFfn(cfg.desc(1), layer) as moe:
+            res = run_and_check(cfg, layer, x, moe=moe)
+            assert 0 <= moe.route_fallbacks() <= 1
+        assert res["rel_l2"] < 1e-3
+
+
+def test_wide_softmax_router_exact_tie_falls_back():
+    """Experts 5 and 9 share a router row that leads every logit: their
+    bounds cannot order them, so the certifying block runs the exact chains
+    and selection itself (one token), which rank 5 before 9."""
+    cfg = WIDE_CFG
+    layer = L.synth_layer(cfg, seed=43)
+    x = L.synth_x(cfg, 1, seed=43, index=0)
+    r = layer["router"].copy()
+    r[:, 5] = 4.0 * np.sign(x[0]) / np.sqrt(cfg.d_model)
+    r[:, 9] = r[:, 5]
+    layer["router"] = r
+    with L.MoeFfn(cfg.desc(1), layer) as moe:
+        res = run_and_check(cfg, layer, x, moe=moe)
+        assert moe.route_fallbacks() == 1
+    idx = res["topk_idx"].reshape(1, cfg.n_expert_used)
+    assert idx[0, 0] == 5 and idx[0, 1] == 9
+    assert res["rel_l2"] < 1e-3
+
+
 def test_e1_k1_reduces_to_dense_ffn():
     """E = 1, K = 1, renormalised: weight exactly 1.0 and the layer is the
     dense SwiGLU ffn_forward (engine.rs:146-164) of the one expert."""
