@@ -253,6 +253,40 @@ __device__ __forceinline__ uint32_t ord_key(float f) {
 // experts fused into the routed launch, in ns slices of sl tokens).  Shared
 // launch (shared = 1): slot s is shared expert s over all T tokens,
 // positions s*T + t.
+// Matrix-core activation format of one 32-column sub-block sbi of row t
+// (row width d, a multiple of 256): the f16 hi = f16(v) and lo = f16(v - hi)
+// halves at columns 32 (sbi % 8) .. +31 of the row's super-block piece sbi / 8
+// (hi[256] then lo[256]), and the sub-block's sum of (hi + lo), added in
+// column order, as a (hi, lo) pair.  v: the 32 values, 16-byte aligned.
+__device__ inline void act16_subblock(const float *v, int64_t t, int d, int sbi,
+                                      _Float16 *__restrict__ x16, _Float16 *__restrict__ xs) {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    const float4 *v4 = reinterpret_cast<const float4 *>(v);
+    _Float16 *piece = x16 + (t * (d >> 8) + (sbi >> 3)) * 512 + 32 * (sbi & 7);
+    h8 *oh = reinterpret_cast<h8 *>(piece);
+    h8 *ol = reinterpret_cast<h8 *>(piece + 256);
+    float sum = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const float4 a = v4[2 * g], b = v4[2 * g + 1];
+        const float f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        h8 hv, lv;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const _Float16 hi = (_Float16)f[i], lo = (_Float16)(f[i] - (float)hi);
+            hv[i] = hi;
+            lv[i] = lo;
+            sum = sum + ((float)hi + (float)lo);
+        }
+        oh[g] = hv;
+        ol[g] = lv;
+    }
+    const _Float16 shi = (_Float16)sum, slo = (_Float16)(sum - (float)shi);
+    const int64_t q = t * (d >> 5) + sbi;
+    xs[q * 2] = shi;
+    xs[q * 2 + 1] = slo;
+}
+
 struct SlotArgs {
     const int32_t *perm, *counts, *offsets, *touched;
     int E, K, T, shared;

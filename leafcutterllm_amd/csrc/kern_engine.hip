@@ -173,9 +173,10 @@ __global__ __launch_bounds__(256) void k_linear_q4k(const uint8_t *__restrict__ 
 // reference) or lens[b] + i (absolute).  freq[d] = 1 / theta^(2d/hd) comes
 // from the host.  Block (q, head): heads [0, H) rotate q, [H, H + KVH)
 // rotate k into the cache, [H + KVH, H + 2 KVH) copy v into it.
-__global__ __launch_bounds__(128) void k_rope_kv(const float *__restrict__ qkv, int nq, int T,
-                                                 int seq0, const int32_t *__restrict__ lens, int H,
-                                                 int KVH, int hd, const float *__restrict__ freq,
+__global__ __launch_bounds__(128) void k_rope_kv(const float *__restrict__ qkv, int ks,
+                                                 int64_t stride, int nq, int T, int seq0,
+                                                 const int32_t *__restrict__ lens, int H, int KVH,
+                                                 int hd, const float *__restrict__ freq,
                                                  int absolute, float *__restrict__ qo,
                                                  _Float16 *__restrict__ kc,
                                                  _Float16 *__restrict__ vc, int ctx) {
@@ -185,17 +186,23 @@ __global__ __launch_bounds__(128) void k_rope_kv(const float *__restrict__ qkv, 
     const int pos = lens[b] + i;
     const int half = hd / 2, ldq = (H + 2 * KVH) * hd;
     const float *src = qkv + (int64_t)q * ldq + (int64_t)hh * hd;
+    // the projection value: its K-slice partials added in slice order
+    auto val = [&](int e) {
+        float v = src[e];
+        for (int z = 1; z < ks; z++) v = v + src[z * stride + e];
+        return v;
+    };
     const int64_t crow = ((int64_t)b * ctx + pos) * KVH * hd;
     if (hh >= H + KVH) {  // v
         _Float16 *dst = vc + crow + (int64_t)(hh - H - KVH) * hd;
-        for (int e = threadIdx.x; e < hd; e += blockDim.x) dst[e] = (_Float16)src[e];
+        for (int e = threadIdx.x; e < hd; e += blockDim.x) dst[e] = (_Float16)val(e);
         return;
     }
     const float fp = (float)(absolute ? pos : i);
     for (int d = threadIdx.x; d < half; d += blockDim.x) {
         const float angle = fp * freq[d];
         const float c = cosf(angle), s = sinf(angle);
-        const float x1 = src[d], x2 = src[d + half];
+        const float x1 = val(d), x2 = val(d + half);
         const float y1 = x1 * c - x2 * s, y2 = x1 * s + x2 * c;
         if (hh < H) {
             float *dst = qo + (int64_t)q * H * hd + (int64_t)hh * hd;
@@ -319,9 +326,14 @@ __global__ __launch_bounds__(256) void k_attn_part(const float *__restrict__ qr,
 }
 
 // out[q][h*hd + d] = sum_c e^(m_c - M) o_c[d] / sum_c e^(m_c - M) l_c
+// With x16, the block's hd outputs also go to the matrix-core activation
+// format (act16_subblock over the row of H * hd, staged through LDS).
 __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ part, int nq,
                                                       int H, int hd, int chunks,
-                                                      float *__restrict__ out) {
+                                                      float *__restrict__ out,
+                                                      _Float16 *__restrict__ x16,
+                                                      _Float16 *__restrict__ xs) {
+    __shared__ __attribute__((aligned(16))) float s_o[256];
     const int q = blockIdx.x, h = blockIdx.y;
     if (q >= nq) return;
     const float *pp = part + ((int64_t)q * H + h) * chunks * (hd + 2);
@@ -339,7 +351,12 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
             if (mc != -INFINITY) acc += expf(mc - M) * pp[c * (hd + 2) + d];
         }
         out[(int64_t)q * H * hd + h * hd + d] = acc / den;
+        s_o[d] = acc / den;
     }
+    if (!x16) return;
+    __syncthreads();
+    const int sb = threadIdx.x;  // this head's 32-column sub-blocks
+    if (sb < hd / 32) act16_subblock(s_o + 32 * sb, q, H * hd, h * (hd / 32) + sb, x16, xs);
 }
 
 // f32::total_cmp order as a signed integer key
@@ -493,18 +510,22 @@ int64_t linear_mfma_part_floats(int N, int K, int T) {
 
 hipError_t launch_linear_mfma(const uint8_t *Wr, int N, int K, const float *X, int T,
                               const float *R, float *Y, int64_t ldy, _Float16 *x16, _Float16 *xs,
-                              float *part, hipStream_t st) {
+                              float *part, hipStream_t st, bool act_ready, int *slices) {
     if (T <= 0 || N <= 0) return hipSuccess;
-    if (!linear_mfma_ok(N, K) || ldy % 4) return hipErrorInvalidValue;
+    if (!linear_mfma_ok(N, K) || ldy % 4 || (slices && (R || ldy != N))) return hipErrorInvalidValue;
     int chunks, ks;
     linear_mfma_plan(N, K, T, chunks, ks);
-    hipError_t e = launch_act16(X, T, K, x16, xs, st);
+    hipError_t e = act_ready ? hipSuccess : launch_act16(X, T, K, x16, xs, st);
     if (e != hipSuccess) return e;
     // one slot of T tokens (the shared-expert form of the slot arguments)
     const SlotArgsHost sa{nullptr, nullptr, nullptr, nullptr, 1, 1, T, 1, 1, 0, INT32_MAX, 1, 32};
     const bool direct = ks == 1 && !R && ldy == N;
     const int64_t stride = (int64_t)T * N;
     e = launch_mfma_down(Wr, 0, x16, xs, sa, 1, chunks, N, K, ks, direct ? Y : part, stride, st);
+    if (slices) {  // the caller adds the slices as it reads them
+        *slices = ks;
+        return e;
+    }
     if (e != hipSuccess || direct) return e;
     hipLaunchKernelGGL(k_linear_reduce, dim3((N / 4 + 255) / 256, T), dim3(256), 0, st, part, ks,
                        stride, N, R, Y, ldy);
@@ -513,21 +534,26 @@ hipError_t launch_linear_mfma(const uint8_t *Wr, int N, int K, const float *X, i
 
 hipError_t launch_rope_kv(const float *qkv, int nq, int T, int seq0, const int32_t *lens, int H,
                           int KVH, int hd, const float *freq, int absolute, float *qo,
-                          _Float16 *kc, _Float16 *vc, int ctx, hipStream_t st) {
+                          _Float16 *kc, _Float16 *vc, int ctx, hipStream_t st, int ks,
+                          int64_t stride) {
     if (nq <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_rope_kv, dim3(nq, H + 2 * KVH), dim3(128), 0, st, qkv, nq, T, seq0, lens,
-                       H, KVH, hd, freq, absolute, qo, kc, vc, ctx);
+    if (ks < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_rope_kv, dim3(nq, H + 2 * KVH), dim3(128), 0, st, qkv, ks, stride, nq, T,
+                       seq0, lens, H, KVH, hd, freq, absolute, qo, kc, vc, ctx);
     return hipGetLastError();
 }
 
 hipError_t launch_attention(const float *qr, int nq, int T, int seq0, const int32_t *lens, int H,
                             int KVH, int hd, const _Float16 *kc, const _Float16 *vc, int ctx,
-                            float *part, float *out, hipStream_t st) {
+                            float *part, float *out, hipStream_t st, _Float16 *x16,
+                            _Float16 *xs) {
     if (nq <= 0) return hipSuccess;
+    if (x16 && ((H * hd) % 256 || hd % 32 || hd > 256)) return hipErrorInvalidValue;
     const int chunks = (ctx + kAttnChunk - 1) / kAttnChunk;
     hipLaunchKernelGGL(k_attn_part, dim3(nq, H, chunks), dim3(256), 0, st, qr, nq, T, seq0, lens,
                        H, KVH, hd, kc, vc, ctx, chunks, part);
-    hipLaunchKernelGGL(k_attn_combine, dim3(nq, H), dim3(128), 0, st, part, nq, H, hd, chunks, out);
+    hipLaunchKernelGGL(k_attn_combine, dim3(nq, H), dim3(128), 0, st, part, nq, H, hd, chunks, out,
+                       x16, xs);
     return hipGetLastError();
 }
 

@@ -225,12 +225,20 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ Yr, i
 
 // CpuBackend::rms_norm (rust/src/backend/cpu.rs:49-60), bit for bit: one
 // wave per token (rmsnorm_wave, norm_device.h).
+// With x16, the normed row also goes to the matrix-core activation format
+// (act16_subblock, read back from out after this wave's stores).
 __global__ __launch_bounds__(64) void k_rmsnorm(const float *__restrict__ x,
                                                 const float *__restrict__ w, float eps, int d,
-                                                float *__restrict__ out) {
+                                                float *__restrict__ out,
+                                                _Float16 *__restrict__ x16,
+                                                _Float16 *__restrict__ xs) {
     __shared__ float s_sq[kRmsnormLds];
     const int64_t t = blockIdx.x;
     rmsnorm_wave(x + t * d, w, eps, d, out + t * d, s_sq);
+    if (!x16) return;
+    __threadfence_block();
+    for (int sb = threadIdx.x; sb < (d >> 5); sb += 64)
+        act16_subblock(out + t * d + 32 * sb, t, d, sb, x16, xs);
 }
 
 template <int QT>
@@ -295,8 +303,9 @@ hipError_t launch_combine(const float *Yr, int ks_r, int64_t stride_r, const flo
 }
 
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int T, int d, float *out,
-                          hipStream_t st) {
-    hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(64), 0, st, x, w, eps, d, out);
+                          hipStream_t st, _Float16 *x16, _Float16 *xs) {
+    if (x16 && d % 256) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(64), 0, st, x, w, eps, d, out, x16, xs);
     return hipGetLastError();
 }
 

@@ -1249,33 +1249,7 @@ __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int 
     const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // sub-block index
     const int nsb = d >> 5;
     if (q >= (int64_t)T * nsb) return;
-    const int64_t t = q / nsb;
-    const int sbi = (int)(q % nsb);
-    const float4 *v = reinterpret_cast<const float4 *>(x + q * 32);
-    _Float16 *piece = x16 + (t * (d >> 8) + (sbi >> 3)) * 512 + 32 * (sbi & 7);
-    half8 *oh = reinterpret_cast<half8 *>(piece);
-    half8 *ol = reinterpret_cast<half8 *>(piece + 256);
-    float sum = 0.0f;
-#pragma unroll
-    for (int g = 0; g < 4; g++) {
-        const float4 a = v[2 * g], b = v[2 * g + 1];
-        const float f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        half8 hv, lv;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            _Float16 hi, lo;
-            split16(f[i], hi, lo);
-            hv[i] = hi;
-            lv[i] = lo;
-            sum = sum + ((float)hi + (float)lo);
-        }
-        oh[g] = hv;
-        ol[g] = lv;
-    }
-    _Float16 hi, lo;
-    split16(sum, hi, lo);
-    xs[q * 2] = hi;
-    xs[q * 2 + 1] = lo;
+    act16_subblock(x + q * 32, q / nsb, d, (int)(q % nsb), x16, xs);
 }
 
 SlotArgs dev_slots(const SlotArgsHost &s) {

@@ -166,8 +166,10 @@ constexpr int64_t kShardScratchFloats = LCMOE_SHARD_SCRATCH_FLOATS;
 hipError_t shard_scratch(float **out);
 // out[t] = rms_norm(x[t]) * w, bit-exact with the reference CPU backend
 // (rust/src/backend/cpu.rs:49-60); x, w, out 16-byte aligned, d % 4 == 0.
+// With x16 (d % 256 == 0) the normed rows also go to the matrix-core
+// activation format in x16 / xs (act16_subblock).
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int T, int d, float *out,
-                          hipStream_t st);
+                          hipStream_t st, _Float16 *x16 = nullptr, _Float16 *xs = nullptr);
 
 // C[m,n] = A[m,k] B[k,n] in f32, bit-identical to the CPU backend's
 // avx2_matmul order (kern_matmul.hip); m <= 65535 * 8.
@@ -189,15 +191,26 @@ hipError_t launch_linear(int qt, const uint8_t *W, int N, int K, const float *X,
 // which a reduce adds in slice order (then R) into Y (row stride ldy).
 inline bool linear_mfma_ok(int64_t N, int64_t K) { return N % 64 == 0 && K % 256 == 0; }
 int64_t linear_mfma_part_floats(int N, int K, int T);
+// act_ready: x16 / xs already hold X's pieces (X is not read).  slices !=
+// null (R null): no reduce; the K-slice partials stay in part (several) or
+// in Y (one, ldy == N), and *slices receives their number (the slices of
+// row t at part + z * T * N + t * N, z in order).
 hipError_t launch_linear_mfma(const uint8_t *Wr, int N, int K, const float *X, int T,
                               const float *R, float *Y, int64_t ldy, _Float16 *x16, _Float16 *xs,
-                              float *part, hipStream_t st);
+                              float *part, hipStream_t st, bool act_ready = false,
+                              int *slices = nullptr);
+// qkv: ks K-slice partials of the projection, `stride` floats apart, added
+// in slice order as they are read (ks = 1: the projection itself)
 hipError_t launch_rope_kv(const float *qkv, int nq, int T, int seq0, const int32_t *lens, int H,
                           int KVH, int hd, const float *freq, int absolute, float *qo,
-                          _Float16 *kc, _Float16 *vc, int ctx, hipStream_t st);
+                          _Float16 *kc, _Float16 *vc, int ctx, hipStream_t st, int ks = 1,
+                          int64_t stride = 0);
+// With x16 (H * hd % 256 == 0), the output rows also go to the matrix-core
+// activation format (act16_subblock) for the output projection.
 hipError_t launch_attention(const float *qr, int nq, int T, int seq0, const int32_t *lens, int H,
                             int KVH, int hd, const _Float16 *kc, const _Float16 *vc, int ctx,
-                            float *part, float *out, hipStream_t st);
+                            float *part, float *out, hipStream_t st, _Float16 *x16 = nullptr,
+                            _Float16 *xs = nullptr);
 hipError_t launch_argmax(const float *logits, int nseq, int V, int seq0, int32_t *next,
                          int32_t *out, int out_ld, const int32_t *step, hipStream_t st);
 hipError_t launch_advance(int32_t *lens, int seq0, int nseq, int T, int32_t *step, int dstep,

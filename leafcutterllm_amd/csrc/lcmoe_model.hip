@@ -169,15 +169,31 @@ lcmoe_status forward_dev(lcmoe_model *m, int seq0, int nseq, int T, const int32_
     for (int l = 0; l < D.n_layer; l++) {
         const auto &L = m->layers[l];
         _Float16 *kc = m->kc + l * cache_layer, *vc = m->vc + l * cache_layer;
-        HIP_TRY(launch_rmsnorm(m->hidden, L.attn_norm, D.norm_eps, nq, d, m->xn, st));
-        HIP_TRY(linear(L.wqkv, L.wqkv_r, nqkv, d, m->xn, nq, nullptr, m->qkv, nqkv));
-        HIP_TRY(launch_rope_kv(m->qkv, nq, T, seq0, m->lens, H, KVH, hd, m->freq,
-                               D.rope_positions == LCMOE_ROPE_ABSOLUTE, m->qr, kc, vc, D.max_ctx,
-                               st));
+        // Batches on the matrix-core linears: the attention norm also writes
+        // the QKV projection's f16 pieces, RoPE adds the projection's K
+        // slices as it reads them, and the attention's combine writes the
+        // output projection's pieces (no launches of their own).
+        const bool mq = L.wqkv_r && nq >= 2;
+        const bool mo = L.wo_r && nq >= 2 && hd % 32 == 0 && hd <= 256;  // whole sub-blocks per head
+        HIP_TRY(launch_rmsnorm(m->hidden, L.attn_norm, D.norm_eps, nq, d, m->xn, st,
+                               mq ? m->x16 : nullptr, m->xs16));
+        int ks = 1;
+        if (mq)
+            HIP_TRY(launch_linear_mfma(L.wqkv_r, nqkv, d, nullptr, nq, nullptr, m->qkv, nqkv,
+                                       m->x16, m->xs16, m->lpart, st, true, &ks));
+        else
+            HIP_TRY(linear(L.wqkv, nullptr, nqkv, d, m->xn, nq, nullptr, m->qkv, nqkv));
+        HIP_TRY(launch_rope_kv(ks > 1 ? m->lpart : m->qkv, nq, T, seq0, m->lens, H, KVH, hd,
+                               m->freq, D.rope_positions == LCMOE_ROPE_ABSOLUTE, m->qr, kc, vc,
+                               D.max_ctx, st, ks, (int64_t)nq * nqkv));
         HIP_TRY(launch_attention(m->qr, nq, T, seq0, m->lens, H, KVH, hd, kc, vc, D.max_ctx,
-                                 m->part, m->attn, st));
+                                 m->part, m->attn, st, mo ? m->x16 : nullptr, m->xs16));
         // hidden += attn W_o (Tensor::add, engine.rs:106)
-        HIP_TRY(linear(L.wo, L.wo_r, d, H * hd, m->attn, nq, m->hidden, m->hidden, d));
+        if (mo)
+            HIP_TRY(launch_linear_mfma(L.wo_r, d, H * hd, nullptr, nq, m->hidden, m->hidden, d,
+                                       m->x16, m->xs16, m->lpart, st, true));
+        else
+            HIP_TRY(linear(L.wo, L.wo_r, d, H * hd, m->attn, nq, m->hidden, m->hidden, d));
         // hidden += ffn(rms_norm(hidden)) (engine.rs:109-115)
         lcmoe_status s = lcmoe_forward_norm_residual_dev(L.moe, m->hidden, nq, m->hidden, st);
         if (s) return s;
