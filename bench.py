@@ -484,9 +484,12 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": ("f32 in/out; expert products on exact weights (f16 sc*q) with f16 hi+lo "
-                  "activations (~22 bits) on MFMA when T*K > E, exact int8 dot4 on 15-bit "
-                  "two-limb activations when T*K <= E; f32 accumulate"),
+        "dtype": (("f32 in/out; expert products exact int8 dot4 of the Q8_0 weights with "
+                   "15-bit two-limb activations at every T; f32 accumulate")
+                  if cfg.qtype_gate == L.TYPE_Q8_0 else
+                  ("f32 in/out; expert products on exact weights (f16 sc*q) with f16 hi+lo "
+                   "activations (~22 bits) on MFMA when T*K > E, exact int8 dot4 on 15-bit "
+                   "two-limb activations when T*K <= E; f32 accumulate")),
         "data": ("synthetic (seeded splitmix64 N(0,1) activations, N(0,0.02) weights quantised "
                  f"to {qdesc})"),
         "config": {
