@@ -245,14 +245,6 @@ __device__ __forceinline__ uint32_t ord_key(float f) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Which expert a block of an expert-product launch serves.  Routed launch:
-// slot i < nr serves touched[i] (nothing when i >= number touched) over
-// positions p in [offsets[e], offsets[e] + counts[e]) whose token is
-// perm[p] / K; slot nr + s*ns + c serves tokens [c*sl, c*sl + sl) of shared
-// expert s < S, stored as expert E + s, at positions sbase + s*T + t (shared
-// experts fused into the routed launch, in ns slices of sl tokens).  Shared
-// launch (shared = 1): slot s is shared expert s over all T tokens,
-// positions s*T + t.
 // Matrix-core activation format of one 32-column sub-block sbi of row t
 // (row width d, a multiple of 256): the f16 hi = f16(v) and lo = f16(v - hi)
 // halves at columns 32 (sbi % 8) .. +31 of the row's super-block piece sbi / 8
@@ -287,6 +279,16 @@ __device__ inline void act16_subblock(const float *v, int64_t t, int d, int sbi,
     xs[q * 2 + 1] = slo;
 }
 
+// Which expert a block of an expert-product launch serves.  Routed launch:
+// slot i < nr serves touched[i] (nothing when i >= number touched) over
+// positions p in [offsets[e], offsets[e] + counts[e]) whose token is
+// perm[p] / K; slot nr + s*ns + c serves tokens [c*sl, c*sl + sl) of shared
+// expert s < S, stored as expert E + s, at positions sbase + s*T + t (shared
+// experts fused into the routed launch, in ns slices of sl tokens).  With
+// pslots, routed slot i < nr is pass slot i instead: pass p of expert e
+// (pslots[1 + i] = 256 p + e; nothing when i >= pslots[0]), positions
+// offsets[e] + 32 p onward, at most 32.  Shared launch (shared = 1): slot s
+// is shared expert s over all T tokens, positions s*T + t.
 struct SlotArgs {
     const int32_t *perm, *counts, *offsets, *touched;
     int E, K, T, shared;
