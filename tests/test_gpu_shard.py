@@ -36,7 +36,8 @@ def _bits(x):
 @pytest.mark.parametrize("qtype", [Q8, Q4])
 @pytest.mark.parametrize("m,k,n", [(1, 64, 32), (1, 1, 4096), (3, 101, 96), (8, 16, 64),
                                    (9, 250, 288), (17, 33, 1056), (64, 512, 512),
-                                   (1, 2048, 2048)])
+                                   (1, 2048, 2048), (1, 777, 1056), (2, 1000, 96),
+                                   (4, 700, 160), (16, 300, 64)])
 def test_shard_matmul_bit_exact(qtype, m, k, n):
     a, b = _case(qtype, m, k, n, seed=m * 1000 + k + n)
     dev = L.shard_matmul(qtype, a, b, k, n)
