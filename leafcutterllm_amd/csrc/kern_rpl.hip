@@ -27,8 +27,12 @@ namespace {
 
 constexpr int kWaves = 4;
 
-__device__ __forceinline__ void unpack_hdr(uint4 h, float (&dl)[8], float (&ml)[8]) {
+// (d2, dmin2) scale sub-blocks 4-7: the split layout's second half block
+// (lcmoe_host.cpp repack_rpl64_q4k_split); the header's own pair otherwise
+__device__ __forceinline__ void unpack_hdr(uint4 h, float (&dl)[8], float (&ml)[8],
+                                           const uint32_t *db = nullptr) {
     const float d = dh2f(h.x & 0xffff), dmin = dh2f(h.x >> 16);
+    const float d2 = db ? dh2f(*db & 0xffff) : d, dmin2 = db ? dh2f(*db >> 16) : dmin;
     // get_scale_min_k4 (rust/src/kernels/mod.rs:54-63) for all 8 sub-blocks
     const uint32_t sc03 = h.y & 0x3F3F3F3Fu, m03 = h.z & 0x3F3F3F3Fu;
     const uint32_t sc47 = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
@@ -36,24 +40,30 @@ __device__ __forceinline__ void unpack_hdr(uint4 h, float (&dl)[8], float (&ml)[
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         dl[i] = d * (float)((sc03 >> (8 * i)) & 0xffu);
-        dl[4 + i] = d * (float)((sc47 >> (8 * i)) & 0xffu);
+        dl[4 + i] = d2 * (float)((sc47 >> (8 * i)) & 0xffu);
         ml[i] = dmin * (float)((m03 >> (8 * i)) & 0xffu);
-        ml[4 + i] = dmin * (float)((m47 >> (8 * i)) & 0xffu);
+        ml[4 + i] = dmin2 * (float)((m47 >> (8 * i)) & 0xffu);
     }
 }
 
 // One 256-element super-block of this lane's row against NT token rows.
 // xh/xl point at the tokens' limbs for this super-block (as ints), xs/xm at
 // their 8 sub-block scales / quantised sums.
+// With db (split layout), sub-blocks 4-7 take the second (d, dmin); with
+// first_half, only sub-blocks 0-3 exist (the last block of a row whose length
+// is an odd multiple of 128: the rest lies past the row).
 template <int NT>
 __device__ __forceinline__ void q4_block_dot(const uint4 (&c)[9], const int *const (&xh)[NT],
                                              const int *const (&xl)[NT],
                                              const float *const (&xs)[NT],
-                                             const float *const (&xm)[NT], float (&acc)[NT]) {
+                                             const float *const (&xm)[NT], float (&acc)[NT],
+                                             const uint32_t *db = nullptr,
+                                             bool first_half = false) {
     float dl[8], ml[8];
-    unpack_hdr(c[0], dl, ml);
+    unpack_hdr(c[0], dl, ml, db);
 #pragma unroll
     for (int j = 0; j < 4; j++) {
+        if (j >= 2 && first_half) break;
         const uint4 a = c[1 + 2 * j], b = c[2 + 2 * j];
         const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
         int lo[8], hi[8];
@@ -158,6 +168,48 @@ __device__ __forceinline__ void pass1(const uint4 *__restrict__ W, int kb0, int 
         dot_sb<NT>(c1, kb + 1, X, row, acc);
     }
     if (kb < kb1) dot_sb<NT>(c0, kb, X, row, acc);
+}
+
+// ---- Q4_K down in the split layout ----------------------------------------
+// Rows whose length F is an odd multiple of 128 (repack_rpl64_q4k_split): per
+// 64-row tile and virtual super-block (256 of the row's own columns), the
+// nine 1 KiB chunks of the RPL64 layout, then the 64 rows' second (d, dmin)
+// for sub-blocks 4-7: 592 uint4.  The last virtual block of a row holds only
+// sub-blocks 0-3 (the rest would lie past F and is never read, neither are
+// the activations there).
+constexpr int kSplitUint4 = (9 * 1024 + 256) / 16;
+
+__device__ __forceinline__ void load_split(uint4 (&c)[9], uint32_t &db, const uint4 *W, int kb,
+                                           int lane) {
+    const uint4 *p = W + (int64_t)kb * kSplitUint4;
+#pragma unroll
+    for (int i = 0; i < 9; i++) c[i] = p[i * 64];
+    db = reinterpret_cast<const uint32_t *>(p - lane + 9 * 64)[lane];
+}
+
+template <int NT>
+__device__ __forceinline__ void pass1_split(const uint4 *__restrict__ W, int kb0, int kb1, int nkb,
+                                            bool half_last, const Limbs &X, const int (&row)[NT],
+                                            float (&acc)[NT]) {
+    if (kb0 >= kb1) return;
+    const int lane = threadIdx.x & 63;
+    uint4 c0[9], c1[9];
+    uint32_t d0, d1;
+    load_split(c0, d0, W, kb0, lane);
+    auto dot = [&](const uint4 (&c)[9], const uint32_t &db, int kb) {
+        const int *xh[NT], *xl[NT];
+        const float *xs[NT], *xm[NT];
+        token_ptrs<NT>(X, row, kb, xh, xl, xs, xm);
+        q4_block_dot<NT>(c, xh, xl, xs, xm, acc, &db, half_last && kb == nkb - 1);
+    };
+    int kb = kb0;
+    for (; kb + 2 <= kb1; kb += 2) {
+        load_split(c1, d1, W, kb + 1, lane);
+        dot(c0, d0, kb);
+        load_split(c0, d0, W, min(kb + 2, kb1 - 1), lane);
+        dot(c1, d1, kb + 1);
+    }
+    if (kb < kb1) dot(c0, d0, kb);
 }
 
 // ---- Q6_K down in the RPL64 Q6_K layout -----------------------------------
@@ -495,6 +547,8 @@ __device__ __forceinline__ void down_chunk(const uint4 *W, const uint16_t *D, in
         pass1_q6<NT>(W, D, kb0, kb1, X, row, acc);
     else if constexpr (FMT == 2)
         pass1_q8<NT>(W, kb0, kb1, X, row, acc);
+    else if constexpr (FMT == 3)
+        pass1_split<NT>(W, kb0, kb1, (X.len + 255) >> 8, (X.len & 255) != 0, X, row, acc);
     else
         pass1<NT>(W, kb0, kb1, X, row, acc);
 #pragma unroll
@@ -512,8 +566,8 @@ __device__ __forceinline__ void down_chunk(const uint4 *W, const uint16_t *D, in
 // grid (d/64 tiles, slots, ksplit): block z covers super-block slices
 // 4z .. 4z+3 of the 4*ksplit slices of the F dimension; its partial row sums
 // go to Y + z * split_stride and the combine adds the splits in order.
-// FMT: RPL64 Q4_K (576 uint4 per tile and super-block), Q6_K (840) or
-// Q8_0 (1,088)
+// FMT: RPL64 Q4_K (576 uint4 per tile and super-block), Q6_K (840), Q8_0
+// (1,088) or split Q4_K (592 per tile and virtual super-block)
 template <int FMT>
 __global__ __launch_bounds__(256) void k_rpl_down(
     const uint8_t *__restrict__ down, int64_t estride, const int8_t *__restrict__ xh,
@@ -526,11 +580,11 @@ __global__ __launch_bounds__(256) void k_rpl_down(
     p0 = __builtin_amdgcn_readfirstlane(p0);
     n = __builtin_amdgcn_readfirstlane(n);
     __shared__ float s_red[kWaves][kMaxNT][64];
-    const int NB = F >> 8, rt = blockIdx.x, lane = threadIdx.x & 63;
+    const int NB = FMT == 3 ? (F + 255) >> 8 : F >> 8, rt = blockIdx.x, lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int slices = kWaves * gridDim.z, s = blockIdx.z * kWaves + wave;
     const int kb0 = (int)((int64_t)NB * s / slices), kb1 = (int)((int64_t)NB * (s + 1) / slices);
-    const int tsb = FMT == 1 ? kQ6Uint4 : FMT == 2 ? kQ8Chunks * 64 : 9 * 64;
+    const int tsb = FMT == 1 ? kQ6Uint4 : FMT == 2 ? kQ8Chunks * 64 : FMT == 3 ? kSplitUint4 : 9 * 64;
     const uint4 *T = reinterpret_cast<const uint4 *>(down + (int64_t)e * estride) +
                      (int64_t)rt * NB * tsb;
     const uint4 *W = T + lane;
@@ -582,6 +636,9 @@ hipError_t launch_rpl_down(const uint8_t *down, int64_t estride, const int8_t *h
                            d, F, Y, split_stride);
     else if (fmt == 2)
         hipLaunchKernelGGL(k_rpl_down<2>, grid, dim3(256), 0, st, down, estride, hh, hl, hs, hm, s,
+                           d, F, Y, split_stride);
+    else if (fmt == 3)
+        hipLaunchKernelGGL(k_rpl_down<3>, grid, dim3(256), 0, st, down, estride, hh, hl, hs, hm, s,
                            d, F, Y, split_stride);
     else
         hipLaunchKernelGGL(k_rpl_down<0>, grid, dim3(256), 0, st, down, estride, hh, hl, hs, hm, s,

@@ -110,7 +110,8 @@ hipError_t launch_rpl_gateup(const uint8_t *gate, const uint8_t *up, int64_t est
                              const SlotArgsHost &sa, int slots, int d, int F, float *Hf, int8_t *hh,
                              int8_t *hl, float *hs, float *hm, _Float16 *h16, _Float16 *hs16,
                              const ChainArgs &ch, hipStream_t st, bool q8 = false);
-// fmt: the down matrices are RPL64 Q4_K (0), Q6_K (1) or Q8_0 (2)
+// fmt: the down matrices are RPL64 Q4_K (0), Q6_K (1), Q8_0 (2) or the split
+// Q4_K layout (3, F an odd multiple of 128)
 hipError_t launch_rpl_down(const uint8_t *down, int64_t estride, const int8_t *hh,
                            const int8_t *hl, const float *hs, const float *hm,
                            const SlotArgsHost &sa, int slots, int d, int F, int ksplit, float *Y,

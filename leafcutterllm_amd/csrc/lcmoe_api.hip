@@ -233,8 +233,8 @@ hipError_t timed(lcmoe_handle *h, hipStream_t st, int slot, Fn fn) {
 // launch 10% faster at 4 splits than at 2); each wave keeps >= 2 super-blocks
 // where it can (it loads the next while computing the current one).
 int choose_ksplit(const ExpertSet &s, int d, int active) {
-    if (!s.rpl_dn && !s.q6_dn && !s.q8) return 1;
-    const int NB = s.F / 256, tiles = (d / 64) * std::max(1, active);
+    if (!s.rpl_dn && !s.q6_dn && !s.q8 && !s.split_dn) return 1;
+    const int NB = (s.F + 255) / 256, tiles = (d / 64) * std::max(1, active);
     int ks = 1;
     while (ks < s.kmax && tiles * ks < 1024 && NB >= 4 * ks * 2 * 2) ks *= 2;
     return ks;
@@ -277,12 +277,12 @@ lcmoe_status setup_set(lcmoe_handle *h, ExpertSet &s, int n, int F, int qgu, int
     if ((st = upload_stack(h, &s.down, down, n, qdn, d, F, s.rpl_dn || s.q6_dn || s.q8, &s.sz_dn,
                            s.split_dn, down2, n2)))
         return st;
-    if (s.rpl_dn || s.q6_dn || s.q8) {  // limbs for the row-per-lane down
+    if (s.rpl_dn || s.q6_dn || s.q8 || s.split_dn) {  // limbs for the row-per-lane down
         if ((st = alloc_n(h, &s.hh, positions * F))) return st;
         if ((st = alloc_n(h, &s.hl, positions * F))) return st;
         if ((st = alloc_n(h, &s.hs, positions * F / 32))) return st;
         if ((st = alloc_n(h, &s.hm, positions * F / 32))) return st;
-    } else if (!s.split_dn) {
+    } else {
         if ((st = alloc_n(h, &s.Hf, positions * F))) return st;
     }
     if (s.rpl_gu) {
@@ -462,7 +462,7 @@ static Plan plan_set(lcmoe_handle *h, const ExpertSet &s, bool shared, int T, in
     p.sl = p.mfma ? 32 * p.chunks : 4;
     p.ns = fused ? (T + p.sl - 1) / p.sl : 0;
     const int all = p.slots + fused * p.ns;
-    p.ks = (p.mfma && (s.rpl_dn || s.q6_dn)) || s.split_dn
+    p.ks = p.mfma && (s.rpl_dn || s.q6_dn || s.split_dn)
                ? choose_ksplit_mfma(s, D.d_model, all * p.chunks)
                : choose_ksplit(s, D.d_model, all);
     return p;
@@ -481,10 +481,10 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
                     pl.passes ? h->pass_slots : nullptr};
     const int slots = pl.slots + fused * pl.ns;
     // H between the products in the form the down kernel reads: f16 pieces
-    // for the matrix-core downs, int8 limbs for the row-per-lane ones (Q4_K
-    // and Q6_K below one token per expert), f32 for the generic one
-    const bool h16_out = (pl.mfma && (s.rpl_dn || s.q6_dn)) || s.split_dn;
-    const bool limb_out = !pl.mfma && (s.rpl_dn || s.q6_dn || s.q8);
+    // for the matrix-core downs, int8 limbs for the row-per-lane ones (Q4_K,
+    // split Q4_K and Q6_K below one token per expert), f32 for the generic one
+    const bool h16_out = pl.mfma && (s.rpl_dn || s.q6_dn || s.split_dn);
+    const bool limb_out = !pl.mfma && (s.rpl_dn || s.q6_dn || s.q8 || s.split_dn);
     HIP_TRY(timed(h, st, shared || fused_only ? kSlotGateUpSh : kSlotGateUp, [&] {
         if (pl.mfma)
             return launch_mfma_gateup(s.gate, s.up, s.sz_gu, h->x16, h->x16s, sa, slots,
@@ -501,9 +501,9 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
         if (s.q6_dn && pl.mfma)  // 16-token passes while slots average at most 16 tokens
             return launch_mfma_down_q6(s.down, s.sz_dn, s.h16, sa, slots, pl.chunks, d, s.F,
                                        pl.ks, s.Y, s.positions * d, st, pl.per_slot <= 16);
-        if (s.q6_dn || s.q8)
+        if (s.q6_dn || s.q8 || (s.split_dn && !pl.mfma))
             return launch_rpl_down(s.down, s.sz_dn, s.hh, s.hl, s.hs, s.hm, sa, slots, d, s.F,
-                                   pl.ks, s.Y, s.positions * d, st, s.q8 ? 2 : 1);
+                                   pl.ks, s.Y, s.positions * d, st, s.q8 ? 2 : s.split_dn ? 3 : 1);
         if (s.split_dn || (s.rpl_dn && pl.mfma))
             return launch_mfma_down(s.down, s.sz_dn, s.h16, s.h16s, sa, slots, pl.chunks, d,
                                     s.F, pl.ks, s.Y, s.positions * d, st);
