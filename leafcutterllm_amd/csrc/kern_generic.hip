@@ -223,18 +223,41 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ Yr, i
     reinterpret_cast<float4 *>(y + (int64_t)t * d)[c4] = acc;
 }
 
-// CpuBackend::rms_norm (rust/src/backend/cpu.rs:49-60), bit for bit: one
-// wave per token (rmsnorm_wave, norm_device.h).
+// CpuBackend::rms_norm (rust/src/backend/cpu.rs:49-60), bit for bit, one
+// token per block.  Rows up to kBlockNormD columns run on 256 threads
+// (rmsnorm_block: loads, squares and scaling spread over the block, the four
+// chains on one wave); wider rows on one wave (rmsnorm_wave) in passes of
+// kNormChunkK columns (a 4096-column pass holds more of the row and weights
+// in registers than fit, and spills).
 // With x16, the normed row also goes to the matrix-core activation format
-// (act16_subblock, read back from out after this wave's stores).
+// (act16_subblock, read back from out after the block's stores).
+constexpr int kNormChunkK = 1024;
+constexpr int kBlockNormD = 4 * 256 * kBlockPer;
+
+__global__ __launch_bounds__(256) void k_rmsnorm_block(const float *__restrict__ x,
+                                                       const float *__restrict__ w, float eps,
+                                                       int d, float *__restrict__ out,
+                                                       _Float16 *__restrict__ x16,
+                                                       _Float16 *__restrict__ xs) {
+    __shared__ float s_sq[rmsnorm_block_lds(kBlockNormD)];
+    __shared__ float s_scale;
+    const int64_t t = blockIdx.x;
+    rmsnorm_block<256>(x + t * d, w, eps, d, out + t * d, s_sq, &s_scale);
+    if (!x16) return;
+    __threadfence_block();
+    __syncthreads();
+    for (int sb = threadIdx.x; sb < (d >> 5); sb += blockDim.x)
+        act16_subblock(out + t * d + 32 * sb, t, d, sb, x16, xs);
+}
+
 __global__ __launch_bounds__(64) void k_rmsnorm(const float *__restrict__ x,
                                                 const float *__restrict__ w, float eps, int d,
                                                 float *__restrict__ out,
                                                 _Float16 *__restrict__ x16,
                                                 _Float16 *__restrict__ xs) {
-    __shared__ float s_sq[kRmsnormLds];
+    __shared__ float s_sq[rmsnorm_lds<kNormChunkK>()];
     const int64_t t = blockIdx.x;
-    rmsnorm_wave(x + t * d, w, eps, d, out + t * d, s_sq);
+    rmsnorm_wave<kNormChunkK>(x + t * d, w, eps, d, out + t * d, s_sq);
     if (!x16) return;
     __threadfence_block();
     for (int sb = threadIdx.x; sb < (d >> 5); sb += 64)
@@ -305,7 +328,10 @@ hipError_t launch_combine(const float *Yr, int ks_r, int64_t stride_r, const flo
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int T, int d, float *out,
                           hipStream_t st, _Float16 *x16, _Float16 *xs) {
     if (x16 && d % 256) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(64), 0, st, x, w, eps, d, out, x16, xs);
+    if (d <= kBlockNormD)
+        hipLaunchKernelGGL(k_rmsnorm_block, dim3(T), dim3(256), 0, st, x, w, eps, d, out, x16, xs);
+    else
+        hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(64), 0, st, x, w, eps, d, out, x16, xs);
     return hipGetLastError();
 }
 

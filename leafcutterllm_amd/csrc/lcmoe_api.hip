@@ -231,12 +231,14 @@ hipError_t timed(lcmoe_handle *h, hipStream_t st, int slot, Fn fn) {
 // Column splits of the row-per-lane down product so that small batches
 // launch about four blocks per CU (measured: T = 2-3 on config 2 run the down
 // launch 10% faster at 4 splits than at 2); each wave keeps >= 2 super-blocks
-// where it can (it loads the next while computing the current one).
+// (it loads the next while computing the current one).  Config 1 (Q8_0,
+// F = 2816: 11 super-blocks) then splits in two: down 10.8 -> 8.4 us at T = 1,
+// 25.3 -> 20.1 us at T = 8; configs 2 and 5 are unchanged.
 int choose_ksplit(const ExpertSet &s, int d, int active) {
     if (!s.rpl_dn && !s.q6_dn && !s.q8 && !s.split_dn) return 1;
     const int NB = (s.F + 255) / 256, tiles = (d / 64) * std::max(1, active);
     int ks = 1;
-    while (ks < s.kmax && tiles * ks < 1024 && NB >= 4 * ks * 2 * 2) ks *= 2;
+    while (ks < s.kmax && tiles * ks < 1024 && NB >= 4 * ks * 2) ks *= 2;
     return ks;
 }
 

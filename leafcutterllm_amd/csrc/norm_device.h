@@ -18,7 +18,7 @@ namespace rmsnorm_detail {
 // one wave per token squares up to kNormChunk columns at a time into LDS,
 // lane j's terms contiguous, and lanes 0-3 advance the chains from there,
 // four terms per LDS read (each chain is padded with zeros to a multiple of
-// 32 terms, which adds exactly nothing: the sums are never -0); then the
+// 64 terms, which adds exactly nothing: the sums are never -0); then the
 // whole wave scales the row (with one chunk, d <= 4096, the row and the
 // weights are still in registers).
 constexpr int kNormChunk = 4096;
@@ -32,7 +32,7 @@ __device__ inline float next_dn(float q) { return __uint_as_float(__float_as_uin
 __device__ inline bool odd(float q) { return __float_as_uint(q) & 1u; }
 
 // a / b for a >= 0, b > 0, both finite
-__device__ float div_rn_pos(float a, float b) {
+__device__ __forceinline__ float div_rn_pos(float a, float b) {
     float q = (float)((double)a / (double)b);
     if (!(q > 0.0f) || __float_as_uint(q) >= 0x7f800000u) return q;  // 0 or overflow
     for (int it = 0; it < 4; it++) {
@@ -46,7 +46,7 @@ __device__ float div_rn_pos(float a, float b) {
 }
 
 // sqrt(m) for m >= 0
-__device__ float sqrt_rn(float m) {
+__device__ __forceinline__ float sqrt_rn(float m) {
     float s = (float)__builtin_sqrt((double)m);
     if (!(s > 0.0f) || __float_as_uint(s) >= 0x7f800000u) return s;  // 0, inf, NaN
     for (int it = 0; it < 4; it++) {
@@ -58,6 +58,29 @@ __device__ float sqrt_rn(float m) {
     }
     return s;
 }
+// One lane's chain: acc + c[0].x + c[0].y + ... + c[n16 - 1].w in order
+// (n16 a positive multiple of 16 float4s).  Each step issues 16 LDS reads at
+// once and adds their 64 terms as they land (the waits count down the reads
+// in order), so one read latency is exposed per 64 dependent adds.  Reads
+// carried in registers from one step into the next would hide that latency
+// too, but the register allocator then copies them between steps, behind
+// waits, which costs more than it saves.
+__device__ __forceinline__ float chain_sum(const float4 *c, int n16, float acc) {
+    for (int gi = 0; gi < n16; gi += 16) {
+        float4 a[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) a[u] = c[gi + u];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            acc = acc + a[u].x;
+            acc = acc + a[u].y;
+            acc = acc + a[u].z;
+            acc = acc + a[u].w;
+        }
+    }
+    return acc;
+}
+
 // LDS floats rmsnorm_wave<CHUNK> needs
 template <int CHUNK = kNormChunk>
 constexpr int rmsnorm_lds() { return 4 * (CHUNK / 4 + 4); }
@@ -86,8 +109,9 @@ __device__ inline void rmsnorm_wave(const float *__restrict__ x, const float *__
     float4 v[kV], gw[kV];
     float acc = 0.0f;
     for (int c0 = 0; c0 < n4; c0 += kNormChunk / 4) {
-        // q: the chunk's float4 count rounded up to whole groups of 8 per chain
-        const int n = min(kNormChunk / 4, n4 - c0), q = (n + 31) & ~31;
+        // q: the chunk's float4 count rounded up to whole pairs of groups of 8
+        // per chain
+        const int n = min(kNormChunk / 4, n4 - c0), q = (n + 63) & ~63;
 #pragma unroll
         for (int k = 0; k < kV; k++) {  // every load of the chunk in flight at once
             const int i = lane + 64 * k;
@@ -111,27 +135,7 @@ __device__ inline void rmsnorm_wave(const float *__restrict__ x, const float *__
             }
         }
         wave_lds_sync();
-        if (lane < 4) {  // groups of 8 float4s, the next group's reads in flight
-            const float4 *c = reinterpret_cast<const float4 *>(s_sq + lane * ld);
-            float4 cur[8], nxt[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) cur[u] = c[u];
-            for (int gi = 8; gi <= q / 4; gi += 8) {
-                if (gi < q / 4) {
-#pragma unroll
-                    for (int u = 0; u < 8; u++) nxt[u] = c[gi + u];
-                }
-#pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    acc = acc + cur[u].x;
-                    acc = acc + cur[u].y;
-                    acc = acc + cur[u].z;
-                    acc = acc + cur[u].w;
-                }
-#pragma unroll
-                for (int u = 0; u < 8; u++) cur[u] = nxt[u];
-            }
-        }
+        if (lane < 4) acc = chain_sum(reinterpret_cast<const float4 *>(s_sq + lane * ld), q / 4, acc);
         wave_lds_sync();
     }
     float sum = 0.0f;
@@ -167,10 +171,84 @@ __device__ inline void rmsnorm_wave(const float *__restrict__ x, const float *__
     }
 }
 
+// The same norm by a block of NT threads (a multiple of 64, >= 64): every
+// thread loads, squares and later scales its float4s i = tid, tid + NT, ...
+// (held in registers: at most kBlockPer per thread, d <= 4 NT kBlockPer),
+// and the chains run on lanes 0-3 of the first wave exactly as
+// rmsnorm_wave's (the same LDS layout, the same padding, the same order), so
+// the bits are the same.  s_sq: rmsnorm_block_lds(d) floats; s_scale: one
+// float of LDS.  x may be a row the block has just written (callers fence).
+constexpr int kBlockPer = 8;  // d <= 8192 with 256 threads
+__host__ __device__ constexpr int rmsnorm_block_lds(int d) { return 4 * (d / 4 + 64 + 4); }
+
+template <int NT>
+__device__ __attribute__((always_inline)) inline void rmsnorm_block(const float *__restrict__ x, const float *__restrict__ w,
+                                     float eps, int d, float *__restrict__ out, float *s_sq,
+                                     float *s_scale) {
+    const int tid = threadIdx.x, n4 = d >> 2, q = (n4 + 63) & ~63, ld = n4 + 64 + 4;
+    const float4 *r = reinterpret_cast<const float4 *>(x);
+    const float4 *g = reinterpret_cast<const float4 *>(w);
+    // the row and the weights in flight together; a thread past the end
+    // re-reads the last float4 (branch-free loads keep the waits partial)
+    float4 v[kBlockPer], gw[kBlockPer];
+#pragma unroll
+    for (int k = 0; k < kBlockPer; k++)
+        if (NT * k < n4) v[k] = r[min(tid + NT * k, n4 - 1)];
+#pragma unroll
+    for (int k = 0; k < kBlockPer; k++)
+        if (NT * k < n4) gw[k] = g[min(tid + NT * k, n4 - 1)];
+#pragma unroll
+    for (int k = 0; k < kBlockPer; k++) {
+        const int i = tid + NT * k;
+        if (i < n4) {
+            s_sq[i] = v[k].x * v[k].x;
+            s_sq[ld + i] = v[k].y * v[k].y;
+            s_sq[2 * ld + i] = v[k].z * v[k].z;
+            s_sq[3 * ld + i] = v[k].w * v[k].w;
+        } else if (i < q) {  // chain padding: adds exactly nothing
+            s_sq[i] = s_sq[ld + i] = s_sq[2 * ld + i] = s_sq[3 * ld + i] = 0.0f;
+        }
+    }
+    if (NT * kBlockPer < q)  // padding past the threads' float4s (d close to the limit)
+        for (int i = NT * kBlockPer + tid; i < q; i += NT)
+            s_sq[i] = s_sq[ld + i] = s_sq[2 * ld + i] = s_sq[3 * ld + i] = 0.0f;
+    __syncthreads();
+    if (tid < 64) {
+        const int lane = tid;
+        float acc = 0.0f;
+        if (lane < 4 && q > 0)
+            acc = chain_sum(reinterpret_cast<const float4 *>(s_sq + lane * ld), q / 4, acc);
+        float sum = 0.0f;
+        for (int j = 0; j < 4; j++) sum = sum + __shfl(acc, j);
+        if (lane == 0) {
+            const float mean = div_rn_pos(sum, (float)d);
+            const float root = sqrt_rn(mean + eps);
+            *s_scale = root > 0.0f ? div_rn_pos(1.0f, root) : 1.0f / root;
+        }
+    }
+    __syncthreads();
+    const float scale = *s_scale;
+    float4 *o = reinterpret_cast<float4 *>(out);
+#pragma unroll
+    for (int k = 0; k < kBlockPer; k++) {
+        const int i = tid + NT * k;
+        if (i < n4) {
+            float4 a;
+            a.x = v[k].x * scale; a.y = v[k].y * scale;
+            a.z = v[k].z * scale; a.w = v[k].w * scale;
+            a.x = a.x * gw[k].x; a.y = a.y * gw[k].y; a.z = a.z * gw[k].z; a.w = a.w * gw[k].w;
+            o[i] = a;
+        }
+    }
+}
+
 }  // namespace rmsnorm_detail
 
 using rmsnorm_detail::kRmsnormLds;
 using rmsnorm_detail::rmsnorm_lds;
 using rmsnorm_detail::rmsnorm_wave;
+using rmsnorm_detail::rmsnorm_block;
+using rmsnorm_detail::rmsnorm_block_lds;
+using rmsnorm_detail::kBlockPer;
 
 }  // namespace lcmoe

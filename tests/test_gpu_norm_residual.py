@@ -25,7 +25,7 @@ def _bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
-@pytest.mark.parametrize("d", [4, 32, 100, 256, 4096, 4100, 6144, 16384])
+@pytest.mark.parametrize("d", [4, 32, 100, 256, 260, 4096, 4100, 6144, 8192, 8196, 16384])
 def test_device_rmsnorm_bit_exact(d):
     rng = np.random.default_rng(d)
     T = 7
