@@ -130,6 +130,7 @@ __global__ __launch_bounds__(256) void k_down(const uint8_t *__restrict__ down, 
 // rust/src/backend/cpu.rs:66-79: max, sequential sum of exp, divide; for
 // the sigmoid-group kind the selected sigmoid scores over their sequential
 // sum, times the scale) and the first column block stores them to topk_w.
+template <int KC, int KS>
 __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ Yr, int ks_r,
                                                  int64_t stride_r, const float *__restrict__ Ys,
                                                  int ks_s, int64_t stride_s,
@@ -139,13 +140,56 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ Yr, i
                                                  float *y) {
     __shared__ float s_w[kMaxK];
     __shared__ float s_z[kMaxE];
+    __shared__ int s_sel[kMaxK];
     const int t = blockIdx.y, c4 = blockIdx.x * blockDim.x + threadIdx.x;
-    if (cr.logits && cr.kind == LCMOE_ROUTE_SIGMOID_GROUP) {
+    // Loads in two waves, each one memory round trip: first the selected
+    // experts (topk_idx, for the weights) and the rows' positions (inv),
+    // then the routing items' logits and, KC > 0, every row this thread
+    // combines (expert k < KC, k >= K re-reading the last; k-split slice
+    // s < KS, s >= ks re-reading the first; the first shared expert's
+    // slices; the residual), all from a clamped column so no row load sits
+    // under a branch.  Waits retire loads in issue order, so the logits go
+    // out before the rows and the weights are formed while the rows land.
+    // The sums keep the order of the KC == 0 loops: the bits are the same.
+    const bool sig = cr.kind == LCMOE_ROUTE_SIGMOID_GROUP;
+    const bool renorm = cr.kind == LCMOE_ROUTE_SOFTMAX_RENORM;
+    const int n = sig || renorm ? K : cr.E;  // routing items (<= 256 = blockDim)
+    // absent inputs read a valid stand-in (never used), so that no load is
+    // conditional and every wait can leave the younger loads in flight
+    const int tk = min((int)threadIdx.x, K - 1);
+    const int sk = (cr.logits ? cr.topk_idx : inv)[(int64_t)t * K + tk];
+    const int cc = min(c4, (d >> 2) - 1);
+    float4 pr[KC > 0 ? KC : 1][KS], ps[KS], rr;
+    float tw[KC > 0 ? KC : 1];
+    int pos[KC > 0 ? KC : 1];
+    if constexpr (KC > 0) {
+#pragma unroll
+        for (int k = 0; k < KC; k++) {
+            pos[k] = inv[(int64_t)t * K + (k < K ? k : K - 1)];
+            tw[k] = topk_w[(int64_t)t * K + (k < K ? k : K - 1)];
+        }
+        const float4 *src = reinterpret_cast<const float4 *>((S > 0 ? Ys : Yr) + (int64_t)t * d) + cc;
+#pragma unroll
+        for (int s = 0; s < KS; s++) ps[s] = src[(s < ks_s && S > 0 ? s : 0) * stride_s / 4];
+        rr = reinterpret_cast<const float4 *>((resid ? resid : Yr) + (int64_t)t * d)[cc];
+    }
+    const bool biased = cr.logits && !sig && cr.bias;
+    const int e = !cr.logits ? 0 : sig || renorm ? sk : min((int)threadIdx.x, cr.E - 1);
+    const float lv = (cr.logits ? cr.logits + (int64_t)t * cr.E : Yr)[e];
+    const float bv = (biased ? cr.bias : Yr)[biased ? e : 0];
+    __builtin_amdgcn_sched_barrier(0);  // the routing loads stay older than the rows
+    if constexpr (KC > 0) {
+#pragma unroll
+        for (int k = 0; k < KC; k++) {
+            const float4 *src = reinterpret_cast<const float4 *>(Yr + (int64_t)pos[k] * d) + cc;
+#pragma unroll
+            for (int s = 0; s < KS; s++) pr[k][s] = src[(s < ks_r ? s : 0) * stride_r / 4];
+        }
+    }
+    if (cr.logits && sig) {
         // sigmoid scores of the K selected, their sequential sum, the scaled
         // shares (token_weights' expressions)
-        const float *l = cr.logits + (int64_t)t * cr.E;
-        const int32_t *sel = cr.topk_idx + (int64_t)t * K;
-        if (threadIdx.x < K) s_z[threadIdx.x] = sigmoid_cw(l[sel[threadIdx.x]]);
+        if (threadIdx.x < K) s_z[threadIdx.x] = sigmoid_cw(lv);
         __syncthreads();
         if (threadIdx.x == 0) {
             float sum = 0.0f;
@@ -162,14 +206,8 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ Yr, i
         // for the renormalised router, all E otherwise) and their exps are
         // formed in parallel; thread 0 then sums the exps in item order, the
         // sequential sum of CpuBackend::softmax
-        const float *l = cr.logits + (int64_t)t * cr.E;
-        const int32_t *sel = cr.topk_idx + (int64_t)t * K;
-        const bool renorm = cr.kind == LCMOE_ROUTE_SOFTMAX_RENORM;
-        const int n = renorm ? K : cr.E;
-        for (int i = threadIdx.x; i < n; i += blockDim.x) {
-            const int e = renorm ? sel[i] : i;
-            s_z[i] = cr.bias ? l[e] + cr.bias[e] : l[e];
-        }
+        if (threadIdx.x < n) s_z[threadIdx.x] = biased ? lv + bv : lv;
+        if (threadIdx.x < K) s_sel[threadIdx.x] = sk;
         __syncthreads();
         if (threadIdx.x < 64) {
             float mx = -__builtin_inff();
@@ -183,7 +221,7 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ Yr, i
             float sum = 0.0f;
             for (int i = 0; i < n; i++) sum = sum + s_z[i];
             for (int k = 0; k < K; k++) {
-                const float w = (s_z[renorm ? k : sel[k]] / sum) * cr.scale;
+                const float w = (s_z[renorm ? k : s_sel[k]] / sum) * cr.scale;
                 s_w[k] = w;
                 if (blockIdx.x == 0) topk_w[(int64_t)t * K + k] = w;
             }
@@ -192,6 +230,49 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ Yr, i
     }
     if (4 * c4 >= d) return;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if constexpr (KC > 0) {
+#pragma unroll
+        for (int k = 0; k < KC; k++) {
+            if (k >= K) break;
+            const float w = cr.logits ? s_w[k] : tw[k];
+            float4 v = pr[k][0];
+#pragma unroll
+            for (int s = 1; s < KS; s++) {
+                if (s >= ks_r) break;
+                v.x = v.x + pr[k][s].x; v.y = v.y + pr[k][s].y;
+                v.z = v.z + pr[k][s].z; v.w = v.w + pr[k][s].w;
+            }
+            float p;
+            p = w * v.x; acc.x = acc.x + p;
+            p = w * v.y; acc.y = acc.y + p;
+            p = w * v.z; acc.z = acc.z + p;
+            p = w * v.w; acc.w = acc.w + p;
+        }
+        for (int j = 0; j < S; j++) {
+            float4 v;
+            if (j == 0) {
+                v = ps[0];
+#pragma unroll
+                for (int s = 1; s < KS; s++) {
+                    if (s >= ks_s) break;
+                    v.x = v.x + ps[s].x; v.y = v.y + ps[s].y; v.z = v.z + ps[s].z; v.w = v.w + ps[s].w;
+                }
+            } else {
+                const float4 *src = reinterpret_cast<const float4 *>(Ys + ((int64_t)j * T + t) * d) + c4;
+                v = src[0];
+                for (int s = 1; s < ks_s; s++) {
+                    const float4 u = src[s * stride_s / 4];
+                    v.x = v.x + u.x; v.y = v.y + u.y; v.z = v.z + u.z; v.w = v.w + u.w;
+                }
+            }
+            acc.x = acc.x + v.x; acc.y = acc.y + v.y; acc.z = acc.z + v.z; acc.w = acc.w + v.w;
+        }
+        if (resid) {  // hidden + ffn_out (engine.rs:115); resid may be y itself
+            acc.x = rr.x + acc.x; acc.y = rr.y + acc.y; acc.z = rr.z + acc.z; acc.w = rr.w + acc.w;
+        }
+        reinterpret_cast<float4 *>(y + (int64_t)t * d)[c4] = acc;
+        return;
+    }
     for (int k = 0; k < K; k++) {
         const int pos = inv[(int64_t)t * K + k];
         const float w = cr.logits ? s_w[k] : topk_w[(int64_t)t * K + k];
@@ -320,8 +401,23 @@ hipError_t launch_combine(const float *Yr, int ks_r, int64_t stride_r, const flo
                           int64_t stride_s, const int32_t *inv, float *topk_w, int T, int K,
                           int S, int d, const CombineRoute &cr, float *y, hipStream_t st,
                           const float *resid) {
-    hipLaunchKernelGGL(k_combine, dim3((d / 4 + 255) / 256, T), dim3(256), 0, st, Yr, ks_r,
-                       stride_r, Ys, ks_s, stride_s, inv, topk_w, T, K, S, d, cr, resid, y);
+    const dim3 grid((d / 4 + 255) / 256, T);
+    const int ks = std::max(ks_r, S > 0 ? ks_s : 1);
+#define LCMOE_COMBINE(KC, KS)                                                                    \
+    hipLaunchKernelGGL((k_combine<KC, KS>), grid, dim3(256), 0, st, Yr, ks_r, stride_r, Ys, ks_s, \
+                       stride_s, inv, topk_w, T, K, S, d, cr, resid, y)
+    // the prefetching forms for up to 8 experts and 4 k-split slices
+    if (K <= 2 && ks <= 1) LCMOE_COMBINE(2, 1);
+    else if (K <= 2 && ks <= 2) LCMOE_COMBINE(2, 2);
+    else if (K <= 2 && ks <= 4) LCMOE_COMBINE(2, 4);
+    else if (K <= 4 && ks <= 1) LCMOE_COMBINE(4, 1);
+    else if (K <= 4 && ks <= 2) LCMOE_COMBINE(4, 2);
+    else if (K <= 4 && ks <= 4) LCMOE_COMBINE(4, 4);
+    else if (K <= 8 && ks <= 1) LCMOE_COMBINE(8, 1);
+    else if (K <= 8 && ks <= 2) LCMOE_COMBINE(8, 2);
+    else if (K <= 8 && ks <= 4) LCMOE_COMBINE(8, 4);
+    else LCMOE_COMBINE(0, 1);
+#undef LCMOE_COMBINE
     return hipGetLastError();
 }
 
