@@ -85,6 +85,9 @@ SMALL = {
     # gate/up, generic expert kernels and the exact router
     "q4k-d288-generic": small_config(
         "d288", 288, 512, 8, 2, L.ROUTE_SOFTMAX_RENORM, Q4, Q4, n_shared=1, d_ff_shared=256),
+    # more than 8 experts per token: the combine's loop form
+    "k12-shared": small_config(
+        "k12", 256, 256, 32, 12, L.ROUTE_SOFTMAX_RENORM, Q4, Q4, n_shared=1, d_ff_shared=256),
 }
 
 
