@@ -233,6 +233,7 @@ __global__ __launch_bounds__(128) void k_rope_kv(const float *__restrict__ qkv, 
 // 256 threads: scores by two threads per position (half the dims each),
 // then the weighted sum of v by 256 / hd groups of hd threads over
 // interleaved positions, added in LDS.
+template <int NK>  // 16-byte K loads per thread: hd / 2 <= 8 NK
 __global__ __launch_bounds__(256) void k_attn_part(const float *__restrict__ qr, int nq, int T,
                                                    int seq0, const int32_t *__restrict__ lens,
                                                    int H, int KVH, int hd,
@@ -261,21 +262,36 @@ __global__ __launch_bounds__(256) void k_attn_part(const float *__restrict__ qr,
     __shared__ float s_p[kAttnChunk];
     __shared__ float s_red[8];
     __shared__ float s_acc[2048];
-    for (int d = t; d < hd; d += blockDim.x) s_q[d] = qr[(int64_t)q * H * hd + h * hd + d];
-    __syncthreads();
+    // One memory round trip for the block: the query element, the chunk's
+    // K rows and the first group of V rows all go out before anything
+    // waits; positions past np (and K offsets past hd / 2) re-read the last
+    // one, never used, so no load sits under a branch.
+    const float qv = qr[(int64_t)q * H * hd + h * hd + min(t, hd - 1)];
     const int64_t pstride = (int64_t)KVH * hd;  // elements between positions
-    // scores: position p0 + (t % 128), dims [half * hd/2, half * hd/2 + hd/2);
-    // the row's loads are all issued before the products
+    // scores: position p0 + (t % 128), dims [half * hd/2, half * hd/2 + hd/2)
     const int key = t & (kAttnChunk - 1), hf = t >> 7, hd2 = hd / 2;
+    h8 kv[NK];
+    {
+        const _Float16 *kr = kc + ((int64_t)b * ctx + p0 + min(key, np - 1)) * pstride +
+                             kvh * hd + hf * hd2;
+#pragma unroll
+        for (int u = 0; u < NK; u++) kv[u] = *reinterpret_cast<const h8 *>(kr + min(8 * u, hd2 - 8));
+    }
+    // weighted sum of v: thread (position group kg, dims 8 dg .. 8 dg + 7)
+    // over positions kg, kg + KG, ... (one 16-byte load each), then the KG
+    // groups added in LDS
+    const int DG = hd / 8, KG = 256 / DG, dg = t % DG, kg = t / DG;
+    const _Float16 *vr = vc + ((int64_t)b * ctx + p0) * pstride + kvh * hd + 8 * dg;
+    h8 vv[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+        vv[u] = *reinterpret_cast<const h8 *>(vr + min(min(kg, KG - 1) + u * KG, np - 1) * pstride);
+    if (t < hd) s_q[t] = qv;
+    __syncthreads();
     float dot = 0.0f;
     if (key < np) {
-        const _Float16 *kr = kc + ((int64_t)b * ctx + p0 + key) * pstride + kvh * hd + hf * hd2;
-        h8 kv[16];
 #pragma unroll
-        for (int u = 0; u < 16; u++)
-            if (8 * u < hd2) kv[u] = *reinterpret_cast<const h8 *>(kr + 8 * u);
-#pragma unroll
-        for (int u = 0; u < 16; u++)
+        for (int u = 0; u < NK; u++)
             if (8 * u < hd2) {
 #pragma unroll
                 for (int e = 0; e < 8; e++)
@@ -298,18 +314,15 @@ __global__ __launch_bounds__(256) void k_attn_part(const float *__restrict__ qr,
     if ((t & 63) == 0) s_red[4 + (t >> 6)] = l;
     __syncthreads();
     l = s_red[4] + s_red[5];
-    // weighted sum of v: thread (position group kg, dims 8 dg .. 8 dg + 7)
-    // over positions kg, kg + KG, ... (one 16-byte load each, all issued
-    // first), then the KG groups added in LDS
-    const int DG = hd / 8, KG = 256 / DG, dg = t % DG, kg = t / DG;
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     if (kg < KG) {
-        const _Float16 *vr = vc + ((int64_t)b * ctx + p0) * pstride + kvh * hd + 8 * dg;
         for (int k0 = kg; k0 < np; k0 += 8 * KG) {
-            h8 vv[8];
+            if (k0 != kg) {  // groups past the first (hd > 128)
 #pragma unroll
-            for (int u = 0; u < 8; u++)
-                if (k0 + u * KG < np) vv[u] = *reinterpret_cast<const h8 *>(vr + (k0 + u * KG) * pstride);
+                for (int u = 0; u < 8; u++)
+                    if (k0 + u * KG < np)
+                        vv[u] = *reinterpret_cast<const h8 *>(vr + (k0 + u * KG) * pstride);
+            }
 #pragma unroll
             for (int u = 0; u < 8; u++)
                 if (k0 + u * KG < np) {
@@ -561,8 +574,16 @@ hipError_t launch_attention(const float *qr, int nq, int T, int seq0, const int3
     if (nq <= 0) return hipSuccess;
     if (x16 && ((H * hd) % 256 || hd % 32 || hd > 256)) return hipErrorInvalidValue;
     const int chunks = (ctx + kAttnChunk - 1) / kAttnChunk;
-    hipLaunchKernelGGL(k_attn_part, dim3(nq, H, chunks), dim3(256), 0, st, qr, nq, T, seq0, lens,
-                       H, KVH, hd, kc, vc, ctx, chunks, part);
+    const dim3 grid(nq, H, chunks);
+    if (hd <= 64)
+        hipLaunchKernelGGL(k_attn_part<4>, grid, dim3(256), 0, st, qr, nq, T, seq0, lens, H, KVH,
+                           hd, kc, vc, ctx, chunks, part);
+    else if (hd <= 128)
+        hipLaunchKernelGGL(k_attn_part<8>, grid, dim3(256), 0, st, qr, nq, T, seq0, lens, H, KVH,
+                           hd, kc, vc, ctx, chunks, part);
+    else
+        hipLaunchKernelGGL(k_attn_part<16>, grid, dim3(256), 0, st, qr, nq, T, seq0, lens, H, KVH,
+                           hd, kc, vc, ctx, chunks, part);
     hipLaunchKernelGGL(k_attn_combine, dim3(nq, H), dim3(128), 0, st, part, nq, H, hd, chunks, out,
                        x16, xs);
     return hipGetLastError();

@@ -103,6 +103,21 @@ def test_tiny_other_weight_types(qt):
             assert rel(m.forward(np.array([c]))[0], ref.forward(c).astype(np.float64)) < LOGIT_TOL
 
 
+@pytest.mark.parametrize("hd,H,KVH", [(160, 2, 1), (256, 2, 2)])
+def test_tiny_wide_heads(hd, H, KVH):
+    """head_dim above 128 (the attention's widest K-load form, a head_dim
+    that is not a power of two, grouped KV heads) over a prompt longer than
+    one 128-position attention chunk, then single-token steps."""
+    mc = ModelConfig("tiny-wide", 2, H, KVH, hd, 64, 10000.0,
+                     small_config("tiny-wide", 256, 256, 8, 2, L.ROUTE_SOFTMAX_RENORM,
+                                  L.TYPE_Q8_0, L.TYPE_Q8_0), attn_type=L.TYPE_Q8_0)
+    w = synth_model(mc, seed=12)
+    ref = E.RefEngine(spec(mc, E.ROPE_ABSOLUTE), w, threads=8)
+    with model(mc, w, E.ROPE_ABSOLUTE, B=1, P=160, ctx=192) as m:
+        for c in ([(7 * i + 3) % 64 for i in range(150)], [1], [2]):
+            assert rel(m.forward(np.array([c]))[0], ref.forward(c).astype(np.float64)) < LOGIT_TOL
+
+
 def test_config5_two_layer_cut():
     """The config-5 model's shapes (d 2048, 16 heads x 128, vocab 32000, the
     60+4-expert Q4_K MoE) cut to two layers: per-step logits and greedy ids
