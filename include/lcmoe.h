@@ -119,7 +119,16 @@ typedef struct lcmoe_handle lcmoe_handle;
  * scan_for_corruption, rust/src/model/loader.rs:301-422), uploads all
  * weights once to the current HIP device and keeps them resident.
  * Replaces the per-forward GGUFModel::load_layer ingest
- * (rust/src/model/loader.rs:145-168, called from engine.rs:96). */
+ * (rust/src/model/loader.rs:145-168, called from engine.rs:96), including
+ * its sanitize_weights step (loader.rs:161, :241-249): every router, bias and
+ * expert weight whose dequantised value is NaN, +-Inf or |v| > 100 is used
+ * as 0 (see lcmoe_sanitize_blocks; a Q4_K matrix kind with an outlier that
+ * Q4_K cannot hold as zero is stored as f32 and runs the generic kernels).
+ * Divergence: a block whose scale is non-finite or above 1e4 is refused
+ * with LCMOE_ERR_CORRUPT, where the reference's Engine::load reports it and
+ * runs on with the zeroed values (rust/src/inference/engine.rs:22-25); a
+ * caller that wants that behaviour applies lcmoe_sanitize_blocks to the
+ * bytes first, which zeroes non-finite-scale blocks. */
 lcmoe_status lcmoe_create(const lcmoe_desc *desc, const lcmoe_weights *w, lcmoe_handle **out);
 void lcmoe_destroy(lcmoe_handle *h);
 
@@ -138,7 +147,9 @@ lcmoe_status lcmoe_forward_dev(lcmoe_handle *h, const float *x_dev, int32_t T, f
 
 /* Post-attention RMSNorm weight [d_model] f32 and epsilon used by the
  * lcmoe_forward_norm_residual* calls below (the reference passes 1e-5,
- * engine.rs:111).  Copied to the device; may be called again to replace it. */
+ * engine.rs:111).  Copied to the device, sanitised as load_layer sanitises
+ * every layer tensor (rust/src/model/loader.rs:161, :241-249: NaN, +-Inf and
+ * |v| > 100 become 0); may be called again to replace it. */
 lcmoe_status lcmoe_set_norm(lcmoe_handle *h, const float *weight, float eps);
 
 /* The FFN half of a decoder layer with its norm and residual fused:
@@ -183,6 +194,26 @@ size_t lcmoe_tensor_size(int32_t type, int64_t count);
 /* Number of blocks whose scale(s) are non-finite or |.| > 1e4
  * (scan_for_corruption's test, rust/src/model/loader.rs:389-398). */
 int64_t lcmoe_scan_blocks(int32_t type, const uint8_t *data, int64_t count);
+
+/* GGUF bytes -> f32 on the host: GGUFModel::dequantize for F32, Q8_0, Q4_K
+ * and Q6_K (rust/src/model/loader.rs:205-235, decoders
+ * rust/src/kernels/mod.rs:37-180: whole blocks only, a partial tail stays 0),
+ * then, when `sanitize` is nonzero, sanitize_weights (loader.rs:241-249:
+ * NaN, +-Inf and |v| > 100 become 0).  Returns the number of values the
+ * sanitising zeroed, or -1 for a NULL pointer, count < 0 or another type. */
+int64_t lcmoe_dequantize(int32_t type, const uint8_t *data, int64_t count, float *out,
+                         int32_t sanitize);
+
+/* sanitize_weights (loader.rs:241-249) applied to GGUF bytes in place, as
+ * lcmoe_create and lcmoe_model_create apply it to every weight they upload:
+ * an element whose decoded value is NaN, +-Inf or |v| > 100 gets the code of
+ * an exact zero (Q8_0: q = 0; Q6_K: 6-bit code 32; Q4_K: q = 0 where
+ * dmin * m is zero; F32: 0.0f), and a block whose scale is not finite gets
+ * zero scales.  Returns the number of elements zeroed, or -1 as above.
+ * *unzeroable (optional) receives the number of Q4_K outliers left as they
+ * are because their sub-block cannot encode zero; lcmoe_create stores such
+ * a tensor as its sanitised f32 dequantisation instead. */
+int64_t lcmoe_sanitize_blocks(int32_t type, uint8_t *data, int64_t count, int64_t *unzeroable);
 
 /* Quantise f32 to GGUF blocks.  Q8_0 is quantize_f32_to_q8_0
  * (rust/src/kernels/q8_0.rs:90-122); Q4_K and Q6_K are this project's own
@@ -302,7 +333,11 @@ typedef struct {
 typedef struct {
     const uint8_t *token_embd;             /* [vocab, d]                  */
     const float *output_norm;              /* [d]                         */
-    const uint8_t *output;                 /* lm_head [vocab, d]          */
+    const uint8_t *output;                 /* lm_head [vocab, d]; NULL =
+                                              tied to token_embd, as
+                                              load_special does without
+                                              output.weight (loader.rs:
+                                              193-199)                    */
     const lcmoe_layer_weights *layers;     /* n_layer of them             */
 } lcmoe_model_weights;
 
@@ -310,7 +345,10 @@ typedef struct lcmoe_model lcmoe_model;
 
 /* Engine::load's resident counterpart: validates, uploads every tensor once
  * (each layer's MoE through lcmoe_create) and allocates the KV caches of
- * max_batch sequences.  The caller keeps ownership of the host bytes. */
+ * max_batch sequences.  The caller keeps ownership of the host bytes.  Every
+ * tensor is sanitised as load_layer / load_special do (loader.rs:161, :188,
+ * :241-249; see lcmoe_sanitize_blocks); a Q4_K tensor with an outlier that
+ * Q4_K cannot hold as zero is stored as its sanitised f32 dequantisation. */
 lcmoe_status lcmoe_model_create(const lcmoe_model_desc *desc, const lcmoe_model_weights *w,
                                 lcmoe_model **out);
 void lcmoe_model_destroy(lcmoe_model *m);
@@ -324,6 +362,10 @@ lcmoe_status lcmoe_model_reset(lcmoe_model *m);
  * (engine.rs:138). */
 lcmoe_status lcmoe_model_forward(lcmoe_model *m, const int32_t *tokens, int32_t B, int32_t T,
                                  float *logits);
+/* A forward or generate that fails after enqueueing device work leaves the
+ * model refusing lcmoe_model_forward with LCMOE_ERR_STATE until
+ * lcmoe_model_reset (the cache lengths on the device may have advanced);
+ * lcmoe_model_generate resets by itself. */
 /* Engine::generate (engine.rs:51-76) with greedy sampling for B sequences
  * of P prompt tokens each (prompt [B, P]): reset, prefill each sequence,
  * then n_new - 1 batched decode steps (one captured HIP graph, replayed).
@@ -437,6 +479,17 @@ lcmoe_status lcmoe_debug_read_bandwidth(int64_t slice_bytes, int32_t reps, doubl
  * forward did not use it.  Waits for the forward.  No counterpart in the
  * reference: it observes which of two bit-identical routes ran. */
 lcmoe_status lcmoe_debug_route_fallbacks(lcmoe_handle *h, int32_t *count);
+
+/* Testing of the error path only (no counterpart in the reference): the
+ * model's n-th internal forward from now on (0-based; one per prefilled
+ * sequence, one per decode step or graph capture) fails before enqueueing
+ * anything; n < 0 cancels. */
+lcmoe_status lcmoe_model_debug_fail_forward(lcmoe_model *m, int32_t n);
+
+/* Observation only (no counterpart in the reference): layer `layer`'s MoE
+ * handle, owned by the model, for lcmoe_get_dispatch (the routing of that
+ * layer's most recent forward).  Not to be destroyed or run by the caller. */
+lcmoe_status lcmoe_model_debug_layer_moe(lcmoe_model *m, int32_t layer, lcmoe_handle **out);
 
 #ifdef __cplusplus
 }

@@ -8,12 +8,12 @@ from ._lib import (ROUTE_SIGMOID_GROUP, ROUTE_SOFTMAX, ROUTE_SOFTMAX_RENORM, TYP
 from .configs import CONFIGS, MODEL_CONFIGS, LayerConfig, ModelConfig, synth_layer, synth_model, synth_x
 from .gguf import GgufFile
 from .model import Model, ModelDesc
-from .moe import (MoeFfn, debug_dequant, debug_rmsnorm, debug_sigmoid, matmul, read_bandwidth,
-                  shard_matmul)
+from .moe import (MoeFfn, debug_dequant, debug_rmsnorm, debug_sigmoid, dequantize, matmul,
+                  read_bandwidth, sanitize_blocks, shard_matmul)
 
 __all__ = [
     "CONFIGS", "MODEL_CONFIGS", "LayerConfig", "ModelConfig", "synth_layer", "synth_model",
     "synth_x", "MoeFfn", "Model", "ModelDesc", "GgufFile", "Desc", "Weights",
-    "LcmoeError", "lib", "debug_dequant", "debug_rmsnorm", "debug_sigmoid", "shard_matmul", "matmul", "read_bandwidth", "TYPE_F32", "TYPE_Q4_0", "TYPE_Q8_0",
+    "LcmoeError", "lib", "dequantize", "sanitize_blocks", "debug_dequant", "debug_rmsnorm", "debug_sigmoid", "shard_matmul", "matmul", "read_bandwidth", "TYPE_F32", "TYPE_Q4_0", "TYPE_Q8_0",
     "TYPE_Q4_K", "TYPE_Q6_K", "ROUTE_SOFTMAX_RENORM", "ROUTE_SOFTMAX", "ROUTE_SIGMOID_GROUP",
 ]

@@ -37,6 +37,8 @@ EXPORTS = (
     "lcmoe_model_reset", "lcmoe_model_forward", "lcmoe_model_generate",
     "lcmoe_model_last_timing", "lcmoe_model_set_decode_graph", "lcmoe_matmul_f32",
     "lcmoe_matmul_f32_dev", "lcmoe_debug_route_fallbacks", "lcmoe_debug_read_bandwidth",
+    "lcmoe_dequantize", "lcmoe_sanitize_blocks", "lcmoe_model_debug_fail_forward",
+    "lcmoe_model_debug_layer_moe",
 )
 
 
@@ -99,6 +101,8 @@ def lib() -> C.CDLL:
         "lcmoe_last_error": (C.c_char_p, []),
         "lcmoe_tensor_size": (C.c_size_t, [i32, i64]),
         "lcmoe_scan_blocks": (i64, [i32, vp, i64]),
+        "lcmoe_dequantize": (i64, [i32, vp, i64, vp, i32]),
+        "lcmoe_sanitize_blocks": (i64, [i32, vp, i64, P(i64)]),
         "lcmoe_quantize": (i32, [i32, vp, vp, i64]),
         "lcmoe_synth_normal": (None, [u64, u64, f32, vp, i64]),
         "lcmoe_debug_dequant": (i32, [i32, vp, i64, vp]),

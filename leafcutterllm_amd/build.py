@@ -10,6 +10,7 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
@@ -40,17 +41,21 @@ def _run(cmd, verbose):
 
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
-    objs = []
+    jobs = []
     for src in sorted(os.listdir(CSRC)):
         if src.endswith(".hip"):
             o = os.path.join(BUILD, src[:-4] + ".o")
-            _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", o], verbose)
-            objs.append(o)
+            jobs.append(([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", o], o))
     for src in sorted(os.listdir(CSRC)):
         if src.endswith(".cpp"):
             o = os.path.join(BUILD, src[:-4] + ".o")
-            _run(["g++", *HOST_FLAGS, "-c", os.path.join(CSRC, src), "-o", o], verbose)
-            objs.append(o)
+            jobs.append((["g++", *HOST_FLAGS, "-c", os.path.join(CSRC, src), "-o", o], o))
+    # one compiler per source, at most MAX_JOBS (or the CPU count) at once
+    workers = max(1, min(len(jobs), int(os.environ.get("MAX_JOBS", 0)) or os.cpu_count() or 1, 16))
+    with ThreadPoolExecutor(workers) as pool:
+        for f in [pool.submit(_run, cmd, verbose) for cmd, _ in jobs]:
+            f.result()
+    objs = [o for _, o in jobs]
     tmp = LIB + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-pthread", *objs, "-o", tmp],
          verbose)

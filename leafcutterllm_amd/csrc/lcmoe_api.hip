@@ -139,28 +139,35 @@ lcmoe_status alloc_n(lcmoe_handle *h, T **dst, size_t n) {
     return st;
 }
 
-// Uploads n stacked expert matrices [rows, cols] of type qt, repacking each
-// to RPL64 (Q4_K or Q6_K, by qt) when `rpl`, or to the split Q4_K layout
-// when `split` (one expert at a time through a host staging buffer).
-// *sz_out: device bytes per expert.
-// n2 > 0: n2 more experts from src2 follow as experts n .. n+n2-1.
-lcmoe_status upload_stack(lcmoe_handle *h, uint8_t **dst, const uint8_t *src, int n, int qt,
-                          int64_t rows, int64_t cols, bool rpl, int64_t *sz_out,
-                          bool split = false, const uint8_t *src2 = nullptr, int n2 = 0) {
-    const int64_t sz = (int64_t)lcmoe_tensor_size(qt, rows * cols);
+// Uploads the stacked expert matrices of `src` (sanitised, as stored: see
+// SanitizedStack), repacking each to RPL64 (Q4_K, Q6_K or Q8_0, by the stored
+// type) when `rpl`, or to the split Q4_K layout when `split` (one expert at a
+// time through a host staging buffer).  *sz_out: device bytes per expert.
+lcmoe_status upload_stack(lcmoe_handle *h, uint8_t **dst, const SanitizedStack &src, bool rpl,
+                          int64_t *sz_out, bool split = false) {
+    const int qt = src.qt, n = src.na + src.nb;
+    const int64_t rows = src.rows, cols = src.cols;
+    const int64_t sz = src.stored_bytes();
     const int64_t dsz = split ? rows / 64 * ((cols + 255) / 256) * (9 * 1024 + 256) : sz;
     *sz_out = dsz;
-    lcmoe_status st = alloc_n(h, dst, (size_t)dsz * (n + n2));
+    lcmoe_status st = alloc_n(h, dst, (size_t)dsz * n);
     if (st) return st;
-    if (!rpl && !split) {
-        HIP_TRY(hipMemcpy(*dst, src, (size_t)sz * n, hipMemcpyHostToDevice));
-        if (n2)
-            HIP_TRY(hipMemcpy(*dst + (size_t)sz * n, src2, (size_t)sz * n2, hipMemcpyHostToDevice));
+    const bool as_given =
+        qt == src.qt_in && std::none_of(src.fix.begin(), src.fix.end(), [](uint8_t f) { return f; });
+    if (!rpl && !split && as_given) {
+        HIP_TRY(hipMemcpy(*dst, src.a, (size_t)sz * src.na, hipMemcpyHostToDevice));
+        if (src.nb)
+            HIP_TRY(hipMemcpy(*dst + (size_t)sz * src.na, src.b, (size_t)sz * src.nb,
+                              hipMemcpyHostToDevice));
         return LCMOE_OK;
     }
-    std::vector<uint8_t> buf((size_t)dsz);
-    for (int e = 0; e < n + n2; e++) {
-        const uint8_t *s = e < n ? src + (size_t)e * sz : src2 + (size_t)(e - n) * sz;
+    std::vector<uint8_t> buf(rpl || split ? (size_t)dsz : 0), sbuf;
+    for (int e = 0; e < n; e++) {
+        const uint8_t *s = src.get(e, sbuf);
+        if (!rpl && !split) {
+            HIP_TRY(hipMemcpy(*dst + (size_t)e * sz, s, (size_t)sz, hipMemcpyHostToDevice));
+            continue;
+        }
         if (split) {  // straddling blocks: one thread (the layout reads across rows)
             repack_rpl64_q4k_split(s, buf.data(), rows, cols);
             HIP_TRY(hipMemcpy(*dst + (size_t)e * dsz, buf.data(), (size_t)dsz,
@@ -252,14 +259,14 @@ int choose_ksplit_mfma(const ExpertSet &s, int d, int active) {
     return ks;
 }
 
-// n experts from gate/up/down, plus n2 fused shared experts from
-// gate2/up2/down2 stored after them (experts n .. n+n2-1)
-lcmoe_status setup_set(lcmoe_handle *h, ExpertSet &s, int n, int F, int qgu, int qdn,
-                       const uint8_t *gate, const uint8_t *up, const uint8_t *down, int64_t positions,
-                       int n2 = 0, const uint8_t *gate2 = nullptr, const uint8_t *up2 = nullptr,
-                       const uint8_t *down2 = nullptr) {
+// An expert family from its sanitised gate, up and down stacks (experts
+// [0, na) routed or shared; fused shared experts as [na, na + nb), stored
+// after them).  The layouts follow the stored types.
+lcmoe_status setup_set(lcmoe_handle *h, ExpertSet &s, int F, const SanitizedStack &g,
+                       const SanitizedStack &u, const SanitizedStack &dn, int64_t positions) {
     const int64_t d = h->desc.d_model;
-    s.n = n;
+    const int qgu = g.qt, qdn = dn.qt;
+    s.n = g.na;
     s.F = F;
     s.qt_gu = qgu;
     s.qt_dn = qdn;
@@ -273,11 +280,9 @@ lcmoe_status setup_set(lcmoe_handle *h, ExpertSet &s, int n, int F, int qgu, int
     int64_t szu = 0;
     lcmoe_status st;
     const bool rgu = s.rpl_gu || s.q8;
-    if ((st = upload_stack(h, &s.gate, gate, n, qgu, F, d, rgu, &s.sz_gu, false, gate2, n2)))
-        return st;
-    if ((st = upload_stack(h, &s.up, up, n, qgu, F, d, rgu, &szu, false, up2, n2))) return st;
-    if ((st = upload_stack(h, &s.down, down, n, qdn, d, F, s.rpl_dn || s.q6_dn || s.q8, &s.sz_dn,
-                           s.split_dn, down2, n2)))
+    if ((st = upload_stack(h, &s.gate, g, rgu, &s.sz_gu))) return st;
+    if ((st = upload_stack(h, &s.up, u, rgu, &szu))) return st;
+    if ((st = upload_stack(h, &s.down, dn, s.rpl_dn || s.q6_dn || s.q8, &s.sz_dn, s.split_dn)))
         return st;
     if (s.rpl_dn || s.q6_dn || s.q8 || s.split_dn) {  // limbs for the row-per-lane down
         if ((st = alloc_n(h, &s.hh, positions * F))) return st;
@@ -332,11 +337,13 @@ extern "C" lcmoe_status lcmoe_create(const lcmoe_desc *desc, const lcmoe_weights
 
     const int64_t d = D.d_model, E = D.n_expert, K = D.n_expert_used, S = D.n_shared,
                   Tm = D.max_tokens, A = Tm * K;
-    // router, transposed to [E, d] so each expert's row is contiguous
+    // router, transposed to [E, d] so each expert's row is contiguous, and
+    // sanitised as load_layer does (loader.rs:161, :241-249)
     {
         std::vector<float> wt((size_t)E * d);
         for (int64_t k = 0; k < d; k++)
             for (int64_t e = 0; e < E; e++) wt[e * d + k] = w->router[k * E + e];
+        lcmoe_sanitize_blocks(LCMOE_TYPE_F32, reinterpret_cast<uint8_t *>(wt.data()), E * d, nullptr);
         if ((st = alloc_n(h, &h->wrt, wt.size()))) return bail(st);
         if (hipMemcpy(h->wrt, wt.data(), wt.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
             return bail(fail(LCMOE_ERR_HIP, "router upload failed"));
@@ -353,27 +360,58 @@ extern "C" lcmoe_status lcmoe_create(const lcmoe_desc *desc, const lcmoe_weights
                 return bail(fail(LCMOE_ERR_HIP, "router upload failed"));
         }
     }
-    if (D.has_bias) {
+    if (D.has_bias) {  // the selection bias is a layer tensor too: sanitised
+        std::vector<float> b(w->bias, w->bias + E);
+        lcmoe_sanitize_blocks(LCMOE_TYPE_F32, reinterpret_cast<uint8_t *>(b.data()), E, nullptr);
         if ((st = alloc_n(h, &h->bias, E))) return bail(st);
-        if (hipMemcpy(h->bias, w->bias, E * 4, hipMemcpyHostToDevice) != hipSuccess)
+        if (hipMemcpy(h->bias, b.data(), E * 4, hipMemcpyHostToDevice) != hipSuccess)
             return bail(fail(LCMOE_ERR_HIP, "bias upload failed"));
     }
-    // shared experts of the routed experts' shape and types run as extra
-    // slots of the routed launches (their positions follow the A routed ones)
-    h->fused = S > 0 && D.d_ff_shared == D.d_ff && D.type_gate_sh == D.type_gate &&
-               D.type_down_sh == D.type_down;
+    // Expert matrices, sanitised (sanitize_weights, loader.rs:241-249):
+    // outliers zero-coded in place where the type can hold a zero; a family
+    // whose Q4_K gate or up (or down) has an outlier that cannot be is
+    // stored as f32 for that matrix kind (gate and up share one type).
+    auto stack = [](const uint8_t *a, int na, int qt, int64_t rows, int64_t cols) {
+        SanitizedStack t;
+        t.a = a;
+        t.na = na;
+        t.qt_in = t.qt = qt;
+        t.rows = rows;
+        t.cols = cols;
+        return t;
+    };
+    const int64_t F = D.d_ff, FS = D.d_ff_shared;
+    SanitizedStack rg = stack(w->gate, (int)E, D.type_gate, F, d),
+                   ru = stack(w->up, (int)E, D.type_up, F, d),
+                   rd = stack(w->down, (int)E, D.type_down, d, F), sg, su, sd;
+    const bool rg_f32 = rg.analyse(), ru_f32 = ru.analyse();  // both scanned: each fills its fix list
+    const bool rgu_f32 = rg_f32 || ru_f32;
+    if (rgu_f32) rg.qt = ru.qt = LCMOE_TYPE_F32;
+    if (rd.analyse()) rd.qt = LCMOE_TYPE_F32;
+    if (S > 0) {
+        sg = stack(w->gate_sh, (int)S, D.type_gate_sh, FS, d);
+        su = stack(w->up_sh, (int)S, D.type_up_sh, FS, d);
+        sd = stack(w->down_sh, (int)S, D.type_down_sh, d, FS);
+        const bool sg_f32 = sg.analyse(), su_f32 = su.analyse();
+        const bool sgu_f32 = sg_f32 || su_f32;
+        if (sgu_f32) sg.qt = su.qt = LCMOE_TYPE_F32;
+        if (sd.analyse()) sd.qt = LCMOE_TYPE_F32;
+    }
+    // shared experts of the routed experts' shape and stored types run as
+    // extra slots of the routed launches (their positions follow the A
+    // routed ones)
+    h->fused = S > 0 && FS == F && sg.qt == rg.qt && sd.qt == rd.qt;
     if (h->fused) {
-        if ((st = setup_set(h, h->routed, (int)E, D.d_ff, D.type_gate, D.type_down, w->gate,
-                            w->up, w->down, A + S * Tm, (int)S, w->gate_sh, w->up_sh,
-                            w->down_sh)))
-            return bail(st);
+        for (SanitizedStack *p : {&rg, &ru, &rd}) {
+            const SanitizedStack &q = p == &rg ? sg : p == &ru ? su : sd;
+            p->b = q.a;
+            p->nb = q.na;
+            p->fix.insert(p->fix.end(), q.fix.begin(), q.fix.end());
+        }
+        if ((st = setup_set(h, h->routed, (int)F, rg, ru, rd, A + S * Tm))) return bail(st);
     } else {
-        if ((st = setup_set(h, h->routed, (int)E, D.d_ff, D.type_gate, D.type_down, w->gate,
-                            w->up, w->down, A)))
-            return bail(st);
-        if (S > 0 && (st = setup_set(h, h->shared, (int)S, D.d_ff_shared, D.type_gate_sh,
-                                     D.type_down_sh, w->gate_sh, w->up_sh, w->down_sh, S * Tm)))
-            return bail(st);
+        if ((st = setup_set(h, h->routed, (int)F, rg, ru, rd, A))) return bail(st);
+        if (S > 0 && (st = setup_set(h, h->shared, (int)FS, sg, su, sd, S * Tm))) return bail(st);
     }
     const bool limbs = h->routed.rpl_gu || h->routed.q8 ||
                        (S > 0 && !h->fused && (h->shared.rpl_gu || h->shared.q8));
@@ -726,7 +764,10 @@ extern "C" lcmoe_status lcmoe_set_norm(lcmoe_handle *h, const float *weight, flo
     // the stream may still be reading the previous weight
     HIP_TRY(hipStreamSynchronize(h->stream));
     if (h->last_stream) HIP_TRY(hipStreamSynchronize(h->last_stream));
-    HIP_TRY(hipMemcpy(h->norm_w, weight, sizeof(float) * d, hipMemcpyHostToDevice));
+    // the norm weight is sanitised as load_layer sanitises it (loader.rs:161)
+    std::vector<float> wn(weight, weight + d);
+    lcmoe_sanitize_blocks(LCMOE_TYPE_F32, reinterpret_cast<uint8_t *>(wn.data()), d, nullptr);
+    HIP_TRY(hipMemcpy(h->norm_w, wn.data(), sizeof(float) * d, hipMemcpyHostToDevice));
     h->norm_eps = eps;
     return LCMOE_OK;
 }

@@ -6,6 +6,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <cstring>
+#include <vector>
 
 #include "../../include/lcmoe.h"
 
@@ -92,5 +93,31 @@ void repack_rpl64_q6k(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t co
 void repack_rpl64_q8(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t cols);
 // Split repack of Q4_K with cols an odd multiple of 128 (lcmoe_host.cpp).
 void repack_rpl64_q4k_split(const uint8_t *src, uint8_t *dst, int64_t rows, int64_t cols);
+
+// Weights the reference's sanitize_weights (rust/src/model/loader.rs:241-249)
+// zeroes in `count` elements of GGUF bytes of `type` (lcmoe_sanitize.cpp);
+// *unzeroable: how many of them a Q4_K block cannot encode as zero in place.
+int64_t count_outliers(int32_t type, const uint8_t *data, int64_t count, int64_t *unzeroable);
+
+// A stack of n expert matrices [rows, cols] as the library uploads them
+// after sanitising: the caller's bytes where no weight trips the rule, a
+// zero-coded copy where every outlier can be written as zero in place, and
+// the sanitised f32 dequantisation of every expert when some Q4_K outlier
+// cannot (the stored type is then LCMOE_TYPE_F32).  Experts [0, na) come
+// from a, [na, na + nb) from b.
+struct SanitizedStack {
+    const uint8_t *a = nullptr, *b = nullptr;
+    int na = 0, nb = 0;
+    int32_t qt_in = 0, qt = 0;  // the caller's type, the stored type
+    int64_t rows = 0, cols = 0;
+    std::vector<uint8_t> fix;   // per expert: needs a zero-coded copy
+    // Scans every expert and fills `fix`; true when some Q4_K outlier cannot
+    // be zero-coded, so the stack must be stored as f32 (qt = F32; the
+    // caller decides, since gate and up share one stored type).
+    bool analyse();
+    // expert e's bytes as stored (`buf` may hold them)
+    const uint8_t *get(int e, std::vector<uint8_t> &buf) const;
+    int64_t stored_bytes() const;  // per expert
+};
 
 }  // namespace lcmoe

@@ -61,6 +61,8 @@ _SIGS = {
     "lcmoe_model_last_timing": (C.c_int32, [C.c_void_p, C.POINTER(C.c_double),
                                             C.POINTER(C.c_double)]),
     "lcmoe_model_set_decode_graph": (C.c_int32, [C.c_void_p, C.c_int32]),
+    "lcmoe_model_debug_fail_forward": (C.c_int32, [C.c_void_p, C.c_int32]),
+    "lcmoe_model_debug_layer_moe": (C.c_int32, [C.c_void_p, C.c_int32, C.POINTER(C.c_void_p)]),
 }
 
 
@@ -80,7 +82,7 @@ class Model:
     """A resident decoder model on the current HIP device.
 
     `weights` holds numpy arrays: token_embd / output (GGUF bytes [vocab,
-    d]), output_norm (f32 [d]) and `layers`, a list of dicts with attn_norm,
+    d]; output absent or None ties the LM head to token_embd), output_norm (f32 [d]) and `layers`, a list of dicts with attn_norm,
     ffn_norm (f32 [d]), attn_q / attn_k / attn_v / attn_o (GGUF bytes) and
     `moe` (the arrays lcmoe_create takes: router, bias, gate, up, down and
     the *_sh tensors)."""
@@ -109,7 +111,7 @@ class Model:
                 setattr(lay.moe, k, p(m.get(k), np.uint8))
         w = ModelWeights()
         w.token_embd = p(weights["token_embd"], np.uint8)
-        w.output = p(weights["output"], np.uint8)
+        w.output = p(weights.get("output"), np.uint8)  # None: tied to token_embd
         w.output_norm = p(weights["output_norm"], np.float32)
         w.layers = C.cast(layers, C.c_void_p)
         h = C.c_void_p()
@@ -143,6 +145,27 @@ class Model:
     def set_decode_graph(self, enable: bool) -> None:
         check(_bound().lcmoe_model_set_decode_graph(self._h, int(enable)),
               "lcmoe_model_set_decode_graph")
+
+    def debug_fail_forward(self, n: int) -> None:
+        """Testing of the error path: the n-th internal forward from now on
+        fails before enqueueing anything (lcmoe_model_debug_fail_forward)."""
+        check(_bound().lcmoe_model_debug_fail_forward(self._h, int(n)),
+              "lcmoe_model_debug_fail_forward")
+
+    def layer_routing(self, layer: int) -> dict:
+        """Routing of layer `layer`'s most recent MoE forward (observation:
+        lcmoe_model_debug_layer_moe + lcmoe_get_dispatch): topk_idx, topk_w
+        [T, K]."""
+        h = C.c_void_p()
+        check(_bound().lcmoe_model_debug_layer_moe(self._h, int(layer), C.byref(h)),
+              "lcmoe_model_debug_layer_moe")
+        K, cap = self.desc.moe.n_expert_used, max(self.desc.max_batch, self.desc.max_prompt)
+        T = C.c_int32()
+        idx = np.empty((cap, K), np.int32)
+        w = np.empty((cap, K), np.float32)
+        check(lib().lcmoe_get_dispatch(h, C.byref(T), idx.ctypes.data, w.ctypes.data, None, None,
+                                       None, None), "lcmoe_get_dispatch")
+        return {"topk_idx": idx[:T.value].copy(), "topk_w": w[:T.value].copy()}
 
     def last_timing(self):
         a, b = C.c_double(), C.c_double()

@@ -164,6 +164,28 @@ class MoeFfn:
             pass
 
 
+def dequantize(qtype: int, data: np.ndarray, count: int, sanitize: bool = True) -> np.ndarray:
+    """GGUFModel::dequantize (+ sanitize_weights) on the host:
+    lcmoe_dequantize."""
+    data = np.ascontiguousarray(data, np.uint8)
+    out = np.empty(count, np.float32)
+    n = lib().lcmoe_dequantize(qtype, data.ctypes.data, count, out.ctypes.data, int(sanitize))
+    if n < 0:
+        raise ValueError(f"lcmoe_dequantize: bad type {qtype} or count {count}")
+    return out
+
+
+def sanitize_blocks(qtype: int, data: np.ndarray, count: int):
+    """sanitize_weights on GGUF bytes, on a copy (lcmoe_sanitize_blocks):
+    (bytes, elements zeroed, outliers Q4_K could not zero in place)."""
+    out = np.array(data, np.uint8, copy=True)
+    unz = C.c_int64()
+    n = lib().lcmoe_sanitize_blocks(qtype, out.ctypes.data, count, C.byref(unz))
+    if n < 0:
+        raise ValueError(f"lcmoe_sanitize_blocks: bad type {qtype} or count {count}")
+    return out, int(n), int(unz.value)
+
+
 def debug_dequant(qtype: int, data: np.ndarray, count: int) -> np.ndarray:
     data = np.ascontiguousarray(data, np.uint8)
     out = np.empty(count, np.float32)

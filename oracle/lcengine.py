@@ -50,14 +50,13 @@ def ingest(qtype: int, data: np.ndarray, rows: int, cols: int, transpose: bool =
     w = O.dequant(qtype, data, rows * cols).reshape(rows, cols)
     if transpose:
         w = np.ascontiguousarray(w.T)
-    w = w.copy()
-    w[~np.isfinite(w) | (np.abs(w) > 100.0)] = 0.0   # sanitize_weights, loader.rs:241-249
-    return w
+    return O.sanitize(w)   # sanitize_weights, loader.rs:241-249
 
 
 class RefEngine:
     """Engine (engine.rs:10-132) over `weights`:
-      token_embd, output: GGUF bytes [vocab, d]; output_norm: f32 [d];
+      token_embd, output: GGUF bytes [vocab, d] (output None: tied to the
+      embedding); output_norm: f32 [d];
       layers[i]: attn_norm, ffn_norm f32 [d]; attn_q [H*hd, d], attn_k,
       attn_v [KVH*hd, d], attn_o [d, H*hd] GGUF bytes; moe: the MoE layer
       arrays (router, bias, gate, up, down, *_sh) as lco_moe_forward takes."""
@@ -69,7 +68,14 @@ class RefEngine:
         d, H, KVH, hd, V = spec.d_model, spec.n_head, spec.n_kv_head, spec.head_dim, spec.vocab
         qt = spec.attn_type
         self.embed = ingest(qt, weights["token_embd"], V, d, transpose=False)
-        self.lm_head = ingest(qt, weights["output"], V, d)          # [d, V]
+        # load_special (loader.rs:193-199): without output.weight the LM head
+        # is the embedding transposed
+        out = weights.get("output")
+        self.lm_head = (np.ascontiguousarray(self.embed.T) if out is None
+                        else ingest(qt, out, V, d))                   # [d, V]
+        # every f32 tensor load_layer / load_special return is sanitised
+        # too (loader.rs:161, :188): the norms here
+        self.out_norm = O.sanitize(weights["output_norm"])
         self.layers = []
         for lw in weights["layers"]:
             self.layers.append({
@@ -77,7 +83,13 @@ class RefEngine:
                 "wk": ingest(qt, lw["attn_k"], KVH * hd, d),
                 "wv": ingest(qt, lw["attn_v"], KVH * hd, d),
                 "wo": ingest(qt, lw["attn_o"], d, H * hd),
+                "attn_norm": O.sanitize(lw["attn_norm"]),
+                "ffn_norm": O.sanitize(lw["ffn_norm"]),
             })
+        # when set, forward() appends each layer's routing (topk_idx, topk_w
+        # of its tokens) to self.routing, in layer order
+        self.record_routing = False
+        self.routing = []
         self.clear()
 
     def clear(self):
@@ -99,7 +111,7 @@ class RefEngine:
             if 0 <= t < s.vocab:
                 hidden[i] = self.embed[t]
         for li, (L, lw) in enumerate(zip(self.layers, self.w["layers"])):
-            normed = O.rms_norm(hidden, lw["attn_norm"], s.eps)
+            normed = O.rms_norm(hidden, L["attn_norm"], s.eps)
             q = self._mm(normed, L["wq"])
             k = self._mm(normed, L["wk"])
             v = self._mm(normed, L["wv"])
@@ -112,10 +124,12 @@ class RefEngine:
             attn = O.attention_core(q, O.f16_bits_to_f32(self.kc[li]),
                                     O.f16_bits_to_f32(self.vc[li]), H, KVH, hd)
             hidden = hidden + self._mm(attn, L["wo"])
-            normed = O.rms_norm(hidden, lw["ffn_norm"], s.eps)
-            ffn = O.moe_forward(s.moe_desc, lw["moe"], normed, threads=self.threads)["y"]
-            hidden = hidden + ffn
-        hidden = O.rms_norm(hidden, self.w["output_norm"], s.eps)
+            normed = O.rms_norm(hidden, L["ffn_norm"], s.eps)
+            moe = O.moe_forward(s.moe_desc, lw["moe"], normed, threads=self.threads)
+            if self.record_routing:
+                self.routing.append({"topk_idx": moe["topk_idx"], "topk_w": moe["topk_w"]})
+            hidden = hidden + moe["y"]
+        hidden = O.rms_norm(hidden, self.out_norm, s.eps)
         return self._mm(hidden[-1:], self.lm_head)[0]
 
     def generate(self, prompt, n_new: int, eos: int = -1):

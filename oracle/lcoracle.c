@@ -768,6 +768,16 @@ static float *ingest(int type, const uint8_t *bytes, int rows, int cols) {
     return (float *)realloc(tmp, sizeof(float) * n);
 }
 
+/* The router and bias as load_layer ingests them (loader.rs:161: every
+ * layer tensor is sanitised, :241-249); NULL in, NULL out. */
+static float *ingest_f32(const float *v, size_t n) {
+    if (!v) return NULL;
+    float *o = (float *)malloc(sizeof(float) * (n ? n : 1));
+    memcpy(o, v, sizeof(float) * n);
+    lco_sanitize(o, n);
+    return o;
+}
+
 static int desc_ok(const lco_desc *d) {
     if (d->d_model <= 0 || d->d_ff <= 0 || d->n_expert <= 0 || d->n_expert_used <= 0) return 0;
     if (d->n_expert_used > d->n_expert || d->n_expert > 256 || d->n_expert_used > 16) return 0;
@@ -810,9 +820,13 @@ int lco_moe_forward(const lco_desc *desc, const lco_weights *w, const float *x, 
     int32_t *inv = (int32_t *)malloc(sizeof(int32_t) * A);
     float *Y = (float *)malloc(sizeof(float) * A * D);
     float *Ysh = (float *)malloc(sizeof(float) * ((size_t)S * T * D + 1));
-    lco_router_logits(x, w->router, logits, T, D, E);
-    lco_route(desc, logits, w->bias, T, idx, tw);
+    float *router = ingest_f32(w->router, (size_t)D * E);
+    float *bias = desc->has_bias ? ingest_f32(w->bias, (size_t)E) : NULL;
+    lco_router_logits(x, router, logits, T, D, E);
+    lco_route(desc, logits, bias, T, idx, tw);
     lco_dispatch(idx, T, K, E, counts, offsets, perm, inv);
+    free(router);
+    free(bias);
 
     size_t szg = lco_tensor_size(desc->type_gate, (size_t)F * D);
     size_t szu = lco_tensor_size(desc->type_up, (size_t)F * D);
@@ -871,9 +885,9 @@ void *lco_resident_create(const lco_desc *desc, const lco_weights *w, int thread
     if (!desc_ok(desc)) return NULL;
     lco_resident *r = (lco_resident *)calloc(1, sizeof *r);
     r->desc = *desc;
-    r->router = w->router;
-    r->bias = w->bias;
     int E = desc->n_expert, S = desc->n_shared, D = desc->d_model, F = desc->d_ff, FS = desc->d_ff_shared;
+    r->router = ingest_f32(w->router, (size_t)D * E);
+    r->bias = desc->has_bias ? ingest_f32(w->bias, (size_t)E) : NULL;
     r->wg = (float **)calloc((size_t)(E + S) * 3, sizeof(float *));
     r->wu = r->wg + (E + S);
     r->wd = r->wu + (E + S);
@@ -936,6 +950,8 @@ void lco_resident_destroy(void *h) {
     int n = r->desc.n_expert + r->desc.n_shared;
     for (int e = 0; e < n; e++) { free(r->wg[e]); free(r->wu[e]); free(r->wd[e]); }
     free(r->wg);
+    free((void *)r->router);
+    free((void *)r->bias);
     free(r);
 }
 

@@ -28,7 +28,16 @@
  *                          dequantise-then-matmul (1e-3), float64 bound, exact
  *                          small-integer KATs that fix operand order and nibbles
  *   rms_norm             : reference test tensor.rs:204-209, float64 closed form,
- *                          exact constant rows, scale-then-weight rounding order
+ *                          exact constant rows, scale-then-weight rounding order;
+ *                          the four-lane sum-of-squares order (simd.rs:390-401)
+ *                          bit for bit against an independent numpy float32
+ *                          restatement, on rows where a sequential sum differs
+ *   sanitize             : tests/test_oracle_core.py -- the closed form of
+ *                          loader.rs:241-249 at its cut-off (+-100 kept, the
+ *                          next float above 100 zeroed, NaN and +-inf zeroed)
+ *                          and through the ingest of every type (hand-built
+ *                          blocks whose outlier positions are known); the
+ *                          layer forward sanitises router and bias as well
  *   route (all kinds)    : tests/test_oracle_route.py -- brute force over the
  *                          full sort of (-z, e) with ties, +-0, +-inf and NaN
  *                          for the softmax, renormalised-softmax and
@@ -149,7 +158,8 @@ int lco_dispatch(const int32_t *topk_idx, int T, int K, int E, int32_t *counts,
 /* ---- whole layer -------------------------------------------------------- */
 /* y[T, d] = MoE FFN of x[T, d].  Optional outputs may be NULL.  Weights are
  * dequantised one expert at a time (dequant -> transpose -> sanitize, as
- * loader.rs:145-168 does per tensor).  threads<=0 -> reference row split. */
+ * loader.rs:145-168 does per tensor); the router and the bias are sanitised
+ * too (loader.rs:161).  threads<=0 -> reference row split. */
 int lco_moe_forward(const lco_desc *desc, const lco_weights *w, const float *x, int T,
                     float *y, int32_t *topk_idx, float *topk_w, int32_t *counts,
                     int32_t *offsets, int32_t *perm, int32_t *inv, int threads);

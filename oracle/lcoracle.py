@@ -118,6 +118,20 @@ def dequant(qtype: int, data: np.ndarray, count: int) -> np.ndarray:
     return out
 
 
+def sanitize(v: np.ndarray) -> np.ndarray:
+    """sanitize_weights (loader.rs:241-249) on a copy: lco_sanitize."""
+    out = np.array(v, np.float32, copy=True)
+    flat = out.reshape(-1)
+    lib().lco_sanitize(_p(flat), flat.size)
+    return out
+
+
+def ingest(qtype: int, data: np.ndarray, count: int) -> np.ndarray:
+    """A tensor's values as the reference's loader leaves them: dequantised
+    (loader.rs:205-235), then sanitised (loader.rs:241-249)."""
+    return sanitize(dequant(qtype, data, count))
+
+
 def quantize(qtype: int, x: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32).ravel()
     out = np.zeros(tensor_size(qtype, x.size), np.uint8)

@@ -51,8 +51,11 @@ def run_and_check(cfg: L.LayerConfig, layer: dict, x: np.ndarray, moe: L.MoeFfn 
         disp = moe.dispatch()
         assert np.array_equal(disp["topk_idx"], idx)
         od = oracle_desc(cfg.desc(max(T, 1)))
-        logits = O.router_logits(x, layer["router"])
-        r_idx, r_w = O.route(od, logits, layer.get("bias"))
+        # the router and bias as the reference ingests them (sanitised,
+        # loader.rs:161), which is what lco_moe_forward routes with
+        bias = layer.get("bias")
+        logits = O.router_logits(x, O.sanitize(layer["router"]))
+        r_idx, r_w = O.route(od, logits, None if bias is None else O.sanitize(bias))
         counts, offsets, perm, inv = O.dispatch(r_idx, cfg.n_expert)
         check_routing(disp, {"topk_idx": r_idx, "topk_w": r_w, "counts": counts,
                              "offsets": offsets, "perm": perm, "inv": inv}, T, cfg.n_expert_used)

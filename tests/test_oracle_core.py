@@ -302,6 +302,56 @@ def test_rms_norm_reference_test_and_float64():
                           (np.float32(x[0, :2] * s) * w[:2]).astype(np.float32))
 
 
+def _rms_norm_four_lanes(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """CpuBackend::rms_norm (cpu.rs:49-60) over x86 simd_sum_sq
+    (kernels/simd.rs:390-409), written out in numpy float32: lane l sums
+    round(v*v) of elements l, l+4, ... as acc = round(v*v) + acc (product
+    then add, no FMA); the lanes add as ((a0 + a1) + a2) + a3; the tail past
+    the last group of four adds one square at a time; mean = sum / n,
+    scale = 1 / sqrt(mean + eps), out = (x * scale) * w."""
+    x = np.asarray(x, np.float32)
+    T, n = x.shape
+    m = n // 4 * 4
+    acc = np.zeros((T, 4), np.float32)
+    for i in range(0, m, 4):
+        v = x[:, i:i + 4]
+        acc = (v * v) + acc
+    s = ((acc[:, 0] + acc[:, 1]) + acc[:, 2]) + acc[:, 3]
+    for r in range(m, n):
+        s = s + x[:, r] * x[:, r]
+    mean = s / np.float32(n)
+    scale = np.float32(1.0) / np.sqrt(mean + np.float32(eps))
+    return (x * scale[:, None]) * np.asarray(w, np.float32)
+
+
+def _rms_norm_sequential(x, w, eps):
+    """The same with one sequential sum: the order a four-lane oracle must not use."""
+    x = np.asarray(x, np.float32)
+    s = np.zeros(x.shape[0], np.float32)
+    for r in range(x.shape[1]):
+        s = s + x[:, r] * x[:, r]
+    scale = np.float32(1.0) / np.sqrt(s / np.float32(x.shape[1]) + np.float32(eps))
+    return (x * scale[:, None]) * np.asarray(w, np.float32)
+
+
+def test_rms_norm_four_lane_order_bit_exact():
+    """lco_rms_norm reproduces the reference's four-lane sum-of-squares order
+    bit for bit, on rows with spread magnitudes where a sequential sum (or a
+    pairwise / float64 one) rounds differently."""
+    rng = np.random.default_rng(11)
+    for d in (4, 7, 64, 130, 1024, 4096):
+        T = 200
+        x = (rng.standard_normal((T, d)) * 10.0 ** rng.uniform(-3, 3, (T, d))).astype(np.float32)
+        w = rng.standard_normal(d).astype(np.float32)
+        ours = O.rms_norm(x, w, 1e-5)
+        lanes = _rms_norm_four_lanes(x, w, 1e-5)
+        assert np.array_equal(ours.view(np.uint32), lanes.view(np.uint32)), d
+        if d >= 64:  # the order matters on these rows: a sequential oracle fails
+            seq = _rms_norm_sequential(x, w, 1e-5)
+            differ = np.any(seq.view(np.uint32) != lanes.view(np.uint32), axis=1)
+            assert differ.sum() >= T // 10, (d, differ.sum())
+
+
 def test_softmax_kat_and_closed_form():
     y = O.softmax(np.array([1.0, 2.0, 3.0], np.float32))  # tensor.rs:211-217
     assert abs(float(np.sum(y)) - 1.0) < 1e-5
