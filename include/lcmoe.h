@@ -145,6 +145,23 @@ lcmoe_status lcmoe_forward(lcmoe_handle *h, const float *x, int32_t T, float *y,
 lcmoe_status lcmoe_forward_dev(lcmoe_handle *h, const float *x_dev, int32_t T, float *y_dev,
                                void *stream);
 
+/* Activation operands of the matrix-core expert products (batches where
+ * the experts see more tokens than there are experts: T*K > E; prefill).
+ * The weights are always exact (sc*q in f16, scales in f32) and the sums
+ * f32; the mode sets how x enters the gate/up products:
+ *   LCMOE_ACT_F16   (default) one f16 per element: layer output within about
+ *                   3.6e-4 relative L2 of the reference CPU path at every
+ *                   benchmark shape (the bar is 1e-3), half the matrix-core
+ *                   work and activation traffic of F16X2;
+ *   LCMOE_ACT_F16X2 two f16 (hi + lo = x to about 22 bits): about 3e-6, for
+ *                   deep stacks where per-layer error compounds (lcmoe_model
+ *                   selects it for every layer).
+ * The down products take H as two f16 in both modes; the row-per-lane
+ * (decode) kernels always use exact integer products on 15-bit activations.
+ * No counterpart in the reference (its CPU path is f32 throughout). */
+enum { LCMOE_ACT_F16 = 0, LCMOE_ACT_F16X2 = 1 };
+lcmoe_status lcmoe_set_act_precision(lcmoe_handle *h, int32_t mode);
+
 /* Post-attention RMSNorm weight [d_model] f32 and epsilon used by the
  * lcmoe_forward_norm_residual* calls below (the reference passes 1e-5,
  * engine.rs:111).  Copied to the device, sanitised as load_layer sanitises

@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(_HERE, "liblcmoe.so")
 TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 0, 8, 12, 14
 TYPE_Q4_0 = 2  # lcmoe_shard_matmul only: the shard engine's interleaved Q4_0
 ROUTE_SOFTMAX_RENORM, ROUTE_SOFTMAX, ROUTE_SIGMOID_GROUP = 0, 1, 2
+ACT_F16, ACT_F16X2 = 0, 1  # lcmoe_set_act_precision
 
 STATUS = {
     0: "LCMOE_OK", 1: "LCMOE_ERR_INVALID_ARG", 2: "LCMOE_ERR_UNSUPPORTED",
@@ -38,7 +39,7 @@ EXPORTS = (
     "lcmoe_model_last_timing", "lcmoe_model_set_decode_graph", "lcmoe_matmul_f32",
     "lcmoe_matmul_f32_dev", "lcmoe_debug_route_fallbacks", "lcmoe_debug_read_bandwidth",
     "lcmoe_dequantize", "lcmoe_sanitize_blocks", "lcmoe_model_debug_fail_forward",
-    "lcmoe_model_debug_layer_moe",
+    "lcmoe_model_debug_layer_moe", "lcmoe_set_act_precision",
 )
 
 
@@ -111,6 +112,7 @@ def lib() -> C.CDLL:
         "lcmoe_debug_read_bandwidth": (i32, [i64, i32, vp]),
         "lcmoe_debug_rmsnorm": (i32, [vp, vp, f32, i32, i32, vp]),
         "lcmoe_set_norm": (i32, [vp, vp, f32]),
+        "lcmoe_set_act_precision": (i32, [vp, i32]),
         "lcmoe_shard_matmul": (i32, [i32, vp, vp, vp, i32, i32, i32]),
         "lcmoe_shard_matmul_dev": (i32, [i32, vp, vp, vp, i32, i32, i32, vp]),
         "lcmoe_shard_matmul_split_dev": (i32, [i32, vp, vp, vp, i32, i32, i32, i32, vp, vp]),

@@ -248,10 +248,12 @@ __device__ __forceinline__ uint32_t ord_key(float f) {
 // Matrix-core activation format of one 32-column sub-block sbi of row t
 // (row width d, a multiple of 256): the f16 hi = f16(v) and lo = f16(v - hi)
 // halves at columns 32 (sbi % 8) .. +31 of the row's super-block piece sbi / 8
-// (hi[256] then lo[256]), and the sub-block's sum of (hi + lo), added in
+// (hi[256] then lo[256]), and the sub-block's sum of (hi + lo) -- of hi
+// alone when !lo, for products that take only the hi halves -- added in
 // column order, as a (hi, lo) pair.  v: the 32 values, 16-byte aligned.
 __device__ inline void act16_subblock(const float *v, int64_t t, int d, int sbi,
-                                      _Float16 *__restrict__ x16, _Float16 *__restrict__ xs) {
+                                      _Float16 *__restrict__ x16, _Float16 *__restrict__ xs,
+                                      bool lo_sum = true) {
     typedef _Float16 h8 __attribute__((ext_vector_type(8)));
     const float4 *v4 = reinterpret_cast<const float4 *>(v);
     _Float16 *piece = x16 + (t * (d >> 8) + (sbi >> 3)) * 512 + 32 * (sbi & 7);
@@ -268,7 +270,7 @@ __device__ inline void act16_subblock(const float *v, int64_t t, int d, int sbi,
             const _Float16 hi = (_Float16)f[i], lo = (_Float16)(f[i] - (float)hi);
             hv[i] = hi;
             lv[i] = lo;
-            sum = sum + ((float)hi + (float)lo);
+            sum = sum + (lo_sum ? (float)hi + (float)lo : (float)hi);
         }
         oh[g] = hv;
         ol[g] = lv;

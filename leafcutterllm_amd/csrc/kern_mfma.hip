@@ -181,6 +181,12 @@ __device__ __forceinline__ half8 min_operand(const Hdr &s, int h) {
 constexpr int kTokBytes = 1040;
 constexpr int kSumsOff = kTok * kTokBytes;
 constexpr int kStageBytes = kSumsOff + kTok * 32;
+// Stages of activations without their lo halves (LO = false: the gate/up
+// products take x as one f16 per element): token rows of 512 + 16 bytes.
+template <bool LO>
+constexpr int kTokB = LO ? kTokBytes : 528;
+template <bool LO>
+constexpr int kSumsOffT = kTok * kTokB<LO>;
 
 // Per-pass source addresses of the block's activation staging: wave w moves
 // the 1 KiB pieces of tokens w + 4i (i = 0..7); wave 0 also moves the 32
@@ -195,30 +201,40 @@ struct StageSrc {
 // registers: loaded at the start of a step, stored to the other LDS stage at
 // its end.  Ordinary loads (not LDS DMA), so that every wait in the pipeline
 // is an in-order vmcnt wait that leaves younger weight loads in flight.
-template <int NI>
+template <int NI, bool LO = true>
 struct StageRegs {
-    u32x4 tok[NI];
+    typename std::conditional<LO, u32x4, u32x2>::type tok[NI];
     u32x4 sums;
 };
 
-template <int NI>
-__device__ __forceinline__ void stage_load(StageRegs<NI> &s, const StageSrc &src, int kb,
+// LO: the whole 1 KiB piece (16 bytes per lane); otherwise its hi half
+// (8 bytes per lane)
+template <int NI, bool LO = true>
+__device__ __forceinline__ void stage_load(StageRegs<NI, LO> &s, const StageSrc &src, int kb,
                                            int wave, int lane) {
 #pragma unroll
-    for (int i = 0; i < NI; i++)
-        s.tok[i] = gload<u32x4>(src.tok[i] + (uint32_t)(kb * 1024 + 16 * lane));
+    for (int i = 0; i < NI; i++) {
+        if constexpr (LO)
+            s.tok[i] = gload<u32x4>(src.tok[i] + (uint32_t)(kb * 1024 + 16 * lane));
+        else
+            s.tok[i] = gload<u32x2>(src.tok[i] + (uint32_t)(kb * 1024 + 8 * lane));
+    }
     // every wave loads and stores the same sums (identical bytes), which
     // keeps the staging free of branches
     s.sums = gload<u32x4>(src.sums + (src.soff + (uint32_t)kb * 32));
 }
 
-template <int NI>
-__device__ __forceinline__ void stage_store(uint8_t *stage, const StageRegs<NI> &s, int wave,
+template <int NI, bool LO = true>
+__device__ __forceinline__ void stage_store(uint8_t *stage, const StageRegs<NI, LO> &s, int wave,
                                             int lane) {
 #pragma unroll
-    for (int i = 0; i < NI; i++)
-        *reinterpret_cast<u32x4 *>(stage + (wave + 4 * i) * kTokBytes + 16 * lane) = s.tok[i];
-    *reinterpret_cast<u32x4 *>(stage + kSumsOff + 16 * lane) = s.sums;
+    for (int i = 0; i < NI; i++) {
+        if constexpr (LO)
+            *reinterpret_cast<u32x4 *>(stage + (wave + 4 * i) * kTokBytes + 16 * lane) = s.tok[i];
+        else
+            *reinterpret_cast<u32x2 *>(stage + (wave + 4 * i) * kTokB<false> + 8 * lane) = s.tok[i];
+    }
+    *reinterpret_cast<u32x4 *>(stage + kSumsOffT<LO> + 16 * lane) = s.sums;
 }
 
 __device__ __forceinline__ void lds_barrier() {
@@ -285,17 +301,20 @@ struct AUnit {
     half8 h0, l0, h1, l1;
 };
 
+template <bool LO = true>
 __device__ __forceinline__ void read_a(AUnit &a, const uint8_t *tokrow, int u, int h) {
     const int col = 2 * (64 * (u >> 1) + 16 * (u & 1) + 8 * h);  // bytes
     a.h0 = *reinterpret_cast<const half8 *>(tokrow + col);
-    a.l0 = *reinterpret_cast<const half8 *>(tokrow + 512 + col);
     a.h1 = *reinterpret_cast<const half8 *>(tokrow + col + 64);
-    a.l1 = *reinterpret_cast<const half8 *>(tokrow + 512 + col + 64);
+    if constexpr (LO) {
+        a.l0 = *reinterpret_cast<const half8 *>(tokrow + 512 + col);
+        a.l1 = *reinterpret_cast<const half8 *>(tokrow + 512 + col + 64);
+    }
 }
 
 // One unit of MATS matrices: decode B for sub-blocks 2p (low nibbles) and
-// 2p+1 (high nibbles), four MFMAs per matrix.
-template <int MATS>
+// 2p+1 (high nibbles), four MFMAs per matrix (two without lo halves).
+template <int MATS, bool LO = true>
 __device__ __forceinline__ void unit_mfma(const WRaw (&w)[MATS], const Hdr (&hd)[MATS], int u,
                                           const AUnit &a, float16v (&S)[MATS]) {
     const int p = u >> 1;
@@ -304,9 +323,9 @@ __device__ __forceinline__ void unit_mfma(const WRaw (&w)[MATS], const Hdr (&hd)
         half8 blo, bhi;
         dec_pair(hd[m], p, w[m].q[u].x, w[m].q[u].y, blo, bhi);
         S[m] = mfma32(a.h0, blo, S[m]);
-        S[m] = mfma32(a.l0, blo, S[m]);
+        if constexpr (LO) S[m] = mfma32(a.l0, blo, S[m]);
         S[m] = mfma32(a.h1, bhi, S[m]);
-        S[m] = mfma32(a.l1, bhi, S[m]);
+        if constexpr (LO) S[m] = mfma32(a.l1, bhi, S[m]);
     }
 }
 
@@ -361,14 +380,14 @@ __device__ __forceinline__ void finish_split(const Hdr &hd, const half8 &amin, i
 
 // One step of a 32-token pass: super-block k from `cur` and w; activations
 // of super-block kn into `nxt`; w reloaded with super-block kn.
-template <int MATS, bool SPLIT = false>
+template <int MATS, bool SPLIT = false, bool LO = true>
 __device__ __forceinline__ void step(g_u8 *const (&wb)[MATS], uint32_t lo,
                                      const uint32_t (&dbo)[MATS], int kn, const uint8_t *cur,
                                      uint8_t *nxt, const StageSrc &src, WRaw (&w)[MATS],
                                      float16v (&acc)[MATS], int wave, int lane) {
     const int r = lane & 31, h = lane >> 5;
-    StageRegs<8> act;
-    stage_load(act, src, kn, wave, lane);
+    StageRegs<8, LO> act;
+    stage_load<8, LO>(act, src, kn, wave, lane);
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads first
     Hdr hd[MATS];
 #pragma unroll
@@ -380,14 +399,14 @@ __device__ __forceinline__ void step(g_u8 *const (&wb)[MATS], uint32_t lo,
     float16v S[MATS];
 #pragma unroll
     for (int m = 0; m < MATS; m++) S[m] = float16v{};
-    const uint8_t *tokrow = cur + r * kTokBytes;
-    const half8 *aminp = reinterpret_cast<const half8 *>(cur + kSumsOff + r * 32 + 16 * h);
+    const uint8_t *tokrow = cur + r * kTokB<LO>;
+    const half8 *aminp = reinterpret_cast<const half8 *>(cur + kSumsOffT<LO> + r * 32 + 16 * h);
     AUnit a[2];  // unit u's operands, and unit u+1's read ahead
-    read_a(a[0], tokrow, 0, h);
+    read_a<LO>(a[0], tokrow, 0, h);
 #pragma unroll
     for (int u = 0; u < 8; u++) {
-        if (u + 1 < 8) read_a(a[(u + 1) & 1], tokrow, u + 1, h);
-        unit_mfma<MATS>(w, hd, u, a[u & 1], S);
+        if (u + 1 < 8) read_a<LO>(a[(u + 1) & 1], tokrow, u + 1, h);
+        unit_mfma<MATS, LO>(w, hd, u, a[u & 1], S);
 #pragma unroll
         for (int m = 0; m < MATS; m++) w[m].q[u] = load_q<SPLIT>(wb[m], lo, kn, 1 + u, 8 * h);
         if (SPLIT && u == 3) {  // sub-blocks 0-3 done: their own d
@@ -407,7 +426,7 @@ __device__ __forceinline__ void step(g_u8 *const (&wb)[MATS], uint32_t lo,
         else
             finish_sb(hd[m], amin, h, S[m], acc[m]);
     }
-    stage_store(nxt, act, wave, lane);
+    stage_store<8, LO>(nxt, act, wave, lane);
     lds_barrier();
 }
 
@@ -416,7 +435,7 @@ __shared__ __attribute__((aligned(1024))) uint8_t s_stage1[kStageBytes];
 
 // One pass of the block over super-blocks [kb0, kb1) for its 32 tokens.
 // wb[m]: the wave's row group of matrix m (uniform); lo: this lane's row offset.
-template <int MATS, bool SPLIT = false>
+template <int MATS, bool SPLIT = false, bool LO = true>
 __device__ __forceinline__ void block_pass(g_u8 *const (&wb)[MATS], uint32_t lo,
                                            const uint32_t (&dbo)[MATS], int kb0, int kb1,
                                            const StageSrc &src, float16v (&acc)[MATS]) {
@@ -427,19 +446,20 @@ __device__ __forceinline__ void block_pass(g_u8 *const (&wb)[MATS], uint32_t lo,
     // instead of per-lane 64-bit addresses folded and kept across passes
     asm volatile("" : "+s"(kb0));
     WRaw w[MATS];
-    StageRegs<8> act;
-    stage_load(act, src, kb0, wave, lane);
+    StageRegs<8, LO> act;
+    stage_load<8, LO>(act, src, kb0, wave, lane);
 #pragma unroll
     for (int m = 0; m < MATS; m++) load_w<SPLIT>(w[m], wb[m], lo, dbo[m], kb0, h);
-    stage_store(s_stage0, act, wave, lane);
+    stage_store<8, LO>(s_stage0, act, wave, lane);
     lds_barrier();
     int kb = kb0;
     for (; kb + 2 <= kb1; kb += 2) {
-        step<MATS, SPLIT>(wb, lo, dbo, kb + 1, s_stage0, s_stage1, src, w, acc, wave, lane);
-        step<MATS, SPLIT>(wb, lo, dbo, min(kb + 2, last), s_stage1, s_stage0, src, w, acc, wave,
-                          lane);
+        step<MATS, SPLIT, LO>(wb, lo, dbo, kb + 1, s_stage0, s_stage1, src, w, acc, wave, lane);
+        step<MATS, SPLIT, LO>(wb, lo, dbo, min(kb + 2, last), s_stage1, s_stage0, src, w, acc,
+                              wave, lane);
     }
-    if (kb < kb1) step<MATS, SPLIT>(wb, lo, dbo, kb, s_stage0, s_stage1, src, w, acc, wave, lane);
+    if (kb < kb1)
+        step<MATS, SPLIT, LO>(wb, lo, dbo, kb, s_stage0, s_stage1, src, w, acc, wave, lane);
 }
 
 // ---- 16-token passes -------------------------------------------------------
@@ -500,25 +520,28 @@ __device__ __forceinline__ void finish16_part(const Hdr &hd, const half4 &amin, 
 
 // Activation operands of pair p for a 16-token pass: token r16, columns
 // 8*c4 .. +7 of sub-blocks 2p and 2p+1, hi and lo halves
+template <bool LO = true>
 __device__ __forceinline__ void read_a16(AUnit &a, const uint8_t *tokrow, int p, int c4) {
     const int col = 2 * (64 * p + 8 * c4);  // bytes
     a.h0 = *reinterpret_cast<const half8 *>(tokrow + col);
-    a.l0 = *reinterpret_cast<const half8 *>(tokrow + 512 + col);
     a.h1 = *reinterpret_cast<const half8 *>(tokrow + col + 64);
-    a.l1 = *reinterpret_cast<const half8 *>(tokrow + 512 + col + 64);
+    if constexpr (LO) {
+        a.l0 = *reinterpret_cast<const half8 *>(tokrow + 512 + col);
+        a.l1 = *reinterpret_cast<const half8 *>(tokrow + 512 + col + 64);
+    }
 }
 
 // One step of a 16-token pass (same pipeline as step()).  Per pair p the
 // activations of sub-blocks 2p and 2p+1 (hi, lo) are read once and shared by
 // both tiles and all matrices.
-template <int MATS, bool SPLIT = false>
+template <int MATS, bool SPLIT = false, bool LO = true>
 __device__ __forceinline__ void step16(g_u8 *const (&wb)[MATS], uint32_t lo,
                                        const uint32_t (&dbo)[MATS], int kn, const uint8_t *cur,
                                        uint8_t *nxt, const StageSrc &src, WRaw16 (&w)[MATS],
                                        float4v (&acc)[MATS][2], int wave, int lane) {
     const int r16 = lane & 15, c4 = lane >> 4;
-    StageRegs<4> act;
-    stage_load(act, src, kn, wave, lane);
+    StageRegs<4, LO> act;
+    stage_load<4, LO>(act, src, kn, wave, lane);
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads first
     Hdr hd[MATS][2];
 #pragma unroll
@@ -532,13 +555,13 @@ __device__ __forceinline__ void step16(g_u8 *const (&wb)[MATS], uint32_t lo,
     float4v S[MATS][2];
 #pragma unroll
     for (int m = 0; m < MATS; m++) S[m][0] = S[m][1] = float4v{};
-    const uint8_t *tokrow = cur + r16 * kTokBytes;
-    const half4 *aminp = reinterpret_cast<const half4 *>(cur + kSumsOff + r16 * 32 + 8 * c4);
+    const uint8_t *tokrow = cur + r16 * kTokB<LO>;
+    const half4 *aminp = reinterpret_cast<const half4 *>(cur + kSumsOffT<LO> + r16 * 32 + 8 * c4);
     AUnit a[2];  // pair p's operands, and pair p+1's read ahead
-    read_a16(a[0], tokrow, 0, c4);
+    read_a16<LO>(a[0], tokrow, 0, c4);
 #pragma unroll
     for (int p = 0; p < 4; p++) {
-        if (p + 1 < 4) read_a16(a[(p + 1) & 1], tokrow, p + 1, c4);
+        if (p + 1 < 4) read_a16<LO>(a[(p + 1) & 1], tokrow, p + 1, c4);
         const half8 h0 = a[p & 1].h0, l0 = a[p & 1].l0, h1 = a[p & 1].h1, l1 = a[p & 1].l1;
 #pragma unroll
         for (int m = 0; m < MATS; m++)
@@ -548,9 +571,9 @@ __device__ __forceinline__ void step16(g_u8 *const (&wb)[MATS], uint32_t lo,
                 dec_pair(hd[m][t], p, w[m].q[p][t].x, w[m].q[p][t].y, blo, bhi);
                 w[m].q[p][t] = load_q16<SPLIT>(wb[m], lo, kn, p, t, c4);
                 S[m][t] = mfma16(h0, blo, S[m][t]);
-                S[m][t] = mfma16(l0, blo, S[m][t]);
+                if constexpr (LO) S[m][t] = mfma16(l0, blo, S[m][t]);
                 S[m][t] = mfma16(h1, bhi, S[m][t]);
-                S[m][t] = mfma16(l1, bhi, S[m][t]);
+                if constexpr (LO) S[m][t] = mfma16(l1, bhi, S[m][t]);
             }
         if (SPLIT && p == 1) {  // sub-blocks 0-3 done: their own d, dmin
             const half4 amin = *aminp;
@@ -574,13 +597,13 @@ __device__ __forceinline__ void step16(g_u8 *const (&wb)[MATS], uint32_t lo,
             else
                 finish16(hd[m][t], amin, c4, S[m][t], acc[m][t]);
         }
-    stage_store(nxt, act, wave, lane);
+    stage_store<4, LO>(nxt, act, wave, lane);
     lds_barrier();
 }
 
 // block_pass() for a pass of at most 16 tokens; lo is the offset of this
 // lane's row r16 of the wave's first tile
-template <int MATS, bool SPLIT = false>
+template <int MATS, bool SPLIT = false, bool LO = true>
 __device__ __forceinline__ void block_pass16(g_u8 *const (&wb)[MATS], uint32_t lo,
                                              const uint32_t (&dbo)[MATS], int kb0, int kb1,
                                              const StageSrc &src, float4v (&acc)[MATS][2]) {
@@ -589,20 +612,20 @@ __device__ __forceinline__ void block_pass16(g_u8 *const (&wb)[MATS], uint32_t l
     const int last = kb1 - 1;
     asm volatile("" : "+s"(kb0));  // see block_pass()
     WRaw16 w[MATS];
-    StageRegs<4> act;
-    stage_load(act, src, kb0, wave, lane);
+    StageRegs<4, LO> act;
+    stage_load<4, LO>(act, src, kb0, wave, lane);
 #pragma unroll
     for (int m = 0; m < MATS; m++) load_w16<SPLIT>(w[m], wb[m], lo, dbo[m], kb0, c4);
-    stage_store(s_stage0, act, wave, lane);
+    stage_store<4, LO>(s_stage0, act, wave, lane);
     lds_barrier();
     int kb = kb0;
     for (; kb + 2 <= kb1; kb += 2) {
-        step16<MATS, SPLIT>(wb, lo, dbo, kb + 1, s_stage0, s_stage1, src, w, acc, wave, lane);
-        step16<MATS, SPLIT>(wb, lo, dbo, min(kb + 2, last), s_stage1, s_stage0, src, w, acc, wave,
-                            lane);
+        step16<MATS, SPLIT, LO>(wb, lo, dbo, kb + 1, s_stage0, s_stage1, src, w, acc, wave, lane);
+        step16<MATS, SPLIT, LO>(wb, lo, dbo, min(kb + 2, last), s_stage1, s_stage0, src, w, acc,
+                                wave, lane);
     }
     if (kb < kb1)
-        step16<MATS, SPLIT>(wb, lo, dbo, kb, s_stage0, s_stage1, src, w, acc, wave, lane);
+        step16<MATS, SPLIT, LO>(wb, lo, dbo, kb, s_stage0, s_stage1, src, w, acc, wave, lane);
 }
 
 // split v into f16 hi + lo
@@ -621,6 +644,8 @@ static_assert(kStageBytes / 8 >= chain_lds_floats(16, 128), "chain tile LDS");
 // grid (F/128 row blocks, [chain row +] slots, pass groups); block = 4 waves
 // x 32 weight rows.  With ch.tiles, row y = 0 runs the exact router chains
 // (a wave per 8 x 8 tile, blocks of z = 0) and slot s is row s + 1.
+// LO: x enters as two f16 (hi + lo); otherwise as its hi half alone.
+template <bool LO>
 __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
     const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up, int64_t estride,
     const _Float16 *__restrict__ x16, const _Float16 *__restrict__ xs, SlotArgs sa, int d, int F,
@@ -666,7 +691,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
         if (n - c <= 16) {
             const int r16 = lane & 15, c4 = lane >> 4;
             float4v acc[2][2] = {};
-            block_pass16<2>(wb, r16 * 16, nodb, 0, NB, src, acc);
+            block_pass16<2, false, LO>(wb, r16 * 16, nodb, 0, NB, src, acc);
             if (grp0 >= ngrp) continue;
             // output addresses are formed here from an opaque row index, so
             // that the compiler does not keep them live across the pass
@@ -708,7 +733,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
             continue;
         }
         float16v acc[2] = {float16v{}, float16v{}};
-        block_pass<2>(wb, r * 16, nodb, 0, NB, src, acc);
+        block_pass<2, false, LO>(wb, r * 16, nodb, 0, NB, src, acc);
         if (grp0 >= ngrp) continue;
         int fo = f;  // opaque copy: output addresses are formed here (see above)
         asm volatile("" : "+v"(fo));
@@ -1245,11 +1270,11 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down_q6(
 // per-sub-block sums (hi, lo); one thread per 32-column sub-block
 __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int T, int d,
                                                _Float16 *__restrict__ x16,
-                                               _Float16 *__restrict__ xs) {
+                                               _Float16 *__restrict__ xs, bool lo) {
     const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // sub-block index
     const int nsb = d >> 5;
     if (q >= (int64_t)T * nsb) return;
-    act16_subblock(x + q * 32, q / nsb, d, (int)(q % nsb), x16, xs);
+    act16_subblock(x + q * 32, q / nsb, d, (int)(q % nsb), x16, xs, lo);
 }
 
 SlotArgs dev_slots(const SlotArgsHost &s) {
@@ -1275,17 +1300,17 @@ hipError_t launch_mfma_down_q6(const uint8_t *down, int64_t estride, const _Floa
 }
 
 hipError_t launch_act16(const float *x, int T, int d, _Float16 *x16, _Float16 *xs,
-                        hipStream_t st) {
+                        hipStream_t st, bool lo) {
     const int64_t n = (int64_t)T * (d / 32);
     hipLaunchKernelGGL(k_act16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, T, d, x16,
-                       xs);
+                       xs, lo);
     return hipGetLastError();
 }
 
 hipError_t launch_mfma_gateup(const uint8_t *gate, const uint8_t *up, int64_t estride,
                               const _Float16 *x16, const _Float16 *xs, const SlotArgsHost &sa,
                               int slots, int chunks, int d, int F, _Float16 *h16, _Float16 *hs,
-                              float *hf, const ChainArgs &ch, hipStream_t st) {
+                              float *hf, const ChainArgs &ch, hipStream_t st, bool x_lo) {
     const int groups = F / 32;
     ChainArgs c = ch;
     if (c.tiles) {
@@ -1293,7 +1318,7 @@ hipError_t launch_mfma_gateup(const uint8_t *gate, const uint8_t *up, int64_t es
         c = with_nt(ch, 8);
     }
     if (chunks < 1 || chunks > 65535) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_mfma_gateup,
+    hipLaunchKernelGGL(x_lo ? k_mfma_gateup<true> : k_mfma_gateup<false>,
                        dim3((groups + kWaves - 1) / kWaves, slots + (c.tiles ? 1 : 0), chunks),
                        dim3(256), 0, st, gate, up, estride, x16, xs, dev_slots(sa), d, F, h16, hs,
                        hf, c);

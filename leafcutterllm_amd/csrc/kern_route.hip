@@ -614,7 +614,8 @@ __device__ void quantise_token(const RouterArgs &a, int t, float *s_x, int share
                 const _Float16 lo = (_Float16)(f[i] - (float)hi);
                 hv[i] = hi;
                 lv[i] = lo;
-                sum = sum + ((float)hi + (float)lo);
+                // the sum of what the products take: hi + lo, or hi alone
+                sum = sum + (a.x16_lo ? (float)hi + (float)lo : (float)hi);
             }
             // the sub-block sum in column order: (c0..7 + c8..15) + (c16..23 + c24..31)
             sum = sum + __shfl_xor(sum, 1, 64);

@@ -30,6 +30,7 @@ struct RouterArgs {
     int8_t *xh, *xl;      // [T, d] limbs, or null
     float *xs, *xm;       // [T, d/32] scale and quantised-sum
     _Float16 *x16, *x16s; // f16 hi/lo pieces and sums for the matrix-core path, or null
+    bool x16_lo = true;   // sums of hi + lo (the products take both halves), else of hi
     int32_t *counts, *offsets, *perm, *inv, *touched;
     // pass slots, or null: [0] = their number P, then per slot v < P the
     // entry pass * 256 + e, the 32-token passes of every touched expert in
@@ -120,13 +121,14 @@ hipError_t launch_rpl_down(const uint8_t *down, int64_t estride, const int8_t *h
 // Matrix-core path on the RPL64 layout: activations as f16 hi/lo pieces
 // (per token and super-block: hi[256] then lo[256]) plus per-sub-block sums,
 // H out in the same format (and/or f32).
-hipError_t launch_act16(const float *x, int T, int d, _Float16 *x16, _Float16 *xs, hipStream_t st);
+hipError_t launch_act16(const float *x, int T, int d, _Float16 *x16, _Float16 *xs, hipStream_t st,
+                        bool lo = true);
 // `chunks` blocks share each slot's 32-token passes (block z takes passes
 // z, z + chunks, ...), so experts with many tokens spread over the chip.
 hipError_t launch_mfma_gateup(const uint8_t *gate, const uint8_t *up, int64_t estride,
                               const _Float16 *x16, const _Float16 *xs, const SlotArgsHost &sa,
                               int slots, int chunks, int d, int F, _Float16 *h16, _Float16 *hs,
-                              float *hf, const ChainArgs &ch, hipStream_t st);
+                              float *hf, const ChainArgs &ch, hipStream_t st, bool x_lo);
 hipError_t launch_mfma_down(const uint8_t *down, int64_t estride, const _Float16 *h16,
                             const _Float16 *hs, const SlotArgsHost &sa, int slots, int chunks,
                             int d, int F, int ksplit, float *Y, int64_t split_stride,

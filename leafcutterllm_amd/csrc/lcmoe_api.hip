@@ -102,6 +102,9 @@ struct lcmoe_handle {
     bool last_sig = false;  // the last forward used the parallel-bounds certified router
     hipStream_t last_stream = nullptr;
     bool timing = false;
+    // matrix-core gate/up products take x as two f16 (hi + lo) instead of
+    // one (lcmoe_set_act_precision)
+    bool x_lo = false;
     struct Pending { int slot; hipEvent_t a, b; };
     std::vector<Pending> pending;
     std::vector<hipEvent_t> event_pool;
@@ -529,7 +532,7 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
         if (pl.mfma)
             return launch_mfma_gateup(s.gate, s.up, s.sz_gu, h->x16, h->x16s, sa, slots,
                                       pl.chunks, d, s.F, h16_out ? s.h16 : nullptr, s.h16s,
-                                      h16_out ? nullptr : s.Hf, ch, st);
+                                      h16_out ? nullptr : s.Hf, ch, st, h->x_lo);
         if (s.rpl_gu || s.q8)
             return launch_rpl_gateup(s.gate, s.up, s.sz_gu, h->xh, h->xl, h->xs, h->xm, sa,
                                      slots, d, s.F, s.Hf, limb_out ? s.hh : nullptr, s.hl,
@@ -600,6 +603,7 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
     ra.xm = h->xm;
     ra.x16 = nullptr;
     ra.x16s = h->x16s;
+    ra.x16_lo = h->x_lo;
     ra.counts = h->counts;
     ra.offsets = h->offsets;
     ra.perm = h->perm;
@@ -673,7 +677,7 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
         HIP_TRY(timed(h, st, kSlotRouter, [&] { return launch_router(ra, st); }));
         if (mfma)
             HIP_TRY(timed(h, st, kSlotPrep, [&] {
-                return launch_act16(x, T, d, h->x16, h->x16s, st);
+                return launch_act16(x, T, d, h->x16, h->x16s, st, h->x_lo);
             }));
     }
     lcmoe_status s;
@@ -742,6 +746,19 @@ extern "C" lcmoe_status lcmoe_forward(lcmoe_handle *h, const float *x, int32_t T
         HIP_TRY(hipMemcpyAsync(topk_idx, h->topk_idx, kb * 4, hipMemcpyDeviceToHost, h->stream));
     if (topk_w) HIP_TRY(hipMemcpyAsync(topk_w, h->topk_w, kb * 4, hipMemcpyDeviceToHost, h->stream));
     HIP_TRY(hipStreamSynchronize(h->stream));
+    return LCMOE_OK;
+}
+
+extern "C" lcmoe_status lcmoe_set_act_precision(lcmoe_handle *h, int32_t mode) {
+    clear_error();
+    if (!h) return fail(LCMOE_ERR_INVALID_ARG, "handle is NULL");
+    if (mode != LCMOE_ACT_F16 && mode != LCMOE_ACT_F16X2)
+        return fail(LCMOE_ERR_INVALID_ARG, "mode=%d (LCMOE_ACT_F16 or LCMOE_ACT_F16X2)", mode);
+    // a forward may still be reading the activations in the other format
+    HIP_TRY(hipSetDevice(h->device));
+    HIP_TRY(hipStreamSynchronize(h->stream));
+    if (h->last_stream) HIP_TRY(hipStreamSynchronize(h->last_stream));
+    h->x_lo = mode == LCMOE_ACT_F16X2;
     return LCMOE_OK;
 }
 

@@ -442,6 +442,9 @@ extern "C" lcmoe_status lcmoe_model_create(const lcmoe_model_desc *desc,
         }
         if ((st = upload_norm(&ML.attn_norm, L.attn_norm))) return bail(st);
         if ((st = lcmoe_create(&md, &L.moe, &ML.moe))) return bail(st);
+        // 24 layers compound each layer's error (and near-tie routing flips
+        // follow it): the decoder takes the two-f16 activations
+        if ((st = lcmoe_set_act_precision(ML.moe, LCMOE_ACT_F16X2))) return bail(st);
         if ((st = lcmoe_set_norm(ML.moe, L.ffn_norm, D.norm_eps))) return bail(st);
     }
     const int64_t cache = (int64_t)D.n_layer * D.max_batch * D.max_ctx * KVH * hd;

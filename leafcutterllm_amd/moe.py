@@ -87,6 +87,11 @@ class MoeFfn:
     def forward_dev(self, x_dev: int, T: int, y_dev: int, stream: int | None = None) -> None:
         check(lib().lcmoe_forward_dev(self._h, x_dev, T, y_dev, stream), "lcmoe_forward_dev")
 
+    def set_act_precision(self, mode: int) -> None:
+        """ACT_F16 (default) or ACT_F16X2: how x enters the matrix-core
+        gate/up products (lcmoe_set_act_precision)."""
+        check(lib().lcmoe_set_act_precision(self._h, int(mode)), "lcmoe_set_act_precision")
+
     def set_norm(self, weight: np.ndarray, eps: float = 1e-5) -> None:
         """Post-attention RMSNorm weight [d_model] for forward_norm_residual."""
         weight = np.ascontiguousarray(weight, np.float32)

@@ -319,17 +319,26 @@ def test_e1_k1_reduces_to_dense_ffn():
     cfg = small_config("dense", 256, 512, 1, 1, L.ROUTE_SOFTMAX_RENORM, Q4, Q4)
     layer = L.synth_layer(cfg, seed=8)
     x = L.synth_x(cfg, 9, seed=8)
-    with L.MoeFfn(cfg.desc(9), layer) as moe:
-        y, idx, w = moe.forward(x)
-    assert np.all(idx == 0) and np.all(w == 1.0)
     wg = O.dequant(Q4, layer["gate"], 512 * 256).reshape(512, 256).T
     wu = O.dequant(Q4, layer["up"], 512 * 256).reshape(512, 256).T
     wd = O.dequant(Q4, layer["down"], 256 * 512).reshape(256, 512).T
-    ref = O.ffn_dense(x, wg, wu, wd)
-    # Q4_K row-per-lane path: x and H enter the integer products as 15-bit
-    # two-limb values (|error| <= max|v| / 32512 per 32-element sub-block),
-    # about 1e-4 relative on y; the layer bar is 1e-3
-    assert rel_l2(y, ref) < 2e-4
+    with L.MoeFfn(cfg.desc(9), layer) as moe:
+        # T = 1: the row-per-lane path: x and H enter the integer products as
+        # 15-bit two-limb values (|error| <= max|v| / 32512 per 32-element
+        # sub-block), about 1e-4 relative on y
+        y, idx, w = moe.forward(x[:1])
+        assert idx[0, 0] == 0 and w[0, 0] == 1.0
+        assert rel_l2(y, O.ffn_dense(x[:1], wg, wu, wd)) < 2e-4
+        # T = 9 > E: the matrix-core path; x as two f16 (about 3e-6), then
+        # as one f16 (the default, about 3e-4; the layer bar is 1e-3)
+        ref = O.ffn_dense(x, wg, wu, wd)
+        moe.set_act_precision(L.ACT_F16X2)
+        y, idx, w = moe.forward(x)
+        assert np.all(idx == 0) and np.all(w == 1.0)
+        assert rel_l2(y, ref) < 2e-5
+        moe.set_act_precision(L.ACT_F16)
+        y, _, _ = moe.forward(x)
+        assert rel_l2(y, ref) < 1e-3
 
 
 # ------------------------------------------------- full BASELINE shapes -----
@@ -384,3 +393,24 @@ def test_full_config3_prefill_parity(full_layers):
     counts = res["counts"]
     assert counts[:8].sum() > counts[8:].sum()   # the +2.0 bias skews routing
     print(f"config 3 T=2048: rel_l2={res['rel_l2']:.2e} biased-share={counts[:8].sum() / counts.sum():.2f}")
+
+
+@pytest.mark.parametrize("c,T", [(2, 64), (3, 256), (4, 256)])
+def test_activation_precision_modes(full_layers, c, T):
+    """The matrix-core gate/up products in both activation modes on the
+    same inputs: LCMOE_ACT_F16 (the default, one f16 per element) within the
+    1e-3 bar, LCMOE_ACT_F16X2 (two f16) within 2e-5 -- and the two differ,
+    so the mode reaches the kernel.  Routing is bit-exact in both (it does
+    not depend on the mode)."""
+    cfg, layer, moe = full_layers(c)
+    x = L.synth_x(cfg, T, seed=0, index=T)
+    try:
+        moe.set_act_precision(L.ACT_F16X2)
+        two = run_and_check(cfg, layer, x, moe=moe)
+        moe.set_act_precision(L.ACT_F16)
+        one = run_and_check(cfg, layer, x, moe=moe)
+    finally:
+        moe.set_act_precision(L.ACT_F16)
+    print(f"config {c} T={T}: F16 rel_l2={one['rel_l2']:.2e}, F16X2 rel_l2={two['rel_l2']:.2e}")
+    assert two["rel_l2"] <= 2e-5
+    assert one["rel_l2"] > 4 * two["rel_l2"]
