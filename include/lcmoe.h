@@ -148,16 +148,17 @@ lcmoe_status lcmoe_forward_dev(lcmoe_handle *h, const float *x_dev, int32_t T, f
 /* Activation operands of the matrix-core expert products (batches where
  * the experts see more tokens than there are experts: T*K > E; prefill).
  * The weights are always exact (sc*q in f16, scales in f32) and the sums
- * f32; the mode sets how x enters the gate/up products:
+ * f32; the mode sets how x enters the gate/up products and H the down
+ * products:
  *   LCMOE_ACT_F16   (default) one f16 per element: layer output within about
- *                   3.6e-4 relative L2 of the reference CPU path at every
+ *                   3.7e-4 relative L2 of the reference CPU path at every
  *                   benchmark shape (the bar is 1e-3), half the matrix-core
  *                   work and activation traffic of F16X2;
  *   LCMOE_ACT_F16X2 two f16 (hi + lo = x to about 22 bits): about 3e-6, for
  *                   deep stacks where per-layer error compounds (lcmoe_model
  *                   selects it for every layer).
- * The down products take H as two f16 in both modes; the row-per-lane
- * (decode) kernels always use exact integer products on 15-bit activations.
+ * The row-per-lane (decode) kernels always use exact integer products on
+ * 15-bit activations.
  * No counterpart in the reference (its CPU path is f32 throughout). */
 enum { LCMOE_ACT_F16 = 0, LCMOE_ACT_F16X2 = 1 };
 lcmoe_status lcmoe_set_act_precision(lcmoe_handle *h, int32_t mode);

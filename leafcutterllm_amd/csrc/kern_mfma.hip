@@ -644,7 +644,9 @@ static_assert(kStageBytes / 8 >= chain_lds_floats(16, 128), "chain tile LDS");
 // grid (F/128 row blocks, [chain row +] slots, pass groups); block = 4 waves
 // x 32 weight rows.  With ch.tiles, row y = 0 runs the exact router chains
 // (a wave per 8 x 8 tile, blocks of z = 0) and slot s is row s + 1.
-// LO: x enters as two f16 (hi + lo); otherwise as its hi half alone.
+// LO: x enters as two f16 (hi + lo); otherwise as its hi half alone.  H
+// leaves in the format the down products of the same mode take (with LO
+// its lo halves and the sums of hi + lo, without it sums of hi alone).
 template <bool LO>
 __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
     const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up, int64_t estride,
@@ -706,7 +708,8 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
                 for (int t = 0; t < 2; t++) {
                     v[t] = silu(acc[0][t][i]) * acc[1][t][i];
                     split16(v[t], hi[t], lo[t]);
-                    part += (float)hi[t] + (float)lo[t];
+                    // the sums of what the down products take
+                    part += LO ? (float)hi[t] + (float)lo[t] : (float)hi[t];
                 }
 #pragma unroll
                 for (int off = 1; off < 16; off <<= 1) part += __shfl_xor(part, off, 64);
@@ -719,7 +722,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
                         if (h16) {
                             _Float16 *piece = h16 + (p * nkb + (ft >> 8)) * 512 + (ft & 255);
                             piece[0] = hi[t];
-                            piece[256] = lo[t];
+                            if (LO) piece[256] = lo[t];
                         }
                     }
                     if (h16 && r16 == 0) {
@@ -744,7 +747,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
             const float v = silu(acc[0][i]) * acc[1][i];
             _Float16 hi, lo;
             split16(v, hi, lo);
-            float part = (float)hi + (float)lo;
+            float part = LO ? (float)hi + (float)lo : (float)hi;
 #pragma unroll
             for (int off = 1; off < 32; off <<= 1) part += __shfl_xor(part, off, 64);
             if (q < n) {
@@ -753,7 +756,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
                 if (h16) {
                     _Float16 *piece = h16 + (p * nkb + (fo >> 8)) * 512 + (fo & 255);
                     piece[0] = hi;
-                    piece[256] = lo;
+                    if (LO) piece[256] = lo;
                     if (r == 0) {
                         _Float16 shi, slo;
                         split16(part, shi, slo);
@@ -772,7 +775,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
 // (the two "matrices" of the pipeline), so each LDS read feeds twice the
 // weight bytes of a 32-row wave.  SPLIT: F is an odd multiple of 128 and the
 // weights are in the split layout (ceil(F / 256) super-blocks per row).
-template <bool SPLIT>
+template <bool SPLIT, bool LO>
 __global__ __launch_bounds__(256, 2) void k_mfma_down(
     const uint8_t *__restrict__ down, int64_t estride, const _Float16 *__restrict__ h16,
     const _Float16 *__restrict__ hs, SlotArgs sa, int d, int F, int ksplit, float *__restrict__ Y,
@@ -822,7 +825,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down(
             const uint32_t dbo[2] = {9 * 1024 + 4 * (uint32_t)r16,
                                      9 * 1024 + 4 * (32 + (uint32_t)r16) - 32 * 16};
             float4v acc[2][2] = {};
-            block_pass16<2, SPLIT>(wb, r16 * 16, dbo, kb0, kb1, src, acc);
+            block_pass16<2, SPLIT, LO>(wb, r16 * 16, dbo, kb0, kb1, src, acc);
             if (tile0 >= ntile) continue;
             int rb = tile * 64 + r16;  // opaque: output addresses are formed here
             asm volatile("" : "+v"(rb));
@@ -842,7 +845,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down(
         const uint32_t dbo[2] = {9 * 1024 + 4 * (uint32_t)r,
                                  9 * 1024 + 4 * (32 + (uint32_t)r) - 32 * 16};
         float16v acc[2] = {float16v{}, float16v{}};
-        block_pass<2, SPLIT>(wb, r * 16, dbo, kb0, kb1, src, acc);
+        block_pass<2, SPLIT, LO>(wb, r * 16, dbo, kb0, kb1, src, acc);
         if (tile0 >= ntile) continue;
         int rb = tile * 64 + r;  // opaque: output addresses are formed here
         asm volatile("" : "+v"(rb));
@@ -941,13 +944,14 @@ __device__ __forceinline__ void dec6(uint32_t g0, uint32_t g1, half2v sh2, half2
 // One step of a 32-token pass over Q6_K: super-block k of both 32-row halves
 // from `cur` and w; activations of super-block kn into `nxt`; w reloaded
 // with kn unit by unit after each unit's decode.
+template <bool LO>
 __device__ __forceinline__ void step_q6(g_u8 *wb, const uint32_t (&lo)[2], const uint32_t (&rlo)[2],
                                         const uint32_t (&dlo)[2], int kn, const uint8_t *cur,
                                         uint8_t *nxt, const StageSrc &src, W6 (&w)[2],
                                         float16v (&acc)[2], int wave, int lane) {
     const int r = lane & 31, h = lane >> 5;
-    StageRegs<8> act;
-    stage_load(act, src, kn, wave, lane);
+    StageRegs<8, LO> act;
+    stage_load<8, LO>(act, src, kn, wave, lane);
     __builtin_amdgcn_sched_barrier(0);
     u32x4 sc[2];
     float dd[2];
@@ -960,7 +964,7 @@ __device__ __forceinline__ void step_q6(g_u8 *wb, const uint32_t (&lo)[2], const
     float16v S1[2], S2[2];
 #pragma unroll
     for (int m = 0; m < 2; m++) S1[m] = S2[m] = float16v{};
-    const uint8_t *tokrow = cur + r * kTokBytes;
+    const uint8_t *tokrow = cur + r * kTokB<LO>;
     const half2v k1024 = half2v{(_Float16)-1024.0f, (_Float16)-1024.0f};
     const half2v k1032 = half2v{(_Float16)-1032.0f, (_Float16)-1032.0f};
     const half2v k1056 = half2v{(_Float16)-1056.0f, (_Float16)-1056.0f};
@@ -982,7 +986,8 @@ __device__ __forceinline__ void step_q6(g_u8 *wb, const uint32_t (&lo)[2], const
         for (int j = 0; j < 4; j++) {
             const int col = 2 * (128 * n + 32 * j + 16 * i + 8 * h);  // bytes
             const half8 ah = *reinterpret_cast<const half8 *>(tokrow + col);
-            const half8 al = *reinterpret_cast<const half8 *>(tokrow + 512 + col);
+            half8 al{};
+            if constexpr (LO) al = *reinterpret_cast<const half8 *>(tokrow + 512 + col);
 #pragma unroll
             for (int m = 0; m < 2; m++) {
                 const int b = i + 2 * (j & 1);
@@ -994,9 +999,9 @@ __device__ __forceinline__ void step_q6(g_u8 *wb, const uint32_t (&lo)[2], const
                 half8 b1, b2;
                 dec6(g0, g1, sh2, c1, sl2, c2, b1, b2);
                 S1[m] = mfma32(ah, b1, S1[m]);
-                S1[m] = mfma32(al, b1, S1[m]);
+                if constexpr (LO) S1[m] = mfma32(al, b1, S1[m]);
                 S2[m] = mfma32(ah, b2, S2[m]);
-                S2[m] = mfma32(al, b2, S2[m]);
+                if constexpr (LO) S2[m] = mfma32(al, b2, S2[m]);
             }
         }
 #pragma unroll
@@ -1012,10 +1017,11 @@ __device__ __forceinline__ void step_q6(g_u8 *wb, const uint32_t (&lo)[2], const
             acc[m][t] = __builtin_fmaf(dd[m], S2[m][t], acc[m][t]);
         }
     }
-    stage_store(nxt, act, wave, lane);
+    stage_store<8, LO>(nxt, act, wave, lane);
     lds_barrier();
 }
 
+template <bool LO>
 __device__ __forceinline__ void block_pass_q6(g_u8 *wb, const uint32_t (&lo)[2],
                                               const uint32_t (&rlo)[2], const uint32_t (&dlo)[2],
                                               int kb0, int kb1, const StageSrc &src,
@@ -1025,22 +1031,23 @@ __device__ __forceinline__ void block_pass_q6(g_u8 *wb, const uint32_t (&lo)[2],
     const int last = kb1 - 1;
     asm volatile("" : "+s"(kb0));  // see block_pass()
     W6 w[2];
-    StageRegs<8> act;
-    stage_load(act, src, kb0, wave, lane);
+    StageRegs<8, LO> act;
+    stage_load<8, LO>(act, src, kb0, wave, lane);
 #pragma unroll
     for (int m = 0; m < 2; m++) {
         load_w6_head(w[m], wb, rlo[m], dlo[m], kb0);
 #pragma unroll
         for (int v = 0; v < 4; v++) load_w6_unit(w[m], wb, lo[m], kb0, v);
     }
-    stage_store(s_stage0, act, wave, lane);
+    stage_store<8, LO>(s_stage0, act, wave, lane);
     lds_barrier();
     int kb = kb0;
     for (; kb + 2 <= kb1; kb += 2) {
-        step_q6(wb, lo, rlo, dlo, kb + 1, s_stage0, s_stage1, src, w, acc, wave, lane);
-        step_q6(wb, lo, rlo, dlo, min(kb + 2, last), s_stage1, s_stage0, src, w, acc, wave, lane);
+        step_q6<LO>(wb, lo, rlo, dlo, kb + 1, s_stage0, s_stage1, src, w, acc, wave, lane);
+        step_q6<LO>(wb, lo, rlo, dlo, min(kb + 2, last), s_stage1, s_stage0, src, w, acc, wave,
+                    lane);
     }
-    if (kb < kb1) step_q6(wb, lo, rlo, dlo, kb, s_stage0, s_stage1, src, w, acc, wave, lane);
+    if (kb < kb1) step_q6<LO>(wb, lo, rlo, dlo, kb, s_stage0, s_stage1, src, w, acc, wave, lane);
 }
 
 // ---- Q6_K down, 16-token passes (v_mfma_f32_16x16x32_f16) ------------------
@@ -1070,14 +1077,15 @@ __device__ __forceinline__ void load_w6t_half(W6t &w, g_u8 *base, uint32_t lo, i
     w.q[n][2] = load_q6(base, lo, kb, 8 + 2 * n + cb);
 }
 
+template <bool LO>
 __device__ __forceinline__ void step16_q6(g_u8 *wb, const uint32_t (&lo)[2][2],
                                           const uint32_t (&rlo)[2][2], const uint32_t (&dlo)[2][2],
                                           int kn, const uint8_t *cur, uint8_t *nxt,
                                           const StageSrc &src, W6t (&w)[2][2],
                                           float4v (&acc)[2][2], int wave, int lane) {
     const int r16 = lane & 15, c4 = lane >> 4, cb = c4 >> 1;
-    StageRegs<4> act;
-    stage_load(act, src, kn, wave, lane);
+    StageRegs<4, LO> act;
+    stage_load<4, LO>(act, src, kn, wave, lane);
     __builtin_amdgcn_sched_barrier(0);
     // scales are read from w and reloaded with kn after the last group
     float dd[2][2];
@@ -1090,7 +1098,7 @@ __device__ __forceinline__ void step16_q6(g_u8 *wb, const uint32_t (&lo)[2][2],
     for (int m = 0; m < 2; m++)
 #pragma unroll
         for (int t = 0; t < 2; t++) S1[m][t] = S2[m][t] = float4v{};
-    const uint8_t *tokrow = cur + r16 * kTokBytes;
+    const uint8_t *tokrow = cur + r16 * kTokB<LO>;
     const half2v k1024 = half2v{(_Float16)-1024.0f, (_Float16)-1024.0f};
     const half2v k1032 = half2v{(_Float16)-1032.0f, (_Float16)-1032.0f};
     const half2v k1056 = half2v{(_Float16)-1056.0f, (_Float16)-1056.0f};
@@ -1100,7 +1108,8 @@ __device__ __forceinline__ void step16_q6(g_u8 *wb, const uint32_t (&lo)[2][2],
         for (int j = 0; j < 4; j++) {
             const int col = 2 * (128 * n + 32 * j + 8 * c4);  // bytes
             const half8 ah = *reinterpret_cast<const half8 *>(tokrow + col);
-            const half8 al = *reinterpret_cast<const half8 *>(tokrow + 512 + col);
+            half8 al{};
+            if constexpr (LO) al = *reinterpret_cast<const half8 *>(tokrow + 512 + col);
             const int b = 2 * (j & 1) + cb;  // scale byte within word 2n + j/2
 #pragma unroll
             for (int m = 0; m < 2; m++)
@@ -1116,9 +1125,9 @@ __device__ __forceinline__ void step16_q6(g_u8 *wb, const uint32_t (&lo)[2][2],
                     half8 b1, b2;
                     dec6(g0, g1, sh2, c1, sl2, c2, b1, b2);
                     S1[m][t] = mfma16(ah, b1, S1[m][t]);
-                    S1[m][t] = mfma16(al, b1, S1[m][t]);
+                    if constexpr (LO) S1[m][t] = mfma16(al, b1, S1[m][t]);
                     S2[m][t] = mfma16(ah, b2, S2[m][t]);
-                    S2[m][t] = mfma16(al, b2, S2[m][t]);
+                    if constexpr (LO) S2[m][t] = mfma16(al, b2, S2[m][t]);
                 }
         }
 #pragma unroll
@@ -1141,10 +1150,11 @@ __device__ __forceinline__ void step16_q6(g_u8 *wb, const uint32_t (&lo)[2][2],
                 acc[m][t][i] = __builtin_fmaf(dd[m][t], S2[m][t][i], acc[m][t][i]);
             }
         }
-    stage_store(nxt, act, wave, lane);
+    stage_store<4, LO>(nxt, act, wave, lane);
     lds_barrier();
 }
 
+template <bool LO>
 __device__ __forceinline__ void block_pass16_q6(g_u8 *wb, const uint32_t (&lo)[2][2],
                                                 const uint32_t (&rlo)[2][2],
                                                 const uint32_t (&dlo)[2][2], int kb0, int kb1,
@@ -1154,8 +1164,8 @@ __device__ __forceinline__ void block_pass16_q6(g_u8 *wb, const uint32_t (&lo)[2
     const int last = kb1 - 1;
     asm volatile("" : "+s"(kb0));  // see block_pass()
     W6t w[2][2];
-    StageRegs<4> act;
-    stage_load(act, src, kb0, wave, lane);
+    StageRegs<4, LO> act;
+    stage_load<4, LO>(act, src, kb0, wave, lane);
 #pragma unroll
     for (int m = 0; m < 2; m++)
 #pragma unroll
@@ -1164,21 +1174,22 @@ __device__ __forceinline__ void block_pass16_q6(g_u8 *wb, const uint32_t (&lo)[2
 #pragma unroll
             for (int n = 0; n < 2; n++) load_w6t_half(w[m][t], wb, lo[m][t], kb0, n, cb);
         }
-    stage_store(s_stage0, act, wave, lane);
+    stage_store<4, LO>(s_stage0, act, wave, lane);
     lds_barrier();
     int kb = kb0;
     for (; kb + 2 <= kb1; kb += 2) {
-        step16_q6(wb, lo, rlo, dlo, kb + 1, s_stage0, s_stage1, src, w, acc, wave, lane);
-        step16_q6(wb, lo, rlo, dlo, min(kb + 2, last), s_stage1, s_stage0, src, w, acc, wave,
-                  lane);
+        step16_q6<LO>(wb, lo, rlo, dlo, kb + 1, s_stage0, s_stage1, src, w, acc, wave, lane);
+        step16_q6<LO>(wb, lo, rlo, dlo, min(kb + 2, last), s_stage1, s_stage0, src, w, acc, wave,
+                      lane);
     }
-    if (kb < kb1) step16_q6(wb, lo, rlo, dlo, kb, s_stage0, s_stage1, src, w, acc, wave, lane);
+    if (kb < kb1)
+        step16_q6<LO>(wb, lo, rlo, dlo, kb, s_stage0, s_stage1, src, w, acc, wave, lane);
 }
 
 // grid (d/256 row blocks, slots, ksplit x pass groups), as k_mfma_down.  P16:
 // passes of 16 tokens (16x16x32 MFMAs), else of 32 (32x32x16); one kind per
 // kernel keeps each within the register file.
-template <bool P16>
+template <bool P16, bool LO>
 __global__ __launch_bounds__(256, 2) void k_mfma_down_q6(
     const uint8_t *__restrict__ down, int64_t estride, const _Float16 *__restrict__ h16,
     SlotArgs sa, int d, int F, int ksplit, float *__restrict__ Y, int64_t split_stride) {
@@ -1232,7 +1243,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down_q6(
                     dlo16[m][t] = row * 2;
                 }
             float4v acc[2][2] = {};
-            block_pass16_q6(wb, lo16, rlo16, dlo16, kb0, kb1, src, acc);
+            block_pass16_q6<LO>(wb, lo16, rlo16, dlo16, kb0, kb1, src, acc);
             if (tile0 >= ntile) continue;
             int rb = tile * 64 + r16;  // opaque: output addresses are formed here
             asm volatile("" : "+v"(rb));
@@ -1249,7 +1260,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down_q6(
             }
         } else {
         float16v acc[2] = {float16v{}, float16v{}};
-        block_pass_q6(wb, lo, rlo, dlo, kb0, kb1, src, acc);
+        block_pass_q6<LO>(wb, lo, rlo, dlo, kb0, kb1, src, acc);
         if (tile0 >= ntile) continue;
         int rb = tile * 64 + r;  // opaque: output addresses are formed here
         asm volatile("" : "+v"(rb));
@@ -1286,16 +1297,14 @@ SlotArgs dev_slots(const SlotArgsHost &s) {
 hipError_t launch_mfma_down_q6(const uint8_t *down, int64_t estride, const _Float16 *h16,
                                const SlotArgsHost &sa, int slots, int chunks, int d, int F,
                                int ksplit, float *Y, int64_t split_stride, hipStream_t st,
-                               bool p16) {
+                               bool p16, bool h_lo) {
     const int tiles = d / 64;
     if (chunks < 1 || ksplit < 1 || (int64_t)chunks * ksplit > 65535) return hipErrorInvalidValue;
     const dim3 grid((tiles + kWaves - 1) / kWaves, slots, ksplit * chunks);
-    if (p16)
-        hipLaunchKernelGGL(k_mfma_down_q6<true>, grid, dim3(256), 0, st, down, estride, h16,
-                           dev_slots(sa), d, F, ksplit, Y, split_stride);
-    else
-        hipLaunchKernelGGL(k_mfma_down_q6<false>, grid, dim3(256), 0, st, down, estride, h16,
-                           dev_slots(sa), d, F, ksplit, Y, split_stride);
+    auto *kern = p16 ? (h_lo ? k_mfma_down_q6<true, true> : k_mfma_down_q6<true, false>)
+                     : (h_lo ? k_mfma_down_q6<false, true> : k_mfma_down_q6<false, false>);
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, down, estride, h16, dev_slots(sa), d, F,
+                       ksplit, Y, split_stride);
     return hipGetLastError();
 }
 
@@ -1328,17 +1337,15 @@ hipError_t launch_mfma_gateup(const uint8_t *gate, const uint8_t *up, int64_t es
 hipError_t launch_mfma_down(const uint8_t *down, int64_t estride, const _Float16 *h16,
                             const _Float16 *hs, const SlotArgsHost &sa, int slots, int chunks,
                             int d, int F, int ksplit, float *Y, int64_t split_stride,
-                            hipStream_t st) {
+                            hipStream_t st, bool h_lo) {
     const int tiles = d / 64;
     if (chunks < 1 || ksplit < 1 || (int64_t)chunks * ksplit > 65535) return hipErrorInvalidValue;
     if (F % 128) return hipErrorInvalidValue;
     const dim3 grid((tiles + kWaves - 1) / kWaves, slots, ksplit * chunks);
-    if (F % 256)
-        hipLaunchKernelGGL(k_mfma_down<true>, grid, dim3(256), 0, st, down, estride, h16, hs,
-                           dev_slots(sa), d, F, ksplit, Y, split_stride);
-    else
-        hipLaunchKernelGGL(k_mfma_down<false>, grid, dim3(256), 0, st, down, estride, h16, hs,
-                           dev_slots(sa), d, F, ksplit, Y, split_stride);
+    auto *kern = F % 256 ? (h_lo ? k_mfma_down<true, true> : k_mfma_down<true, false>)
+                         : (h_lo ? k_mfma_down<false, true> : k_mfma_down<false, false>);
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, down, estride, h16, hs, dev_slots(sa), d, F,
+                       ksplit, Y, split_stride);
     return hipGetLastError();
 }
 

@@ -543,13 +543,13 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
     HIP_TRY(timed(h, st, shared || fused_only ? kSlotDownSh : kSlotDown, [&] {
         if (s.q6_dn && pl.mfma)  // 16-token passes while slots average at most 16 tokens
             return launch_mfma_down_q6(s.down, s.sz_dn, s.h16, sa, slots, pl.chunks, d, s.F,
-                                       pl.ks, s.Y, s.positions * d, st, pl.per_slot <= 16);
+                                       pl.ks, s.Y, s.positions * d, st, pl.per_slot <= 16, h->x_lo);
         if (s.q6_dn || s.q8 || (s.split_dn && !pl.mfma))
             return launch_rpl_down(s.down, s.sz_dn, s.hh, s.hl, s.hs, s.hm, sa, slots, d, s.F,
                                    pl.ks, s.Y, s.positions * d, st, s.q8 ? 2 : s.split_dn ? 3 : 1);
         if (s.split_dn || (s.rpl_dn && pl.mfma))
             return launch_mfma_down(s.down, s.sz_dn, s.h16, s.h16s, sa, slots, pl.chunks, d,
-                                    s.F, pl.ks, s.Y, s.positions * d, st);
+                                    s.F, pl.ks, s.Y, s.positions * d, st, h->x_lo);
         if (s.rpl_dn)
             return launch_rpl_down(s.down, s.sz_dn, s.hh, s.hl, s.hs, s.hm, sa, slots, d, s.F,
                                    pl.ks, s.Y, s.positions * d, st);
