@@ -10,7 +10,9 @@ import ctypes as C
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "liblcmoe.so")
+# LCMOE_LIB names another build of the same library (e.g. a variant being
+# timed); the default is the in-tree build
+LIB_PATH = os.environ.get("LCMOE_LIB") or os.path.join(_HERE, "liblcmoe.so")
 
 TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 0, 8, 12, 14
 TYPE_Q4_0 = 2  # lcmoe_shard_matmul only: the shard engine's interleaved Q4_0

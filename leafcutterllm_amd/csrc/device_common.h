@@ -248,9 +248,17 @@ __device__ __forceinline__ uint32_t ord_key(float f) {
 // Matrix-core activation format of one 32-column sub-block sbi of row t
 // (row width d, a multiple of 256): the f16 hi = f16(v) and lo = f16(v - hi)
 // halves at columns 32 (sbi % 8) .. +31 of the row's super-block piece sbi / 8
-// (hi[256] then lo[256]), and the sub-block's sum of (hi + lo) -- of hi
+// (hi[256] then lo[256], columns at act16_pos), and the sub-block's sum of (hi + lo) -- of hi
 // alone when !lo, for products that take only the hi halves -- added in
 // column order, as a (hi, lo) pair.  v: the 32 values, 16-byte aligned.
+// Position of column c (0..255) inside its piece of the matrix-core
+// activation format: columns are stored permuted within each group of four
+// as (c0, c2, c1, c3), the order in which one and-or pulls two nibbles out of
+// a packed weight word as f16 magic values (bytes 0 and 2, then 1 and 3).
+// The permutation is applied to both operands of every product, so the sums
+// are unchanged.
+__device__ __forceinline__ int act16_pos(int c) { return (c & ~3) | ((c & 1) << 1) | ((c >> 1) & 1); }
+
 __device__ inline void act16_subblock(const float *v, int64_t t, int d, int sbi,
                                       _Float16 *__restrict__ x16, _Float16 *__restrict__ xs,
                                       bool lo_sum = true) {
@@ -268,8 +276,8 @@ __device__ inline void act16_subblock(const float *v, int64_t t, int d, int sbi,
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const _Float16 hi = (_Float16)f[i], lo = (_Float16)(f[i] - (float)hi);
-            hv[i] = hi;
-            lv[i] = lo;
+            hv[act16_pos(i)] = hi;
+            lv[act16_pos(i)] = lo;
             sum = sum + (lo_sum ? (float)hi + (float)lo : (float)hi);
         }
         oh[g] = hv;

@@ -89,23 +89,12 @@ __device__ __forceinline__ half2v magic2(uint32_t w, uint32_t sel) {
 }
 constexpr uint32_t kSel01 = 0x04010400u;  // bytes 0, 1
 constexpr uint32_t kSel23 = 0x04030402u;  // bytes 2, 3
+constexpr uint32_t kSel02 = 0x04020400u;  // bytes 0, 2
+constexpr uint32_t kSel13 = 0x04030401u;  // bytes 1, 3
 constexpr uint32_t kSel00 = 0x04000400u;  // byte 0 twice
 constexpr uint32_t kSel11 = 0x04010401u;
 constexpr uint32_t kSel22 = 0x04020402u;
 constexpr uint32_t kSel33 = 0x04030403u;
-
-// 8 masked bytes b (one per byte of w0, w1) -> 8 f16 values (1024 + b) * sc2 + c2,
-// natural column order
-__device__ __forceinline__ half8 dec8(uint32_t w0, uint32_t w1, half2v sc2, half2v c2) {
-    const half2v p0 = __builtin_elementwise_fma(magic2(w0, kSel01), sc2, c2);
-    const half2v p1 = __builtin_elementwise_fma(magic2(w0, kSel23), sc2, c2);
-    const half2v p2 = __builtin_elementwise_fma(magic2(w1, kSel01), sc2, c2);
-    const half2v p3 = __builtin_elementwise_fma(magic2(w1, kSel23), sc2, c2);
-    half8 r;
-    r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
-    r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
-    return r;
-}
 
 // Per-row super-block header (d, dmin, 12 packed scale bytes) unpacked;
 // d2, dmin2: the scales of sub-blocks 4-7 in the split layout.
@@ -149,14 +138,41 @@ __device__ __forceinline__ void pair_scales(const Hdr &s, int p, half2v &s2, hal
     c2 = s2 * half2v{(_Float16)-1024.0f, (_Float16)-1024.0f};
 }
 
+// Two f16 magic values from the nibbles of bytes 0 and 2 of w, one and-or:
+// the low nibbles (mask 0x000F000F) as 1024 + q, the high ones (0x00F000F0)
+// as 1024 + 16 q
+// mg: kMagicH held in a vector register (magic_reg()), so that the and-or
+// takes the mask as its one constant operand
+constexpr uint32_t kMagicH = 0x64006400u;
+__device__ __forceinline__ half2v nib2(uint32_t w, uint32_t mask, uint32_t mg) {
+    return as_h2((w & mask) | mg);
+}
+__device__ __forceinline__ uint32_t magic_reg() {
+    uint32_t mg = kMagicH;
+    asm volatile("" : "+v"(mg));
+    return mg;
+}
+
 // B operands (sc*q, 8 columns each) of pair p's two sub-blocks from one
-// lane's 8 qs bytes w0, w1
+// lane's 8 qs bytes w0, w1 (bytes j = columns j), in the activation format's
+// column order (act16_pos): bytes 0, 2, 1, 3, 4, 6, 5, 7.  Per pair of
+// weights one and-or and one packed fma; the shifted words w >> 8 bring
+// bytes 1 and 3 down to the places of 0 and 2.
 __device__ __forceinline__ void dec_pair(const Hdr &s, int p, uint32_t w0, uint32_t w1,
-                                         half8 &blo, half8 &bhi) {
+                                         uint32_t mg, half8 &blo, half8 &bhi) {
     half2v s2, c2;
     pair_scales(s, p, s2, c2);
-    blo = dec8(w0 & 0x0F0F0F0Fu, w1 & 0x0F0F0F0Fu, half2v{s2[0], s2[0]}, half2v{c2[0], c2[0]});
-    bhi = dec8(w0 & 0xF0F0F0F0u, w1 & 0xF0F0F0F0u, half2v{s2[1], s2[1]}, half2v{c2[1], c2[1]});
+    const uint32_t w[4] = {w0, w0 >> 8, w1, w1 >> 8};
+    const half2v sl{s2[0], s2[0]}, cl{c2[0], c2[0]}, sh{s2[1], s2[1]}, ch{c2[1], c2[1]};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const half2v a = __builtin_elementwise_fma(nib2(w[i], 0x000F000Fu, mg), sl, cl);
+        const half2v b = __builtin_elementwise_fma(nib2(w[i], 0x00F000F0u, mg), sh, ch);
+        blo[2 * i] = a[0];
+        blo[2 * i + 1] = a[1];
+        bhi[2 * i] = b[0];
+        bhi[2 * i + 1] = b[1];
+    }
 }
 
 // B operand of the min MFMA: (m_j, m_j) for sub-blocks j = 4h .. 4h+3
@@ -316,12 +332,12 @@ __device__ __forceinline__ void read_a(AUnit &a, const uint8_t *tokrow, int u, i
 // 2p+1 (high nibbles), four MFMAs per matrix (two without lo halves).
 template <int MATS, bool LO = true>
 __device__ __forceinline__ void unit_mfma(const WRaw (&w)[MATS], const Hdr (&hd)[MATS], int u,
-                                          const AUnit &a, float16v (&S)[MATS]) {
+                                          const AUnit &a, uint32_t mg, float16v (&S)[MATS]) {
     const int p = u >> 1;
 #pragma unroll
     for (int m = 0; m < MATS; m++) {
         half8 blo, bhi;
-        dec_pair(hd[m], p, w[m].q[u].x, w[m].q[u].y, blo, bhi);
+        dec_pair(hd[m], p, w[m].q[u].x, w[m].q[u].y, mg, blo, bhi);
         S[m] = mfma32(a.h0, blo, S[m]);
         if constexpr (LO) S[m] = mfma32(a.l0, blo, S[m]);
         S[m] = mfma32(a.h1, bhi, S[m]);
@@ -403,10 +419,11 @@ __device__ __forceinline__ void step(g_u8 *const (&wb)[MATS], uint32_t lo,
     const half8 *aminp = reinterpret_cast<const half8 *>(cur + kSumsOffT<LO> + r * 32 + 16 * h);
     AUnit a[2];  // unit u's operands, and unit u+1's read ahead
     read_a<LO>(a[0], tokrow, 0, h);
+    const uint32_t mg = magic_reg();
 #pragma unroll
     for (int u = 0; u < 8; u++) {
         if (u + 1 < 8) read_a<LO>(a[(u + 1) & 1], tokrow, u + 1, h);
-        unit_mfma<MATS, LO>(w, hd, u, a[u & 1], S);
+        unit_mfma<MATS, LO>(w, hd, u, a[u & 1], mg, S);
 #pragma unroll
         for (int m = 0; m < MATS; m++) w[m].q[u] = load_q<SPLIT>(wb[m], lo, kn, 1 + u, 8 * h);
         if (SPLIT && u == 3) {  // sub-blocks 0-3 done: their own d
@@ -559,6 +576,7 @@ __device__ __forceinline__ void step16(g_u8 *const (&wb)[MATS], uint32_t lo,
     const half4 *aminp = reinterpret_cast<const half4 *>(cur + kSumsOffT<LO> + r16 * 32 + 8 * c4);
     AUnit a[2];  // pair p's operands, and pair p+1's read ahead
     read_a16<LO>(a[0], tokrow, 0, c4);
+    const uint32_t mg = magic_reg();
 #pragma unroll
     for (int p = 0; p < 4; p++) {
         if (p + 1 < 4) read_a16<LO>(a[(p + 1) & 1], tokrow, p + 1, c4);
@@ -568,7 +586,7 @@ __device__ __forceinline__ void step16(g_u8 *const (&wb)[MATS], uint32_t lo,
 #pragma unroll
             for (int t = 0; t < 2; t++) {
                 half8 blo, bhi;
-                dec_pair(hd[m][t], p, w[m].q[p][t].x, w[m].q[p][t].y, blo, bhi);
+                dec_pair(hd[m][t], p, w[m].q[p][t].x, w[m].q[p][t].y, mg, blo, bhi);
                 w[m].q[p][t] = load_q16<SPLIT>(wb[m], lo, kn, p, t, c4);
                 S[m][t] = mfma16(h0, blo, S[m][t]);
                 if constexpr (LO) S[m][t] = mfma16(l0, blo, S[m][t]);
@@ -720,7 +738,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
                         const int ft = fb + 16 * t;
                         if (hf) hf[p * F + ft] = v[t];
                         if (h16) {
-                            _Float16 *piece = h16 + (p * nkb + (ft >> 8)) * 512 + (ft & 255);
+                            _Float16 *piece = h16 + (p * nkb + (ft >> 8)) * 512 + act16_pos(ft & 255);
                             piece[0] = hi[t];
                             if (LO) piece[256] = lo[t];
                         }
@@ -754,7 +772,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_gateup(
                 const int64_t p = p0 + q;
                 if (hf) hf[p * F + fo] = v;
                 if (h16) {
-                    _Float16 *piece = h16 + (p * nkb + (fo >> 8)) * 512 + (fo & 255);
+                    _Float16 *piece = h16 + (p * nkb + (fo >> 8)) * 512 + act16_pos(fo & 255);
                     piece[0] = hi;
                     if (LO) piece[256] = lo;
                     if (r == 0) {
@@ -928,8 +946,9 @@ __device__ __forceinline__ half2v magic_bb(uint32_t w, int b) {
 // (1024 + q) s - 1056 s, one rounding of an exact integer result
 __device__ __forceinline__ void dec6(uint32_t g0, uint32_t g1, half2v sh2, half2v c1, half2v sl2,
                                      half2v c2, half8 &b1, half8 &b2) {
-    const half2v m[4] = {magic2(g0, kSel01), magic2(g0, kSel23), magic2(g1, kSel01),
-                         magic2(g1, kSel23)};
+    // the activation format's column order (act16_pos): bytes 0, 2, 1, 3, ...
+    const half2v m[4] = {magic2(g0, kSel02), magic2(g0, kSel13), magic2(g1, kSel02),
+                         magic2(g1, kSel13)};
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const half2v x = __builtin_elementwise_fma(m[k], sh2, c1);

@@ -612,8 +612,8 @@ __device__ void quantise_token(const RouterArgs &a, int t, float *s_x, int share
             for (int i = 0; i < 8; i++) {
                 const _Float16 hi = (_Float16)f[i];
                 const _Float16 lo = (_Float16)(f[i] - (float)hi);
-                hv[i] = hi;
-                lv[i] = lo;
+                hv[act16_pos(i)] = hi;  // the format's column order
+                lv[act16_pos(i)] = lo;
                 // the sum of what the products take: hi + lo, or hi alone
                 sum = sum + (a.x16_lo ? (float)hi + (float)lo : (float)hi);
             }

@@ -460,7 +460,7 @@ __device__ __forceinline__ void gateup_chunk(const uint4 *G, const uint4 *U, int
             float part = (float)hi + (float)lo;
 #pragma unroll
             for (int off = 1; off < 32; off <<= 1) part += __shfl_xor(part, off, 64);
-            _Float16 *piece = out.h16 + (p * nkb + (f >> 8)) * 512 + (f & 255);
+            _Float16 *piece = out.h16 + (p * nkb + (f >> 8)) * 512 + act16_pos(f & 255);
             piece[0] = hi;
             piece[256] = lo;
             if ((lane & 31) == 0) {
