@@ -1205,10 +1205,13 @@ __device__ __forceinline__ void block_pass16_q6(g_u8 *wb, const uint32_t (&lo)[2
         step16_q6<LO>(wb, lo, rlo, dlo, kb, s_stage0, s_stage1, src, w, acc, wave, lane);
 }
 
-// grid (d/256 row blocks, slots, ksplit x pass groups), as k_mfma_down.  P16:
-// passes of 16 tokens (16x16x32 MFMAs), else of 32 (32x32x16); one kind per
-// kernel keeps each within the register file.
-template <bool P16, bool LO>
+// grid (d/256 row blocks, slots, ksplit x pass groups), as k_mfma_down.
+// PASS 0: each slot takes passes of 32 tokens (32x32x16 MFMAs: one decode
+// per weight for up to 32 tokens) while more than 16 remain, the rest as
+// one pass of up to 16 (16x16x32 MFMAs: half the matrix-core work).  With
+// two f16 per activation that kernel outgrows the register file, so LO
+// takes one kind per kernel: PASS 16 or 32.
+template <bool LO, int PASS>
 __global__ __launch_bounds__(256, 2) void k_mfma_down_q6(
     const uint8_t *__restrict__ down, int64_t estride, const _Float16 *__restrict__ h16,
     SlotArgs sa, int d, int F, int ksplit, float *__restrict__ Y, int64_t split_stride) {
@@ -1240,7 +1243,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down_q6(
     const uint32_t dlo[2] = {(uint32_t)r * 2, (uint32_t)(32 + r) * 2};
     float *Yz = Y + (int64_t)bz * split_stride;
     const uint8_t *hb = reinterpret_cast<const uint8_t *>(h16);
-    constexpr int kPass = P16 ? 16 : kTok;
+    constexpr int kPass = PASS == 16 ? 16 : kTok;
     for (int c = cz * kPass; c < n; c += nz * kPass) {
         StageSrc src;
 #pragma unroll
@@ -1249,7 +1252,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down_q6(
         // the sums are not used (Q6_K has no mins): stage a valid row
         src.sums = uniform(hb);
         src.soff = 16 * (uint32_t)lane;
-        if constexpr (P16) {
+        if (PASS == 16 || (PASS == 0 && n - c <= 16)) {
             const int r16 = lane & 15, c4 = lane >> 4;
             uint32_t lo16[2][2], rlo16[2][2], dlo16[2][2];
 #pragma unroll
@@ -1277,7 +1280,7 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down_q6(
                         for (int t = 0; t < 2; t++) yrow[32 * m + 16 * t] = acc[m][t][i];
                 }
             }
-        } else {
+        } else if constexpr (PASS != 16) {
         float16v acc[2] = {float16v{}, float16v{}};
         block_pass_q6<LO>(wb, lo, rlo, dlo, kb0, kb1, src, acc);
         if (tile0 >= ntile) continue;
@@ -1316,12 +1319,12 @@ SlotArgs dev_slots(const SlotArgsHost &s) {
 hipError_t launch_mfma_down_q6(const uint8_t *down, int64_t estride, const _Float16 *h16,
                                const SlotArgsHost &sa, int slots, int chunks, int d, int F,
                                int ksplit, float *Y, int64_t split_stride, hipStream_t st,
-                               bool p16, bool h_lo) {
+                               bool h_lo, bool p16) {
     const int tiles = d / 64;
     if (chunks < 1 || ksplit < 1 || (int64_t)chunks * ksplit > 65535) return hipErrorInvalidValue;
     const dim3 grid((tiles + kWaves - 1) / kWaves, slots, ksplit * chunks);
-    auto *kern = p16 ? (h_lo ? k_mfma_down_q6<true, true> : k_mfma_down_q6<true, false>)
-                     : (h_lo ? k_mfma_down_q6<false, true> : k_mfma_down_q6<false, false>);
+    auto *kern = !h_lo ? k_mfma_down_q6<false, 0>
+                       : p16 ? k_mfma_down_q6<true, 16> : k_mfma_down_q6<true, 32>;
     hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, down, estride, h16, dev_slots(sa), d, F,
                        ksplit, Y, split_stride);
     return hipGetLastError();

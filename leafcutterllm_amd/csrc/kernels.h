@@ -134,12 +134,13 @@ hipError_t launch_mfma_down(const uint8_t *down, int64_t estride, const _Float16
                             int d, int F, int ksplit, float *Y, int64_t split_stride,
                             hipStream_t st, bool h_lo = true);
 // The same down product for Q6_K weights in the RPL64 Q6_K layout (H as f16
-// pieces, no sums needed), in passes of 16 tokens (p16) or 32.  h_lo: H
-// enters as two f16 (hi + lo), else as its hi halves (and sums of hi).
+// pieces, no sums needed).  h_lo: H enters as two f16 (hi + lo), in passes
+// of 16 tokens (p16) or 32; without it as its hi halves, each slot in passes
+// of 32 tokens and a last one of at most 16.
 hipError_t launch_mfma_down_q6(const uint8_t *down, int64_t estride, const _Float16 *h16,
                                const SlotArgsHost &sa, int slots, int chunks, int d, int F,
                                int ksplit, float *Y, int64_t split_stride, hipStream_t st,
-                               bool p16, bool h_lo);
+                               bool h_lo, bool p16);
 
 // Routing weights computed by the combine from exact logits (fast-router
 // path); logits == null: the weights are already in topk_w.

@@ -541,9 +541,16 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
                                      s.Hf, nullptr, nullptr, nullptr, nullptr, ch, st);
     }));
     HIP_TRY(timed(h, st, shared || fused_only ? kSlotDownSh : kSlotDown, [&] {
-        if (s.q6_dn && pl.mfma)  // 16-token passes while slots average at most 16 tokens
+        // Q6_K: each expert's passes sized by its own token count (32-token
+        // passes decode each weight once for up to 32 tokens, a 16-token one
+        // does half the matrix-core work; config 4 T = 256, where the 136
+        // touched experts hold 15 tokens on average and the busiest dozens:
+        // down 876 us with 16-token passes, 717 with 32-token passes); with
+        // two f16 per activation one pass size per launch, by the average
+        if (s.q6_dn && pl.mfma)
             return launch_mfma_down_q6(s.down, s.sz_dn, s.h16, sa, slots, pl.chunks, d, s.F,
-                                       pl.ks, s.Y, s.positions * d, st, pl.per_slot <= 16, h->x_lo);
+                                       pl.ks, s.Y, s.positions * d, st, h->x_lo,
+                                       pl.per_slot <= 16);
         if (s.q6_dn || s.q8 || (s.split_dn && !pl.mfma))
             return launch_rpl_down(s.down, s.sz_dn, s.hh, s.hl, s.hs, s.hm, sa, slots, d, s.F,
                                    pl.ks, s.Y, s.positions * d, st, s.q8 ? 2 : s.split_dn ? 3 : 1);
