@@ -146,7 +146,8 @@ lcmoe_status lcmoe_forward_dev(lcmoe_handle *h, const float *x_dev, int32_t T, f
                                void *stream);
 
 /* Activation operands of the matrix-core expert products (batches where
- * the experts see more tokens than there are experts: T*K > E; prefill).
+ * the experts see more tokens than there are experts, T*K > E, or T >= 4;
+ * prefill).
  * The weights are always exact (sc*q in f16, scales in f32) and the sums
  * f32; the mode sets how x enters the gate/up products and H the down
  * products:

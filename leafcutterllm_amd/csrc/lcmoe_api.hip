@@ -479,11 +479,13 @@ static Plan plan_set(lcmoe_handle *h, const ExpertSet &s, bool shared, int T, in
     // the matrix-core kernels decode each weight once for up to 32 tokens,
     // the row-per-lane ones once per pass of up to 4 tokens: matrix cores
     // when there are more assignments than experts (T K > E; a shared expert
-    // sees every token, so T > 1).  Measured at the boundary T K = E: config 2
-    // T = 4 runs 141 us row-per-lane against 148 us, config 4 T = 32 1.01 ms
-    // against 1.17 ms.
+    // sees every token, so T > 1), and from 4 tokens on.  Measured with one
+    // f16 per activation (tokens/s, row-per-lane against matrix cores):
+    // config 4 T = 2 / 4 / 16 / 32: 12.0k / 16.1k / 26.8k / 32.5k against
+    // 11.5k / 19.0k / 34.1k / 53.1k; config 2 T = 3 / 4: 25.7k / 28.5k
+    // against 22.2k / 28.4k; config 5's layer T = 4: 54.0k against 60.2k.
     const int64_t assign = shared ? T : (int64_t)T * D.n_expert_used;
-    p.mfma = s.rpl_gu && assign > (shared ? 1 : (int64_t)D.n_expert);
+    p.mfma = s.rpl_gu && (shared ? assign > 1 : (assign > (int64_t)D.n_expert || T >= 4));
     // passes per slot: all T tokens for a shared expert, the average over
     // the touched experts for the routed ones (busier experts run several
     // passes per block)
