@@ -22,6 +22,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16 matrix peak
+FP32_PEAK_TFLOPS = 157.3  # MI355X fp32 (vector) peak
 MALL_BYTES = 256 << 20
 
 
@@ -111,10 +112,26 @@ def layer_flops(cfg, T):
             + 6 * cfg.d_model * cfg.d_ff_shared * T * cfg.n_shared)
 
 
+# sources of the matrix-core expert kernels: a traffic figure measured on
+# other sources is stale
+TRAFFIC_SOURCES = ("leafcutterllm_amd/csrc/kern_mfma.hip", "leafcutterllm_amd/csrc/device_common.h",
+                   "leafcutterllm_amd/csrc/chains.h", "leafcutterllm_amd/csrc/lcmoe_api.hip")
+
+
+def kernel_source_stamp() -> str:
+    import hashlib
+    h = hashlib.sha256()
+    for rel in TRAFFIC_SOURCES:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic(config: int, tokens: int):
     """HBM bytes per gate/up launch from the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE passes (profiles/traffic.json, calibrated by a plain copy), when
-    they were taken on this workload; None otherwise."""
+    they were taken on this workload and on the kernel sources of this tree
+    (their stamp); None otherwise."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
@@ -122,6 +139,8 @@ def measured_traffic(config: int, tokens: int):
     except (OSError, ValueError):
         return None
     if t.get("workload") != f"config {config}, T={tokens}":
+        return None
+    if t.get("source_stamp") != kernel_source_stamp():
         return None
     return int(t["bytes"])
 
@@ -195,6 +214,58 @@ def shard_matmul_bench(args) -> None:
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                      "algorithmic_bytes": alg},
+    }))
+
+
+def matmul_f32_bench(args) -> None:
+    """Times Backend::matmul's HIP replacement (lcmoe_matmul_f32_dev, the x86
+    CpuBackend's per-output order, bit for bit) on resident device buffers:
+    HIP events around `steps` launches, B cycled through replicas past the
+    MALL.  Each output is one k-long chain of dependent fused multiply-adds
+    in k order, so besides HBM bytes and fp32 flops the bound is that chain:
+    k steps of the dependent-FMA latency, measured at about 2.7 ns per step
+    (a one-wave clock64 probe, 4096 steps in ~11 us)."""
+    import numpy as np
+
+    from leafcutterllm_amd import hip
+    from leafcutterllm_amd._lib import check
+    import leafcutterllm_amd as L
+
+    m, k, n = (int(v) for v in args.matmul_f32.split(","))
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    R = max(2, -(-2 * MALL_BYTES // b.nbytes) + 1)
+    dbs = [hip.DeviceBuffer(b.nbytes).upload(b) for _ in range(R)]
+    da, dc = hip.DeviceBuffer(a.nbytes).upload(a), hip.DeviceBuffer(4 * m * n)
+    st = hip.Stream()
+
+    def launch(i):
+        check(L.lib().lcmoe_matmul_f32_dev(da.ptr, dbs[i % R].ptr, dc.ptr, m, k, n, st.ptr),
+              "lcmoe_matmul_f32_dev")
+
+    for i in range(args.warmup):
+        launch(i)
+    st.synchronize()
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record(st)
+    for i in range(args.steps):
+        launch(i)
+    e1.record(st)
+    ms = e0.elapsed_ms(e1) / args.steps
+    alg = a.nbytes + b.nbytes + 4 * m * n
+    tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    chain_us = k * 2.7e-3
+    gbs = alg / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "Backend::matmul (f32, CPU-backend order) time", "value": round(ms * 1e3, 3),
+        "unit": "us", "higher_is_better": False, "steps": args.steps, "warmup": args.warmup,
+        "dtype": "f32 (fused multiply-add chains in k order, bit-identical to the x86 CpuBackend)",
+        "config": {"workload": f"lcmoe_matmul_f32_dev m={m} k={k} n={n}", "replicas": R},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": alg},
+        "fp32_TFLOPs": round(tflops, 3), "fp32_frac": round(tflops / FP32_PEAK_TFLOPS, 4),
+        "chain_floor_us": round(chain_us, 2), "frac_of_chain_floor": round(chain_us / (ms * 1e3), 4),
     }))
 
 
@@ -296,6 +367,8 @@ def main():
                     help="only run device-to-device copies of this size (FETCH_SIZE calibration)")
     ap.add_argument("--shard-matmul", default="", metavar="TYPE,M,K,N",
                     help="only time lcmoe_shard_matmul_dev (TYPE q8 or q4) on one shape")
+    ap.add_argument("--matmul-f32", default="", metavar="M,K,N",
+                    help="only time lcmoe_matmul_f32_dev (Backend::matmul) on one shape")
     ap.add_argument("--shard-split", type=int, default=1, metavar="S",
                     help="with --shard-matmul: time lcmoe_shard_matmul_split_dev with S k-slices")
     ap.add_argument("--e2e-batches", default="1,16",
@@ -318,6 +391,9 @@ def main():
         return
     if args.shard_matmul:
         shard_matmul_bench(args)
+        return
+    if args.matmul_f32:
+        matmul_f32_bench(args)
         return
 
     if args.config == 5 and args.gpus == 1 and not args.layer:
@@ -464,7 +540,9 @@ def main():
             "unit": "GB/s",
             "frac": round(head["gateup_GBps"] / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(args.config, args.tokens),
-            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
+            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated, "
+                            "profiles/traffic.json; null when measured on other kernel sources)",
+            "kernel_source_stamp": kernel_source_stamp(),
             "algorithmic_bytes": round(head["gateup_bytes"]),
         }
     qdesc = qname[cfg.qtype_gate] + ("" if cfg.qtype_down == cfg.qtype_gate
@@ -487,9 +565,10 @@ def main():
         "dtype": (("f32 in/out; expert products exact int8 dot4 of the Q8_0 weights with "
                    "15-bit two-limb activations at every T; f32 accumulate")
                   if cfg.qtype_gate == L.TYPE_Q8_0 else
-                  ("f32 in/out; expert products on exact weights (f16 sc*q) with f16 hi+lo "
-                   "activations (~22 bits) on MFMA when T*K > E, exact int8 dot4 on 15-bit "
-                   "two-limb activations when T*K <= E; f32 accumulate")),
+                  ("f32 in/out; expert products on exact weights (f16 sc*q, f32 scales) with "
+                   "one f16 per activation (x and H) on MFMA when T >= 4 or T*K > E "
+                   "(LCMOE_ACT_F16, the default: layer rel-L2 3.6e-4 vs the reference CPU path), "
+                   "exact int8 dot4 on 15-bit two-limb activations below; f32 accumulate")),
         "data": ("synthetic (seeded splitmix64 N(0,1) activations, N(0,0.02) weights quantised "
                  f"to {qdesc})"),
         "config": {
