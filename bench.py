@@ -118,12 +118,21 @@ TRAFFIC_SOURCES = ("leafcutterllm_amd/csrc/kern_mfma.hip", "leafcutterllm_amd/cs
                    "leafcutterllm_amd/csrc/chains.h", "leafcutterllm_amd/csrc/lcmoe_api.hip")
 
 
+def _code_tokens(text: str) -> str:
+    """The source without comments and whitespace: edits to comments leave
+    the stamp unchanged, any change to the code changes it."""
+    import re
+    text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", " ", text)
+    return "".join(text.split())
+
+
 def kernel_source_stamp() -> str:
     import hashlib
     h = hashlib.sha256()
     for rel in TRAFFIC_SOURCES:
-        with open(os.path.join(ROOT, rel), "rb") as f:
-            h.update(f.read())
+        with open(os.path.join(ROOT, rel), encoding="utf-8") as f:
+            h.update(_code_tokens(f.read()).encode())
     return h.hexdigest()[:16]
 
 

@@ -12,19 +12,21 @@
 //
 // Exact operands: B = sc_j * q (6-bit * 4-bit integers, exact in f16), built
 // from the nibbles as the f16 bit pattern 0x6400 | q = 1024 + q and one
-// packed-f16 fma (1024+q)*sc - 1024*sc.  Activations enter as two f16 halves
-// hi + lo (lo = v - hi rounded again), about 22 significant bits.  Per
+// packed-f16 fma (1024+q)*sc - 1024*sc.  Activations enter as one f16 per
+// element (LO = false, the default mode) or as two f16 halves hi + lo
+// (lo = v - hi rounded again, about 22 significant bits).  Per
 // super-block
 //   sum_k w_k v_k = d * sum_k (sc*q)_k v_k - dmin * sum_j m_j * V_j
 // with V_j the sub-block sums of v; the second sum is one more MFMA whose 16
-// input columns are (sub-block, half).
+// input columns are (sub-block, half), V_j the sums of what the products take.
 //
 // Work split: a wave owns 32 weight rows and ALL tokens of its expert (32 per
-// pass), so every weight byte is read and decoded once per 32 tokens.  Waves
-// are independent (no barriers); four consecutive row groups of one expert
-// form a block so that their activation reads share the CU's L1.  The next
-// super-block's weights are loaded into registers while the current one is
-// computed, and each activation unit one step ahead.
+// pass), so every weight byte is read and decoded once per 32 tokens.  Four
+// consecutive row groups of one expert form a block: they stage each
+// super-block's activations in LDS together and meet at one barrier per
+// super-block step.  The next super-block's weights are loaded into
+// registers while the current one is computed, and each activation unit one
+// step ahead.
 
 #include "device_common.h"
 #include "kernels.h"
