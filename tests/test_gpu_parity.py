@@ -88,6 +88,12 @@ SMALL = {
     # more than 8 experts per token: the combine's loop form
     "k12-shared": small_config(
         "k12", 256, 256, 32, 12, L.ROUTE_SOFTMAX_RENORM, Q4, Q4, n_shared=1, d_ff_shared=256),
+    # E % 8 == 4 past 64 experts: at T * E * d > 2^25 the chain router's
+    # streaming logits product, with its own block of tail columns
+    "e68-chain": small_config("e68", 512, 256, 68, 4, L.ROUTE_SOFTMAX, Q4, Q4),
+    "sig64-chain": small_config(
+        "sig64", 512, 256, 64, 4, L.ROUTE_SIGMOID_GROUP, Q4, Q6, n_group=8, topk_group=4,
+        routed_scale=2.5, bias="normal0.1"),
 }
 
 
@@ -102,10 +108,13 @@ def test_small_layer_parity(name, T):
 
 
 @pytest.mark.parametrize("name,T", [("q6k-down-e16", 160), ("q4k-split-shared", 200),
-                                    ("sigmoid-group-q6k", 300)])
+                                    ("sigmoid-group-q6k", 300), ("e68-chain", 1000),
+                                    ("sig64-chain", 1100)])
 def test_small_layer_parity_many_tokens(name, T):
     """Tens of tokens per expert: 32-token matrix-core passes (Q6_K, split
-    Q4_K), several pass groups per slot and prefill-style shared launches."""
+    Q4_K), several pass groups per slot and prefill-style shared launches;
+    the last two run the chain router (exact logits of every token and
+    expert, T * E * d > 2^25)."""
     cfg = SMALL[name]
     layer = L.synth_layer(cfg, seed=5)
     x = L.synth_x(cfg, T, seed=5, index=T)
