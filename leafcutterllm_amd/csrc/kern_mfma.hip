@@ -803,14 +803,16 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down(
     // Workgroups go to the 8 XCDs round-robin in dispatch order and each XCD
     // has its own L2.  Every (slot, split) pair reads one slice of H, shared
     // by its row blocks: remap the grid so that each XCD runs whole pairs and
-    // keeps only its pairs' slices (identity when the grid does not divide).
+    // keeps only its pairs' slices.  Pair p goes to XCD p % 8, so the pairs of
+    // slot rows that exit at once (pass slots past the realised count) spread
+    // over the XCDs (identity when the pair count is not a multiple of 8).
     int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
     {
-        const int nx = gridDim.x, ny = gridDim.y, total = nx * ny * gridDim.z;
-        const int id = bx + nx * (by + ny * bz), per = total / kXcds;
-        if (total % kXcds == 0 && per % nx == 0) {
-            const int q = (id % kXcds) * per + id / kXcds, pair = q / nx;
-            bx = q % nx;
+        const int nx = gridDim.x, ny = gridDim.y;
+        const int id = bx + nx * (by + ny * bz), pairs = ny * gridDim.z;
+        if (pairs % kXcds == 0) {  // pair p on XCD p % 8, all of its row blocks
+            const int j = id / kXcds, pair = id % kXcds + kXcds * (j / nx);
+            bx = j % nx;
             by = pair % ny;
             bz = pair / ny;
         }
@@ -1219,11 +1221,11 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down_q6(
     SlotArgs sa, int d, int F, int ksplit, float *__restrict__ Y, int64_t split_stride) {
     int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
     {
-        const int nx = gridDim.x, ny = gridDim.y, total = nx * ny * gridDim.z;
-        const int id = bx + nx * (by + ny * bz), per = total / kXcds;
-        if (total % kXcds == 0 && per % nx == 0) {
-            const int q = (id % kXcds) * per + id / kXcds, pair = q / nx;
-            bx = q % nx;
+        const int nx = gridDim.x, ny = gridDim.y;
+        const int id = bx + nx * (by + ny * bz), pairs = ny * gridDim.z;
+        if (pairs % kXcds == 0) {  // pair p on XCD p % 8, all of its row blocks
+            const int j = id / kXcds, pair = id % kXcds + kXcds * (j / nx);
+            bx = j % nx;
             by = pair % ny;
             bz = pair / ny;
         }

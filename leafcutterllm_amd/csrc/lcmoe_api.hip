@@ -464,9 +464,6 @@ struct Plan {
     int chunks;  // blocks sharing one matrix-core slot's 32-token passes
     int sl, ns;  // fused shared experts: tokens per slot, slots per expert
     int per_slot;  // average tokens per slot
-    // the gate/up launch alone takes the routed experts on pass slots (the
-    // down keeps one slot per touched expert)
-    bool gu_passes = false;
 };
 
 
@@ -496,23 +493,18 @@ static Plan plan_set(lcmoe_handle *h, const ExpertSet &s, bool shared, int T, in
         shared ? T : ((int64_t)T * D.n_expert_used + p.slots - 1) / std::max(1, p.slots);
     p.chunks = p.mfma ? (int)std::min<int64_t>(64, std::max<int64_t>(1, (per_slot + 31) / 32)) : 1;
     p.per_slot = (int)std::min<int64_t>(per_slot, INT32_MAX);
-    // Routed experts averaging more than one pass: one block per 32-token
-    // pass of each touched expert (pass slots from the dispatch), so skewed
-    // routing spreads its busy experts over the grid instead of leaving
-    // their passes to a fixed number of blocks each.
-    p.passes = p.mfma && !shared && p.chunks > 1 && h->pass_slots;
+    // Routed experts averaging more than one pass, and any batch past 32
+    // tokens (an expert can then need several passes although the average
+    // is under one: config 4 T = 256, 21 of 137 touched experts hold 33-85
+    // tokens): one block per 32-token pass of each touched expert (pass
+    // slots from the dispatch), so busy experts spread over the grid instead
+    // of leaving their passes to one block after another (config 4 T = 256:
+    // gate/up 570 -> 500 us, down 470 -> 447 us).
+    p.passes = p.mfma && !shared && (p.chunks > 1 || T > 32) && h->pass_slots;
     if (p.passes) {
         p.slots = (int)max_pass_slots(D, T);
         p.chunks = 1;
     }
-    // Past 32 tokens an expert can need several passes even when the
-    // average is under one (config 4 T = 256: 21 of 137 touched experts
-    // hold 33-85 tokens): its block would run them one after another at the
-    // launch's end.  Pass slots spread them for the gate/up launch (config 4
-    // T = 256: 564 -> 484 us).  The down keeps one slot per expert: its grid
-    // is remapped to keep each (slot, split) pair on one XCD, and the pass
-    // rows that exit at once unbalanced that (config 2 T = 64: 58 -> 73 us).
-    p.gu_passes = !p.passes && p.mfma && !shared && T > 32 && h->pass_slots;
     // fused shared experts: slices of the tokens one slot takes (the passes
     // of its chunk blocks, or one row-per-lane pass)
     p.sl = p.mfma ? 32 * p.chunks : 4;
@@ -536,15 +528,6 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
                     pl.slots, fused, fused ? A : INT32_MAX, std::max(1, pl.ns), pl.sl,
                     pl.passes ? h->pass_slots : nullptr};
     const int slots = pl.slots + fused * pl.ns;
-    // the gate/up launch on pass slots (gu_passes): routed slot rows for
-    // every possible pass, the fused shared slices after them
-    SlotArgsHost sa_gu = sa;
-    int slots_gu = slots;
-    if (pl.gu_passes) {
-        sa_gu.nr = (int)max_pass_slots(D, T);
-        sa_gu.pslots = h->pass_slots;
-        slots_gu = sa_gu.nr + fused * pl.ns;
-    }
     // H between the products in the form the down kernel reads: f16 pieces
     // for the matrix-core downs, int8 limbs for the row-per-lane ones (Q4_K,
     // split Q4_K and Q6_K below one token per expert), f32 for the generic one
@@ -552,9 +535,8 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
     const bool limb_out = !pl.mfma && (s.rpl_dn || s.q6_dn || s.q8 || s.split_dn);
     HIP_TRY(timed(h, st, shared || fused_only ? kSlotGateUpSh : kSlotGateUp, [&] {
         if (pl.mfma)
-            return launch_mfma_gateup(s.gate, s.up, s.sz_gu, h->x16, h->x16s, sa_gu, slots_gu,
-                                      pl.gu_passes ? 1 : pl.chunks, d, s.F,
-                                      h16_out ? s.h16 : nullptr, s.h16s,
+            return launch_mfma_gateup(s.gate, s.up, s.sz_gu, h->x16, h->x16s, sa, slots,
+                                      pl.chunks, d, s.F, h16_out ? s.h16 : nullptr, s.h16s,
                                       h16_out ? nullptr : s.Hf, ch, st, h->x_lo);
         if (s.rpl_gu || s.q8)
             return launch_rpl_gateup(s.gate, s.up, s.sz_gu, h->xh, h->xl, h->xs, h->xm, sa,
@@ -639,7 +621,7 @@ static lcmoe_status enqueue_forward(lcmoe_handle *h, const float *x, int32_t T, 
     ra.perm = h->perm;
     ra.inv = h->inv;
     ra.touched = h->touched;
-    ra.pass_slots = pr.passes || pr.gu_passes ? h->pass_slots : nullptr;
+    ra.pass_slots = pr.passes ? h->pass_slots : nullptr;
     ra.sync = h->sync;
     // the fast router reads the whole router matrix once per token: past
     // kFastRouterElems multiply-adds per forward the chain router, which
