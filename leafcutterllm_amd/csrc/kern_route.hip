@@ -916,25 +916,56 @@ __host__ __device__ constexpr bool sig_nc4_ok(int n) {
     return n == 1 || n == 2 || n == 4 || n == 8 || n == 16 || n == 28 || n == 32;
 }
 
-__device__ __forceinline__ void store_agent_f64(double *p, double v) {
-    __hip_atomic_store(reinterpret_cast<unsigned long long *>(p),
-                       (unsigned long long)__double_as_longlong(v), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void store_agent_u64(uint64_t *p, uint64_t v) {
+    __hip_atomic_store(reinterpret_cast<unsigned long long *>(p), (unsigned long long)v,
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ double load_agent_f64(const double *p) {
-    return __longlong_as_double((long long)__hip_atomic_load(
-        reinterpret_cast<unsigned long long *>(const_cast<double *>(p)), __ATOMIC_RELAXED,
-        __HIP_MEMORY_SCOPE_AGENT));
+__device__ __forceinline__ uint64_t load_agent_u64(const uint64_t *p) {
+    return __hip_atomic_load(reinterpret_cast<unsigned long long *>(const_cast<uint64_t *>(p)),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The certification keys of one expert from its chain logit interval
+// [S - B, S + B]: the interval's float ends zlo = up(S - B), zhi = down(S + B)
+// and the point zm = (float)S, as scores (sigmoid_cw for the group kind,
+// whose dips are at most one ulp, so the low and high scores widen by one
+// step each way) plus the bias, rounded to nearest (monotone).  Returns
+// whether every key is finite (a NaN bias or an overflowing bound goes to
+// the exact path).
+__device__ __forceinline__ bool interval_keys(bool grouped, bool has_bias, float bias, double S,
+                                              double B, float &klo, float &khi, float &km) {
+    const double lo = S - B, hi = S + B;
+    const bool fin = __builtin_isfinite(lo) && __builtin_isfinite(hi);
+    const float zlo = fin ? ceil_f32(lo) : 0.0f, zhi = fin ? floor_f32(hi) : 0.0f;
+    const float zm = fin ? (float)S : 0.0f;
+    float kl = zlo, kh = zhi, kp = zm;
+    if (grouped) {  // scores lie in [0, 1]
+        kl = sigmoid_cw(zlo);
+        kh = next_up(sigmoid_cw(zhi));
+        kp = sigmoid_cw(zm);
+        kl = kl > 0.0f ? next_down(kl) : 0.0f;
+    }
+    if (has_bias) {
+        kl = kl + bias;
+        kh = kh + bias;
+        kp = kp + bias;
+    }
+    klo = kl;
+    khi = kh;
+    km = kp;
+    return fin && __builtin_isfinite(kl) && __builtin_isfinite(kh) && __builtin_isfinite(kp);
 }
 
 // float64 chain logit and error bound of (t, e), as logit_bounds(): lane l
 // holds columns [l C, l C + C) (C = 4 NC4) of the token row (read through
 // the cache: every wave of the token reads it) and of the router row in
-// lane-chunk order (a.wlc); written to a.bnd[(t E + e) 2 + {0, 1}].
+// lane-chunk order (a.wlc).  The expert's certification keys (klo, khi)
+// and (km, finite) go to a.bnd[(t E + e) 2 + {0, 1}] as float pairs.
 template <int NC4>
 __device__ void sig_bounds(const RouterArgs &a, int t, int e) {
     constexpr int C = 4 * NC4;
     const int lane = threadIdx.x & 63, d = a.d;
+    const float bias = a.rp.has_bias ? a.bias[e] : 0.0f;
     const f32x4 *xr = reinterpret_cast<const f32x4 *>(a.x + (int64_t)t * d + lane * C);
     const f32x4 *wr = reinterpret_cast<const f32x4 *>(a.wlc) + (int64_t)e * NC4 * 64 + lane;
     f32x4 wv[NC4], xv[NC4];
@@ -970,126 +1001,181 @@ __device__ void sig_bounds(const RouterArgs &a, int t, int e) {
         const double sabs = 4.0 * sg + 4.0 * absp;
         double B = u * gm * sabs + 0x1p-36 * absp + (double)d * 0x1p-149;
         if (e >= (a.E & ~7)) B += u * (1.0 + u) * gm * absp;
-        store_agent_f64(a.bnd + ((int64_t)t * a.E + e) * 2, total);
-        store_agent_f64(a.bnd + ((int64_t)t * a.E + e) * 2 + 1, B);
+        float klo, khi, km;
+        const bool fin = interval_keys(a.rp.kind == LCMOE_ROUTE_SIGMOID_GROUP, a.rp.has_bias != 0,
+                                       bias, total, B, klo, khi, km);
+        uint64_t *out = a.bnd + ((int64_t)t * a.E + e) * 2;
+        store_agent_u64(out, ((uint64_t)__float_as_uint(khi) << 32) | __float_as_uint(klo));
+        store_agent_u64(out + 1, ((uint64_t)(fin ? 1u : 0u) << 32) | __float_as_uint(km));
     }
 }
 
 // Certification of token t by one wave (E <= 256, G <= 64);
-// s_lo / s_hi / s_m: E floats each (the low, high and point keys), s_g:
-// 3 x 64 group scores, s_sel: K.  Writes topk_idx[t] when certified and
-// flag[t] (0 certified, 1 for the exact path); returns the verdict, with the
+// s_lo / s_hi / s_m: E floats each (the low, high and point keys, for the
+// group scores of sizes the lane butterfly does not cover), s_g: 3 x 64
+// group scores, s_sel: K.  Writes topk_idx[t] when certified and flag[t]
+// (0 certified, 1 for the exact path); returns the verdict, with the
 // selection in s_sel when certified.  The softmax kinds select the K largest
 // keys z = c + bias over all experts (select_token): one group, kept.
+//
+// Lane l holds experts l + 64 i (i < 4) and keeps their three keys in
+// registers.  An argmax round is a 32-bit wave maximum of the order keys and
+// a ballot per slice for the lowest index at that maximum (the tie rule of
+// better()).
+
+// v from lane l ^ off for off = 1, 2 (quad permutes), or from a lane of the
+// partner block of size off = 4, 8 (half-row and row mirrors: lane j of an
+// 8- or 16-lane block reads lane 7 - j or 15 - j); 16 and 32 by shuffle.
+// The butterfly below only needs the partner block, whose lanes agree.
+template <int OFF>
+__device__ __forceinline__ float xchg_block(float v) {
+    constexpr int ctrl = OFF == 1 ? 0xB1 : OFF == 2 ? 0x4E : OFF == 4 ? 0x141 : 0x140;
+    if constexpr (OFF >= 16) {
+        return __shfl_xor(v, OFF, 64);
+    } else {
+        return __int_as_float(
+            __builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xf, 0xf, false));
+    }
+}
+
+// (largest, second largest) over aligned lane blocks of size 2 OFF, from
+// blocks of size OFF whose lanes agree; 12 independent pairs interleaved
+template <int OFF>
+__device__ __forceinline__ void top2_step(float (&k1)[3][4], float (&k2)[3][4]) {
+#pragma unroll
+    for (int arr = 0; arr < 3; arr++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float o1 = xchg_block<OFF>(k1[arr][i]), o2 = xchg_block<OFF>(k2[arr][i]);
+            const float hi1 = fmaxf(k1[arr][i], o1), lo1 = fminf(k1[arr][i], o1);
+            k2[arr][i] = fmaxf(lo1, fmaxf(k2[arr][i], o2));
+            k1[arr][i] = hi1;
+        }
+}
+
+// the lowest expert e = l + 64 i whose lane flag is set in slice i, or -1
+__device__ __forceinline__ int lowest_flagged(const bool (&f)[4]) {
+    int w = -1;
+#pragma unroll
+    for (int i = 3; i >= 0; i--) {
+        const uint64_t b = __ballot(f[i]);
+        if (b) w = 64 * i + __builtin_ctzll(b);
+    }
+    return w;
+}
+
 __device__ bool sig_certify(const RouterArgs &a, int t, float *s_lo, float *s_hi, float *s_m,
                             float *s_g, int *s_sel) {
-    const int lane = threadIdx.x & 63, E = a.E, K = a.K, NI = (E + 63) / 64;
+    const int lane = threadIdx.x & 63, E = a.E, K = a.K;
     const RouteParams &rp = a.rp;
     const bool grouped = rp.kind == LCMOE_ROUTE_SIGMOID_GROUP;
     const int G = grouped ? rp.n_group : 1, gs = E / G;
     bool ok = true;
-    double Sv[4], Bv[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {  // all of this lane's bounds in flight
-        const int e = min(lane + 64 * i, E - 1);
-        Sv[i] = load_agent_f64(a.bnd + ((int64_t)t * E + e) * 2);
-        Bv[i] = load_agent_f64(a.bnd + ((int64_t)t * E + e) * 2 + 1);
-    }
+    // the keys the bound waves stored, every load of the lane in flight
+    uint64_t kv[4][2];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int e = lane + 64 * i;
-        if (i >= NI || e >= E) break;
-        const double S = Sv[i], B = Bv[i];
-        const double lo = S - B, hi = S + B;
-        const bool fin = __builtin_isfinite(lo) && __builtin_isfinite(hi);
-        ok = ok && fin;
-        const float zlo = fin ? ceil_f32(lo) : 0.0f, zhi = fin ? floor_f32(hi) : 0.0f;
-        const float zm = fin ? (float)S : 0.0f;
-        float klo = zlo, khi = zhi, km = zm;
-        if (grouped) {
-            // sigmoid_cw's dips are at most one ulp: widen by one step each
-            // way (scores lie in [0, 1])
-            klo = sigmoid_cw(zlo);
-            khi = next_up(sigmoid_cw(zhi));
-            km = sigmoid_cw(zm);
-            klo = klo > 0.0f ? next_down(klo) : 0.0f;
-        }
-        if (rp.has_bias) {  // rounding to nearest is monotone
-            const float b = a.bias[e];
-            klo = klo + b;
-            khi = khi + b;
-            km = km + b;
-        }
-        // finite keys order as values (a NaN bias goes to the exact path)
-        ok = ok && __builtin_isfinite(klo) && __builtin_isfinite(khi) && __builtin_isfinite(km);
-        s_lo[e] = klo;
-        s_hi[e] = khi;
-        s_m[e] = km;
+        const uint64_t *src = a.bnd + ((int64_t)t * E + min(lane + 64 * i, E - 1)) * 2;
+        kv[i][0] = load_agent_u64(src);
+        kv[i][1] = load_agent_u64(src + 1);
     }
-    chain_detail::wave_lds_sync();
+    bool valid[4];
+    float klo[4], khi[4], km[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        valid[i] = lane + 64 * i < E;
+        klo[i] = __uint_as_float((uint32_t)kv[i][0]);
+        khi[i] = __uint_as_float((uint32_t)(kv[i][0] >> 32));
+        km[i] = __uint_as_float((uint32_t)kv[i][1]);
+        if (valid[i]) ok = ok && (kv[i][1] >> 32) != 0;
+    }
     uint64_t kmask = ~0ull;  // kept groups (one for the softmax kinds)
     if (grouped) {
         // group scores of the three key sets: the rounded sum of the group's
         // two largest keys (select_token's expression; only the values
         // matter, and the keys are finite when they count).  Groups of a
-        // power-of-two size up to 64 are lane segments of each 64-expert
-        // slice: a butterfly over the segment merges (largest, second) pairs.
+        // power-of-two size up to 64 are aligned lane blocks of each
+        // 64-expert slice: a butterfly over the block merges (largest,
+        // second) pairs.
         if (gs <= 64 && (gs & (gs - 1)) == 0) {
-            for (int arr = 0; arr < 3; arr++) {
-                const float *v = arr == 0 ? s_lo : arr == 1 ? s_hi : s_m;
-                for (int i = 0; i < NI; i++) {
-                    const int e = lane + 64 * i;
-                    float k1 = e < E ? v[e] : -__builtin_inff(), k2 = -__builtin_inff();
-                    for (int off = 1; off < gs; off <<= 1) {
-                        const float o1 = __shfl_xor(k1, off, 64), o2 = __shfl_xor(k2, off, 64);
-                        const float hi1 = fmaxf(k1, o1), lo1 = fminf(k1, o1);
-                        k2 = fmaxf(lo1, fmaxf(k2, o2));
-                        k1 = hi1;
-                    }
-                    if (e < E && (lane & (gs - 1)) == 0)
-                        s_g[64 * arr + e / gs] = gs >= 2 ? k1 + k2 : k1;
-                }
+            float k1[3][4], k2[3][4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float ninf = -__builtin_inff();
+                k1[0][i] = valid[i] ? klo[i] : ninf;
+                k1[1][i] = valid[i] ? khi[i] : ninf;
+                k1[2][i] = valid[i] ? km[i] : ninf;
+                k2[0][i] = k2[1][i] = k2[2][i] = ninf;
             }
-        } else if (lane < G) {
-            for (int arr = 0; arr < 3; arr++) {
-                const float *v = arr == 0 ? s_lo : arr == 1 ? s_hi : s_m;
-                float k1 = -__builtin_inff(), k2 = -__builtin_inff();
-                int e1 = INT_MAX, e2 = INT_MAX;
-                for (int i = 0; i < gs; i++) {
-                    const int e = lane * gs + i;
-                    const float k = sel_key(v[e]);
-                    if (better(k, e, k1, e1)) {
-                        k2 = k1;
-                        e2 = e1;
-                        k1 = k;
-                        e1 = e;
-                    } else if (better(k, e, k2, e2)) {
-                        k2 = k;
-                        e2 = e;
-                    }
+            if (gs > 1) top2_step<1>(k1, k2);
+            if (gs > 2) top2_step<2>(k1, k2);
+            if (gs > 4) top2_step<4>(k1, k2);
+            if (gs > 8) top2_step<8>(k1, k2);
+            if (gs > 16) top2_step<16>(k1, k2);
+            if (gs > 32) top2_step<32>(k1, k2);
+            if ((lane & (gs - 1)) == 0) {
+#pragma unroll
+                for (int arr = 0; arr < 3; arr++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if (valid[i])
+                            s_g[64 * arr + (lane + 64 * i) / gs] =
+                                gs >= 2 ? k1[arr][i] + k2[arr][i] : k1[arr][i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (valid[i]) {
+                    s_lo[lane + 64 * i] = klo[i];
+                    s_hi[lane + 64 * i] = khi[i];
+                    s_m[lane + 64 * i] = km[i];
                 }
-                s_g[64 * arr + lane] = gs >= 2 ? v[e1] + v[min(e2, E - 1)] : v[e1];
+            chain_detail::wave_lds_sync();
+            if (lane < G) {
+                for (int arr = 0; arr < 3; arr++) {
+                    const float *v = arr == 0 ? s_lo : arr == 1 ? s_hi : s_m;
+                    float k1 = -__builtin_inff(), k2 = -__builtin_inff();
+                    int e1 = INT_MAX, e2 = INT_MAX;
+                    for (int i = 0; i < gs; i++) {
+                        const int e = lane * gs + i;
+                        const float k = sel_key(v[e]);
+                        if (better(k, e, k1, e1)) {
+                            k2 = k1;
+                            e2 = e1;
+                            k1 = k;
+                            e1 = e;
+                        } else if (better(k, e, k2, e2)) {
+                            k2 = k;
+                            e2 = e;
+                        }
+                    }
+                    s_g[64 * arr + lane] = gs >= 2 ? v[e1] + v[min(e2, E - 1)] : v[e1];
+                }
             }
         }
         chain_detail::wave_lds_sync();
-        // kept groups by the point scores, topk_group rounds of a wave argmax
+        // kept groups by the point scores: topk_group argmax rounds, ties to
+        // the lower group index
         const bool gv = lane < G;
         const float glo = gv ? s_g[lane] : 0.0f, ghi = gv ? s_g[64 + lane] : 0.0f;
-        uint64_t gkey = gv ? ((uint64_t)ord_key(sel_key(s_g[128 + lane])) << 32) | (uint32_t)~lane : 0;
+        uint32_t gkey = gv ? ord_key(sel_key(s_g[128 + lane])) : 0u;
         bool kept = false;
         for (int r = 0; r < rp.topk_group; r++) {
-            const uint64_t best = wave_max_u64(gkey);
-            if (gv && lane == (int)~(uint32_t)best) {
+            const uint32_t m = wave_max_u32(gkey);
+            const uint64_t b = __ballot(gkey == m && m != 0u);
+            if (!b) break;
+            if (lane == __builtin_ctzll(b)) {
                 kept = true;
-                gkey = 0;
+                gkey = 0u;
             }
         }
-        // every kept group above every dropped one: the dropped groups' highest
-        // score Mx and the lowest index at it, two wave reductions
+        // every kept group above every dropped one: the dropped groups'
+        // highest score Mx and the lowest index at it
         {
             const bool dropped = gv && !kept;
             const uint32_t mx = wave_max_u32(dropped ? ord_key(ghi) : 0u);
-            const uint32_t fmin = 64u - wave_max_u32(dropped && ord_key(ghi) == mx ? 64u - lane : 0u);
+            const uint64_t b = __ballot(dropped && ord_key(ghi) == mx);
+            const uint32_t fmin = b ? (uint32_t)__builtin_ctzll(b) : 64u;
             if (kept && mx != 0) {
                 const uint32_t ol = ord_key(glo);
                 ok = ok && (ol > mx || (ol == mx && (uint32_t)lane < fmin));
@@ -1097,65 +1183,74 @@ __device__ bool sig_certify(const RouterArgs &a, int t, float *s_lo, float *s_hi
         }
         kmask = __ballot(kept);
     }
-    // K rounds of a wave argmax over the kept groups' experts (point keys)
-    uint64_t ek[4];
+    // K argmax rounds over the kept groups' experts (point keys)
+    uint32_t ck[4];
     int rank[4];
     bool cand[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int e = lane + 64 * i;
-        cand[i] = i < NI && e < E && ((kmask >> (e / gs)) & 1ull);
-        ek[i] = cand[i] ? ((uint64_t)ord_key(sel_key(s_m[e])) << 32) | (uint32_t)~e : 0;
+        cand[i] = valid[i] && ((kmask >> (e / gs)) & 1ull);
+        ck[i] = cand[i] ? ord_key(sel_key(km[i])) : 0u;
         rank[i] = -1;
     }
     for (int r = 0; r < K; r++) {
-        uint64_t mine = 0;
+        const uint32_t m = wave_max_u32(max(max(ck[0], ck[1]), max(ck[2], ck[3])));
+        bool at[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) mine = ek[i] > mine ? ek[i] : mine;
-        const uint64_t best = wave_max_u64(mine);
-        const int be = (int)~(uint32_t)best;
+        for (int i = 0; i < 4; i++) at[i] = ck[i] == m && m != 0u;
+        const int f = lowest_flagged(at);
+        if (f < 0) {  // fewer candidates than K: left to the exact path
+            ok = false;
+            break;
+        }
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            if (lane + 64 * i == be) {
+            if (lane + 64 * i == f) {
                 rank[i] = r;
-                ek[i] = 0;
+                ck[i] = 0u;
             }
-        if (lane == 0) s_sel[r] = be;
+        if (lane == 0) s_sel[r] = f;
     }
-    chain_detail::wave_lds_sync();
-    // each selected expert certainly above every unselected candidate ...
+    // every selected expert certainly above every unselected candidate (their
+    // highest interval end Mx and the lowest index at it) ...
     {
         uint32_t ml = 0;
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            if (cand[i] && rank[i] < 0) ml = max(ml, ord_key(s_hi[lane + 64 * i]));
-        const uint32_t mx = wave_max_u32(ml);
-        uint32_t fl = 0;
+        bool un[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int e = lane + 64 * i;
-            if (cand[i] && rank[i] < 0 && ord_key(s_hi[e]) == mx) fl = max(fl, (uint32_t)(E - e));
+            un[i] = cand[i] && rank[i] < 0;
+            if (un[i]) ml = max(ml, ord_key(khi[i]));
         }
-        const uint32_t fmin = (uint32_t)E - wave_max_u32(fl);
+        const uint32_t mx = wave_max_u32(ml);
+        bool at[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) at[i] = un[i] && ord_key(khi[i]) == mx;
+        const int w = lowest_flagged(at);
+        const uint32_t fmin = w < 0 ? (uint32_t)E : (uint32_t)w;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int e = lane + 64 * i;
             if (rank[i] >= 0 && mx != 0) {
-                const uint32_t ol = ord_key(s_lo[e]);
+                const uint32_t ol = ord_key(klo[i]);
                 ok = ok && (ol > mx || (ol == mx && (uint32_t)e < fmin));
+            }
+            // the selected experts' interval ends by rank, for the pair checks
+            if (rank[i] >= 0) {
+                s_lo[rank[i]] = klo[i];
+                s_hi[rank[i]] = khi[i];
             }
         }
     }
-    // ... and above every selected expert of a later rank
-    for (int r2 = 1; r2 < K; r2++) {
-        const int f = s_sel[r2];
-        const float hf = s_hi[f];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int e = lane + 64 * i;
-            if (rank[i] >= 0 && rank[i] < r2) {
-                const float le = s_lo[e];
-                ok = ok && (le > hf || (le == hf && e < f));
+    chain_detail::wave_lds_sync();
+    // ... and above every selected expert of a later rank (interval ends
+    // apart, or touching with the lower index first): pair (r1, r2) per lane
+    if (ok) {
+        for (int q = lane; q < K * K; q += 64) {
+            const int r1 = q / K, r2 = q % K;
+            if (r1 < r2) {
+                const float le = s_lo[r1], hf = s_hi[r2];
+                ok = ok && (le > hf || (le == hf && s_sel[r1] < s_sel[r2]));
             }
         }
     }
@@ -1166,6 +1261,7 @@ __device__ bool sig_certify(const RouterArgs &a, int t, float *s_lo, float *s_hi
             if (rank[i] >= 0) store_agent(a.topk_idx + (int64_t)t * K + rank[i], lane + 64 * i);
     }
     if (lane == 0) store_agent(a.flag + t, ok ? 0 : 1);
+    chain_detail::wave_lds_sync();  // s_sel for the caller's wave
     return ok;
 }
 
@@ -1179,10 +1275,10 @@ __global__ __launch_bounds__(64 * kSigWaves) void k_route_sig(RouterArgs a, Chai
     const int nsig = a.E / kSigWaves;  // bound blocks per token
     if ((int)blockIdx.x >= nsig) {
         // blocks past them (row 0): the first column range of the exact
-        // chains, wave 0, one tile at a time
+        // chains, wave 0, one tile at a time, two chunks of loads ahead
         if (t == 0 && wave == 0) {
             for (int tile = blockIdx.x - nsig; tile < ch.tiles; tile += gridDim.x - nsig)
-                chain_tile<1, 256, 1>(ch, tile, s_chain);
+                chain_tile<1, 256, 2>(ch, tile, s_chain);
         }
         return;
     }

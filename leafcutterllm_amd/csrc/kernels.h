@@ -47,7 +47,7 @@ struct RouterArgs {
     // per-token block counters, and per-token fallback marks (1: the exact
     // chains decide this token); the chain and select launches that follow
     // it serve only the marked tokens when `flag` is set.
-    double *bnd = nullptr;      // [T, E, 2]
+    uint64_t *bnd = nullptr;    // [T, E, 2]: keys (klo, khi), (km, finite) as float pairs
     uint32_t *tsync = nullptr;  // [T] zero-initialised
     int32_t *flag = nullptr;    // [T]
 };

@@ -95,7 +95,7 @@ struct lcmoe_handle {
     float *topk_w = nullptr;
     uint32_t *sync = nullptr;
     // certified sigmoid-group router: bounds, per-token counters and marks
-    double *sig_bnd = nullptr;
+    uint64_t *sig_bnd = nullptr;
     uint32_t *sig_sync = nullptr;
     int32_t *sig_flag = nullptr;
     int last_T = -1;
