@@ -244,7 +244,8 @@ __device__ void scan_experts(const RouterArgs &a, int *s_off) {
 // its base per expert, pass 2 ranks equal experts inside each 64-assignment
 // group with ballots (lower lane = lower a) and advances the wave's private
 // counters.  The selections are read with device-coherent loads, kDispBatch
-// groups in flight per lane.
+// groups in flight per lane; when a wave's chunk is one such batch (A <=
+// 64 kDispBatch NT / 64), pass 2 takes them from registers.
 constexpr int kDispBatch = 8;
 
 template <int NT>
@@ -256,12 +257,15 @@ __device__ void dispatch_block(const RouterArgs &a, int (*s_cw)[kMaxE], int *s_o
     __syncthreads();
     const int chunk = (((A + W - 1) / W) + 63) & ~63;
     const int a0 = min(A, wave * chunk), a1 = min(A, a0 + chunk);
+    const bool one = chunk <= 64 * kDispBatch;
+    int keep[kDispBatch];
     for (int base = a0; base < a1; base += 64 * kDispBatch) {
         int ev[kDispBatch];
 #pragma unroll
         for (int j = 0; j < kDispBatch; j++) {
             const int q = base + 64 * j + lane;
             ev[j] = q < a1 ? load_agent(a.topk_idx + q) : -1;
+            keep[j] = ev[j];
         }
 #pragma unroll
         for (int j = 0; j < kDispBatch; j++)
@@ -286,7 +290,7 @@ __device__ void dispatch_block(const RouterArgs &a, int (*s_cw)[kMaxE], int *s_o
 #pragma unroll
         for (int j = 0; j < kDispBatch; j++) {
             const int q = base + 64 * j + lane;
-            ev[j] = q < a1 ? load_agent(a.topk_idx + q) : 0;
+            ev[j] = q >= a1 ? 0 : one ? keep[j] : load_agent(a.topk_idx + q);
         }
 #pragma unroll
         for (int j = 0; j < kDispBatch; j++) {
