@@ -284,6 +284,53 @@ def test_sigmoid_router_mixed_tokens():
     assert int(tied.sum()) <= fb <= int(tied.sum()) + max(1, T // 8), fb
 
 
+# group sizes E / n_group of the certifying wave's butterfly (1 .. 64 lanes,
+# aligned blocks of each 64-expert slice) and one it leaves to the LDS path
+# (12, not a power of two)
+SIG_GROUPS = [(256, 4, 2, 8), (64, 4, 2, 6), (32, 8, 4, 4), (16, 8, 4, 4), (16, 16, 8, 4),
+              (48, 4, 2, 6)]
+
+
+@pytest.mark.parametrize("E,G,TG,K", SIG_GROUPS)
+@pytest.mark.parametrize("T", [1, 5])
+def test_sigmoid_router_group_sizes(E, G, TG, K, T):
+    """The certified sigmoid-group router at group sizes 64, 16, 4, 2, 1 and
+    12: routing, dispatch and weights equal the oracle's exact chains."""
+    cfg = small_config(f"sig{E}g{G}", 512, 256, E, K, L.ROUTE_SIGMOID_GROUP, Q4, Q6,
+                       n_group=G, topk_group=TG, routed_scale=2.5, bias="normal0.1")
+    layer = L.synth_layer(cfg, seed=34 + E + G)
+    x = L.synth_x(cfg, T, seed=34, index=T)
+    with L.MoeFfn(cfg.desc(T), layer) as moe:
+        res = run_and_check(cfg, layer, x, moe=moe)
+        fb = moe.route_fallbacks()
+    assert res["rel_l2"] < 1e-3
+    assert 0 <= fb <= max(1, T // 4), fb
+
+
+@pytest.mark.parametrize("T", [1, 6])
+def test_sigmoid_router_group_tie_falls_back(T):
+    """Groups 0 and 1 are copies (router columns and biases) that lead every
+    token, and only one group is kept: their group scores tie exactly, so no
+    bound separates them and every token takes the exact chains, which keep
+    the lower group."""
+    cfg = small_config("sig32g4", 512, 256, 32, 4, L.ROUTE_SIGMOID_GROUP, Q4, Q6, n_group=4,
+                       topk_group=1, routed_scale=2.5, bias="normal0.1")
+    layer = L.synth_layer(cfg, seed=35)
+    r = layer["router"].copy()
+    r[:, 8:16] = r[:, 0:8]
+    layer["router"] = r
+    b = layer["bias"].copy()
+    b[0:8] = 1.0 + 0.01 * np.arange(8)
+    b[8:16] = b[0:8]
+    layer["bias"] = b
+    x = L.synth_x(cfg, T, seed=35, index=T)
+    with L.MoeFfn(cfg.desc(T), layer) as moe:
+        res = run_and_check(cfg, layer, x, moe=moe)
+        assert moe.route_fallbacks() == T
+    idx = res["topk_idx"].reshape(T, cfg.n_expert_used)
+    assert np.all(idx < 8), idx
+
+
 WIDE_CFG = small_config("wide64", 512, 256, 64, 4, L.ROUTE_SOFTMAX_RENORM, Q4, Q4, n_shared=1,
                         d_ff_shared=256)
 
