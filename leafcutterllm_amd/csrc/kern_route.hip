@@ -46,59 +46,156 @@ __device__ __forceinline__ int32_t load_agent(const int32_t *p) {
 }
 
 // Routing weights of token t from its scores s_z (sigmoid scores s_s for the
-// group router) and its selection sel[0..K), in slot order (one thread).
-__device__ void token_weights(const RouterArgs &a, int t, const float *s_z, const float *s_s,
+// group router) and its selection sel[0..K), in slot order, by one wave: the
+// full-E softmax's maximum and exps across the lanes (the exps into s_s,
+// which the softmax kinds leave free), every sum on lane 0 in item order.
+__device__ void token_weights(const RouterArgs &a, int t, const float *s_z, float *s_s,
                               const int *sel) {
-    const int E = a.E, K = a.K;
+    const int lane = threadIdx.x & 63, E = a.E, K = a.K;
     const RouteParams &rp = a.rp;
     float *ow = a.topk_w + (int64_t)t * K;
+    if (rp.kind == LCMOE_ROUTE_SOFTMAX) {  // full-E softmax probabilities of the selected
+        float mx = -__builtin_inff();
+        for (int e = lane; e < E; e += 64) mx = nan_max(mx, s_z[e]);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) mx = nan_max(mx, __shfl_xor(mx, off, 64));
+        for (int e = lane; e < E; e += 64) s_s[e] = expf(s_z[e] - mx);
+        chain_detail::wave_lds_sync();
+        if (lane == 0) {
+            float sum = 0.0f;
+            for (int e = 0; e < E; e++) sum = sum + s_s[e];
+            for (int k = 0; k < K; k++) ow[k] = (s_s[sel[k]] / sum) * rp.scale;
+        }
+        return;
+    }
+    if (lane != 0) return;
     if (rp.kind == LCMOE_ROUTE_SIGMOID_GROUP) {
         float sum = 0.0f;
         for (int k = 0; k < K; k++) sum = sum + s_s[sel[k]];
         for (int k = 0; k < K; k++) ow[k] = (s_s[sel[k]] / sum) * rp.scale;
-    } else if (rp.kind == LCMOE_ROUTE_SOFTMAX_RENORM) {  // cpu.rs:66-79 over the K
+    } else {  // cpu.rs:66-79 over the K
         float mx = -__builtin_inff(), sum = 0.0f;
         for (int k = 0; k < K; k++) mx = nan_max(mx, s_z[sel[k]]);
         for (int k = 0; k < K; k++) sum = sum + expf(s_z[sel[k]] - mx);
         for (int k = 0; k < K; k++) ow[k] = (expf(s_z[sel[k]] - mx) / sum) * rp.scale;
-    } else {  // full-E softmax probabilities of the selected experts
-        float mx = -__builtin_inff(), sum = 0.0f;
-        for (int e = 0; e < E; e++) mx = nan_max(mx, s_z[e]);
-        for (int e = 0; e < E; e++) sum = sum + expf(s_z[e] - mx);
-        for (int k = 0; k < K; k++) ow[k] = (expf(s_z[sel[k]] - mx) / sum) * rp.scale;
     }
 }
 
+// v from lane l ^ off for off = 1, 2 (quad permutes), or from a lane of the
+// partner block of size off = 4, 8 (half-row and row mirrors: lane j of an
+// 8- or 16-lane block reads lane 7 - j or 15 - j); 16 and 32 by shuffle.
+// A butterfly only needs the partner block, whose lanes agree.
+template <int OFF>
+__device__ __forceinline__ float xchg_block(float v) {
+    constexpr int ctrl = OFF == 1 ? 0xB1 : OFF == 2 ? 0x4E : OFF == 4 ? 0x141 : 0x140;
+    if constexpr (OFF >= 16) {
+        return __shfl_xor(v, OFF, 64);
+    } else {
+        return __int_as_float(
+            __builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xf, 0xf, false));
+    }
+}
+
+// (largest, second largest) over aligned lane blocks of size 2 OFF, from
+// blocks of size OFF whose lanes agree; NA x 4 independent pairs interleaved
+template <int OFF, int NA>
+__device__ __forceinline__ void top2_step(float (&k1)[NA][4], float (&k2)[NA][4]) {
+#pragma unroll
+    for (int arr = 0; arr < NA; arr++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float o1 = xchg_block<OFF>(k1[arr][i]), o2 = xchg_block<OFF>(k2[arr][i]);
+            const float hi1 = fmaxf(k1[arr][i], o1), lo1 = fminf(k1[arr][i], o1);
+            k2[arr][i] = fmaxf(lo1, fmaxf(k2[arr][i], o2));
+            k1[arr][i] = hi1;
+        }
+}
+
+// the largest two of every aligned block of gs lanes (gs a power of two up
+// to 64) in every lane of the block, for the NA x 4 key sets
+template <int NA>
+__device__ __forceinline__ void block_top2(int gs, float (&k1)[NA][4], float (&k2)[NA][4]) {
+    if (gs > 1) top2_step<1>(k1, k2);
+    if (gs > 2) top2_step<2>(k1, k2);
+    if (gs > 4) top2_step<4>(k1, k2);
+    if (gs > 8) top2_step<8>(k1, k2);
+    if (gs > 16) top2_step<16>(k1, k2);
+    if (gs > 32) top2_step<32>(k1, k2);
+}
+
+// the lowest expert e = l + 64 i whose lane flag is set in slice i, or -1
+__device__ __forceinline__ int lowest_flagged(const bool (&f)[4]) {
+    int w = -1;
+#pragma unroll
+    for (int i = 3; i >= 0; i--) {
+        const uint64_t b = __ballot(f[i]);
+        if (b) w = 64 * i + __builtin_ctzll(b);
+    }
+    return w;
+}
+
+// The exact selection of token t from its chain logits, by one wave (the
+// reference's route order, ties to the lower index): keys z_e = logit (the
+// sigmoid score for the group kind) + bias, expert l + 64 i in lane l; for
+// the group kind the topk_group groups with the largest sums of their two
+// largest keys, by argmax rounds; then K argmax rounds over the kept
+// experts, each a 32-bit wave maximum of the order keys and a ballot per
+// slice for the lowest index at it.  s_z, s_s: this wave's E scores and
+// sigmoid scores (for the weights); s_g: group scores; s_sel: K.
 __device__ void select_token(const RouterArgs &a, int t, float *s_z, float *s_s, float *s_g,
-                             unsigned char *s_ok, int *s_sel) {
-    // one wave: lane-strided over experts; s_* are this wave's LDS rows
+                             int *s_sel) {
     const int lane = threadIdx.x & 63, E = a.E, K = a.K;
     const RouteParams &rp = a.rp;
+    const bool grouped = rp.kind == LCMOE_ROUTE_SIGMOID_GROUP;
     const float *l = a.logits + (int64_t)t * E;
-    for (int e = lane; e < E; e += 64) {
-        float v = l[e], z;
-        if (rp.kind == LCMOE_ROUTE_SIGMOID_GROUP) {
-            float s = sigmoid_cw(v);
-            s_s[e] = s;
-            z = rp.has_bias ? s + a.bias[e] : s;
-        } else {
-            z = rp.has_bias ? v + a.bias[e] : v;
-        }
-        s_z[e] = z;
-        s_ok[e] = 1;
+    float lv[4], bv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {  // every load of the lane in flight at once
+        const int e = min(lane + 64 * i, E - 1);
+        lv[i] = l[e];
+        bv[i] = rp.has_bias ? a.bias[e] : 0.0f;
     }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    if (rp.kind == LCMOE_ROUTE_SIGMOID_GROUP) {
-        const int G = rp.n_group, gs = E / G;
-        // group score = top-1 z + top-2 z (ties -> lower index), one group
-        // at a time across the wave: per lane the best two of its experts,
-        // then a butterfly merge of (best, second) pairs
-        for (int g = 0; g < G; g++) {
+    bool valid[4];
+    float z[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int e = lane + 64 * i;
+        valid[i] = e < E;
+        float v = lv[i];
+        if (grouped) {
+            const float sg = sigmoid_cw(v);
+            if (valid[i]) s_s[e] = sg;
+            v = sg;
+        }
+        z[i] = rp.has_bias ? v + bv[i] : v;
+        if (valid[i]) s_z[e] = z[i];
+    }
+    chain_detail::wave_lds_sync();
+    uint64_t kmask = ~0ull;  // kept groups (one for the softmax kinds)
+    const int G = grouped ? rp.n_group : 1, gs = E / G;
+    if (grouped) {
+        // group score = the rounded sum of the group's two largest keys (a
+        // NaN key ranks as -inf and counts as one; group scores are only
+        // compared through sel_key, where NaN and -inf are the same)
+        if (gs <= 64 && (gs & (gs - 1)) == 0) {
+            float k1[1][4], k2[1][4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                k1[0][i] = valid[i] ? sel_key(z[i]) : -__builtin_inff();
+                k2[0][i] = -__builtin_inff();
+            }
+            block_top2<1>(gs, k1, k2);
+            if ((lane & (gs - 1)) == 0) {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (valid[i])
+                        s_g[(lane + 64 * i) / gs] = gs >= 2 ? k1[0][i] + k2[0][i] : k1[0][i];
+            }
+        } else if (lane < G) {
             float k1 = -__builtin_inff(), k2 = -__builtin_inff();
             int e1 = INT_MAX, e2 = INT_MAX;
-            for (int i = lane; i < gs; i += 64) {
-                const int e = g * gs + i;
+            for (int i = 0; i < gs; i++) {
+                const int e = lane * gs + i;
                 const float k = sel_key(s_z[e]);
                 if (better(k, e, k1, e1)) {
                     k2 = k1;
@@ -110,86 +207,44 @@ __device__ void select_token(const RouterArgs &a, int t, float *s_z, float *s_s,
                     e2 = e;
                 }
             }
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                const float o1 = __shfl_xor(k1, off, 64), o2 = __shfl_xor(k2, off, 64);
-                const int f1 = __shfl_xor(e1, off, 64), f2 = __shfl_xor(e2, off, 64);
-                if (better(o1, f1, k1, e1)) {  // other's best leads
-                    const bool keep = better(k1, e1, o2, f2);
-                    k2 = keep ? k1 : o2;
-                    e2 = keep ? e1 : f2;
-                    k1 = o1;
-                    e1 = f1;
-                } else if (better(o1, f1, k2, e2)) {
-                    k2 = o1;
-                    e2 = f1;
-                }
-            }
-            if (lane == 0) s_g[g] = gs >= 2 ? s_z[e1] + s_z[min(e2, E - 1)] : s_z[e1];
+            s_g[lane] = gs >= 2 ? s_z[e1] + s_z[min(e2, E - 1)] : s_z[e1];
         }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        // keep the topk_group best groups (ties -> lower group index)
-        unsigned long long keep = 0;  // G <= 64 groups supported here
-        for (int i = 0; i < rp.topk_group; i++) {
-            float bk = -__builtin_inff();
-            int bg = INT_MAX;
-            for (int g = lane; g < G; g += 64) {
-                if ((keep >> g) & 1ull) continue;
-                float k = sel_key(s_g[g]);
-                if (better(k, g, bk, bg)) {
-                    bk = k;
-                    bg = g;
-                }
+        chain_detail::wave_lds_sync();
+        // keep the topk_group best groups (ties to the lower group index)
+        uint32_t gkey = lane < G ? ord_key(sel_key(s_g[lane])) : 0u;
+        bool kept = false;
+        for (int r = 0; r < rp.topk_group; r++) {
+            const uint32_t m = wave_max_u32(gkey);
+            const uint64_t b = __ballot(gkey == m && m != 0u);
+            if (!b) break;
+            if (lane == __builtin_ctzll(b)) {
+                kept = true;
+                gkey = 0u;
             }
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                float ok = __shfl_xor(bk, off, 64);
-                int og = __shfl_xor(bg, off, 64);
-                if (better(ok, og, bk, bg)) {
-                    bk = ok;
-                    bg = og;
-                }
-            }
-            if (bg < G) keep |= 1ull << bg;
         }
-        for (int e = lane; e < E; e += 64) s_ok[e] = (keep >> (e / gs)) & 1ull;
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        kmask = __ballot(kept);
     }
-    // K rounds of wave-wide argmax, ties -> lower expert index
-    unsigned used = 0;  // bit i: expert lane + 64*i taken
-    for (int slot = 0; slot < K; slot++) {
-        float bk = -__builtin_inff();
-        int be = INT_MAX;
-        for (int i = 0, e = lane; e < E; i++, e += 64) {
-            if (!s_ok[e] || ((used >> i) & 1u)) continue;
-            float k = sel_key(s_z[e]);
-            if (better(k, e, bk, be)) {
-                bk = k;
-                be = e;
-            }
-        }
+    uint32_t ck[4];
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            float ok = __shfl_xor(bk, off, 64);
-            int oe = __shfl_xor(be, off, 64);
-            if (better(ok, oe, bk, be)) {
-                bk = ok;
-                be = oe;
-            }
-        }
-        if (be >= E) be = 0;  // unreachable: K <= candidates is validated on the host
-        if ((be & 63) == lane) used |= 1u << (be >> 6);
-        if (lane == 0) s_sel[slot] = be;
+    for (int i = 0; i < 4; i++) {
+        const int e = lane + 64 * i;
+        ck[i] = valid[i] && ((kmask >> (e / gs)) & 1ull) ? ord_key(sel_key(z[i])) : 0u;
     }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    if (lane == 0) {
-        token_weights(a, t, s_z, s_s, s_sel);
-        int32_t *oi = a.topk_idx + (int64_t)t * K;
-        for (int k = 0; k < K; k++) store_agent(oi + k, s_sel[k]);
+    for (int r = 0; r < K; r++) {
+        const uint32_t m = wave_max_u32(max(max(ck[0], ck[1]), max(ck[2], ck[3])));
+        bool at[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) at[i] = ck[i] == m && m != 0u;
+        int f = lowest_flagged(at);
+        if (f < 0) f = 0;  // unreachable: K <= candidates is validated on the host
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (lane + 64 * i == f) ck[i] = 0u;
+        if (lane == 0) s_sel[r] = f;
     }
+    chain_detail::wave_lds_sync();
+    token_weights(a, t, s_z, s_s, s_sel);
+    if (lane < K) store_agent(a.topk_idx + (int64_t)t * K + lane, s_sel[lane]);
 }
 
 // Inclusive scan across the wave
@@ -421,7 +476,6 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB, int E
     float *s_x = smem;                // [TB][d + pad]
     float *s_w = smem + TB * stride;  // [EG][d + pad], this block's router rows
     __shared__ float s_z[4][kMaxE], s_s[4][kMaxE], s_g[4][kMaxE];
-    __shared__ unsigned char s_ok[4][kMaxE];
     __shared__ int s_sel[4][kMaxK];
     __shared__ int s_cw[kThreads / 64][kMaxE];
     __shared__ int s_off[kMaxE + 1];
@@ -496,7 +550,7 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a, int TB, int E
     __threadfence();
     const int wave = tid >> 6;
     for (int t = wave; t < nt; t += kThreads / 64)
-        select_token(a, t0 + t, s_z[wave], s_s[wave], s_g[wave], s_ok[wave], s_sel[wave]);
+        select_token(a, t0 + t, s_z[wave], s_s[wave], s_g[wave], s_sel[wave]);
 
     // ---- last token group runs the dispatch
     __threadfence();
@@ -745,7 +799,6 @@ __device__ __forceinline__ void logits_and_activations(const RouterArgs &a, int 
 __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a, ChainArgs ch) {
     __shared__ double s_a[kMaxE], s_b[kMaxE];
     __shared__ float s_z[kMaxE], s_zlo[kMaxE], s_zhi[kMaxE], s_s[kMaxE], s_g[kMaxE];
-    __shared__ unsigned char s_ok[kMaxE];
     __shared__ int s_sel[kMaxK];
     __shared__ int s_cw[kFastThreads / 64][kMaxE];
     __shared__ int s_off[kMaxE + 1];
@@ -854,7 +907,7 @@ __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a, Chain
         __threadfence_block();
         __syncthreads();
         if (wave == 0) {
-            select_token(a, t, s_z, s_s, s_g, s_ok, s_sel);
+            select_token(a, t, s_z, s_s, s_g, s_sel);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
         __syncthreads();
@@ -1027,47 +1080,6 @@ __device__ void sig_bounds(const RouterArgs &a, int t, int e) {
 // a ballot per slice for the lowest index at that maximum (the tie rule of
 // better()).
 
-// v from lane l ^ off for off = 1, 2 (quad permutes), or from a lane of the
-// partner block of size off = 4, 8 (half-row and row mirrors: lane j of an
-// 8- or 16-lane block reads lane 7 - j or 15 - j); 16 and 32 by shuffle.
-// The butterfly below only needs the partner block, whose lanes agree.
-template <int OFF>
-__device__ __forceinline__ float xchg_block(float v) {
-    constexpr int ctrl = OFF == 1 ? 0xB1 : OFF == 2 ? 0x4E : OFF == 4 ? 0x141 : 0x140;
-    if constexpr (OFF >= 16) {
-        return __shfl_xor(v, OFF, 64);
-    } else {
-        return __int_as_float(
-            __builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xf, 0xf, false));
-    }
-}
-
-// (largest, second largest) over aligned lane blocks of size 2 OFF, from
-// blocks of size OFF whose lanes agree; 12 independent pairs interleaved
-template <int OFF>
-__device__ __forceinline__ void top2_step(float (&k1)[3][4], float (&k2)[3][4]) {
-#pragma unroll
-    for (int arr = 0; arr < 3; arr++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float o1 = xchg_block<OFF>(k1[arr][i]), o2 = xchg_block<OFF>(k2[arr][i]);
-            const float hi1 = fmaxf(k1[arr][i], o1), lo1 = fminf(k1[arr][i], o1);
-            k2[arr][i] = fmaxf(lo1, fmaxf(k2[arr][i], o2));
-            k1[arr][i] = hi1;
-        }
-}
-
-// the lowest expert e = l + 64 i whose lane flag is set in slice i, or -1
-__device__ __forceinline__ int lowest_flagged(const bool (&f)[4]) {
-    int w = -1;
-#pragma unroll
-    for (int i = 3; i >= 0; i--) {
-        const uint64_t b = __ballot(f[i]);
-        if (b) w = 64 * i + __builtin_ctzll(b);
-    }
-    return w;
-}
-
 __device__ bool sig_certify(const RouterArgs &a, int t, float *s_lo, float *s_hi, float *s_m,
                             float *s_g, int *s_sel) {
     const int lane = threadIdx.x & 63, E = a.E, K = a.K;
@@ -1111,12 +1123,7 @@ __device__ bool sig_certify(const RouterArgs &a, int t, float *s_lo, float *s_hi
                 k1[2][i] = valid[i] ? km[i] : ninf;
                 k2[0][i] = k2[1][i] = k2[2][i] = ninf;
             }
-            if (gs > 1) top2_step<1>(k1, k2);
-            if (gs > 2) top2_step<2>(k1, k2);
-            if (gs > 4) top2_step<4>(k1, k2);
-            if (gs > 8) top2_step<8>(k1, k2);
-            if (gs > 16) top2_step<16>(k1, k2);
-            if (gs > 32) top2_step<32>(k1, k2);
+            block_top2<3>(gs, k1, k2);
             if ((lane & (gs - 1)) == 0) {
 #pragma unroll
                 for (int arr = 0; arr < 3; arr++)
@@ -1309,8 +1316,7 @@ __global__ __launch_bounds__(64 * kSigWaves) void k_route_sig(RouterArgs a, Chai
             for (int g = 0; g < ca.tiles; g++) chain_tile<1, 256, 1>(ca, g, s_chain);
             __threadfence_block();
             float *s_z = s_f, *s_s = s_f + kMaxE, *s_g = s_f + 2 * kMaxE;
-            unsigned char *s_ok = reinterpret_cast<unsigned char *>(s_f + 3 * kMaxE);
-            select_token(a, t, s_z, s_s, s_g, s_ok, s_sel);
+            select_token(a, t, s_z, s_s, s_g, s_sel);
             chain_detail::wave_lds_sync();
         }
         dispatch_one(a, s_sel);
@@ -1362,7 +1368,6 @@ __global__ __launch_bounds__(64 * kChainWaves) void k_route_chains(RouterArgs a,
 
 __global__ __launch_bounds__(64 * kSelWaves) void k_route_select(RouterArgs a) {
     __shared__ float s_z[kSelWaves][kMaxE], s_s[kSelWaves][kMaxE], s_g[kSelWaves][kMaxE];
-    __shared__ unsigned char s_ok[kSelWaves][kMaxE];
     __shared__ int s_sel[kSelWaves][kMaxK];
     __shared__ int s_cw[kSelWaves][kMaxE];
     __shared__ int s_off[kMaxE + 1];
@@ -1370,7 +1375,7 @@ __global__ __launch_bounds__(64 * kSelWaves) void k_route_select(RouterArgs a) {
     const int tid = threadIdx.x, wave = tid >> 6, t = blockIdx.x * kSelWaves + wave;
     // after the certified sigmoid router: only the tokens it marked
     const bool sel = t < a.T && (!a.flag || a.flag[t] != 0);
-    if (sel) select_token(a, t, s_z[wave], s_s[wave], s_g[wave], s_ok[wave], s_sel[wave]);
+    if (sel) select_token(a, t, s_z[wave], s_s[wave], s_g[wave], s_sel[wave]);
     if (a.T == 1) {
         if (wave == 0) {
             if (!sel) {  // certified: the selection is in topk_idx
