@@ -364,6 +364,8 @@ def main():
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--tokens", type=int, default=64, help="headline batch")
     ap.add_argument("--sweep", default="1,8,64")
+    ap.add_argument("--device-warmup", type=float, default=0.5, metavar="S",
+                    help="seconds of untimed forwards at the headline batch before the sweep")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--norm-residual", action="store_true",
                     help="time lcmoe_forward_norm_residual_dev (post-attention RMSNorm, "
@@ -447,6 +449,19 @@ def main():
         for r in range(R):
             x = L.synth_x(cfg, T, seed=0, index=1000 * r + T)
             xbufs[(r, T)] = hip.DeviceBuffer(x.nbytes).upload(x)
+
+    # Device warm-up: the headline batch runs untimed for `device_warmup`
+    # seconds before the sweep, so that every batch size is timed at the
+    # clocks a busy GPU holds.  From idle, the first tenths of a second of
+    # forwards run slower (config 2: T=8 ~177-185 us against ~168 us warm,
+    # T=64 ~203-220 against ~198 us; T=1 unchanged).
+    t_w = time.perf_counter()
+    n_w = 0
+    while time.perf_counter() - t_w < args.device_warmup:
+        for _ in range(16):
+            step(n_w % R, args.tokens)
+            n_w += 1
+        stream.synchronize()
 
     per_batch = {}
     for T in sweep:
@@ -587,6 +602,7 @@ def main():
             "entry": "lcmoe_forward_norm_residual_dev" if args.norm_residual else "lcmoe_forward_dev",
             "batch": args.tokens, "d_model": cfg.d_model, "d_ff": cfg.d_ff,
             "n_expert": cfg.n_expert, "top_k": cfg.n_expert_used, "replicas": R,
+            "device_warmup_s": args.device_warmup,
         },
         "roofline": roof,
         "layer_roofline_frac": round(head["layer_GBps"] / HBM_PEAK_GBS, 4),
