@@ -1303,6 +1303,242 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down_q6(
     }
 }
 
+// ---- Q8_0 on the matrix cores ---------------------------------------------
+// Weights in the RPL64 Q8_0 layout (lcmoe_host.cpp repack_rpl64_q8): per
+// 64-row tile and 256-column group, chunk 0 holds each row's eight f16
+// block scales (16 bytes) and chunk 1 + j the row's columns 16j .. 16j+15.
+// A Q8_0 block (32 columns) is exactly the K of one v_mfma_f32_16x16x32_f16:
+// each block's product S_b = sum_k x_k q_k starts from zero and its scale is
+// applied once, acc += d_b * S_b in f32 (dequantize_q8_0,
+// rust/src/kernels/mod.rs:37-51: w = q * d).  B = q is exact in f16: the
+// biased byte q ^ 0x80 under the 0x64 exponent byte is 1152 + q, and one
+// packed add leaves q.  Activations enter as one f16 per element (the
+// default mode).  A block is one wave and one 16-token pass over NTL 16-row
+// tiles of each of its MATS matrices: small layers (config 1: F = 2816,
+// d = 1024) need the many blocks, and the wave stages its own tokens'
+// activations.
+constexpr int kQ8Group = 17 * 1024;  // bytes per 64-row tile and group
+constexpr int kQ8Tok = 16;
+constexpr int kQ8Stage = kQ8Tok * kTokB<false>;  // 16 token rows of 528 bytes
+constexpr int kQ8Lds = 2 * kQ8Stage > 4 * chain_lds_floats(16, 128)
+                           ? 2 * kQ8Stage : 4 * chain_lds_floats(16, 128);
+__shared__ __attribute__((aligned(1024))) uint8_t s_q8[kQ8Lds];
+
+// One matrix's NTL 16-row tiles for one group: lane (r16, c4) holds row r16
+// of tile t's eight scales and, per block b, the row's columns 32b + 8c4 .. +7.
+template <int NTL>
+struct WQ8 {
+    u32x4 d[NTL];
+    u32x2 q[8][NTL];  // [block][tile]
+};
+
+// lo: this lane's row offset r16 * 16 from the wave's row base; tile t is
+// 16 t rows further (256 bytes in every chunk)
+__device__ __forceinline__ u32x4 load_q8d(g_u8 *base, uint32_t lo, int g, int t) {
+    return gload<u32x4>(base + (lo + (uint32_t)(g * kQ8Group + 256 * t)));
+}
+__device__ __forceinline__ u32x2 load_q8q(g_u8 *base, uint32_t lo, int g, int b, int t, int c4) {
+    return gload<u32x2>(base + (lo + (uint32_t)(g * kQ8Group + (1 + 2 * b + (c4 >> 1)) * 1024 +
+                                                256 * t + 8 * (c4 & 1))));
+}
+
+// B operand of 8 quants in the activation format's column order
+// (act16_pos: bytes 0, 2, 1, 3, 4, 6, 5, 7)
+__device__ __forceinline__ half8 dec_q8(u32x2 q) {
+    const uint32_t w0 = q.x ^ 0x80808080u, w1 = q.y ^ 0x80808080u;
+    const half2v k = half2v{(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const half2v a = magic2(w0, kSel02) + k, b = magic2(w0, kSel13) + k;
+    const half2v c = magic2(w1, kSel02) + k, e = magic2(w1, kSel13) + k;
+    return half8{a[0], a[1], b[0], b[1], c[0], c[1], e[0], e[1]};
+}
+
+// the 16 tokens' activations of one group through this wave's registers
+struct Q8Act {
+    u32x2 tok[kQ8Tok];
+};
+
+__device__ __forceinline__ void q8_act_load(Q8Act &s, g_u8 *const (&tok)[kQ8Tok], int g,
+                                            int lane) {
+#pragma unroll
+    for (int i = 0; i < kQ8Tok; i++)
+        s.tok[i] = gload<u32x2>(tok[i] + (uint32_t)(g * 1024 + 8 * lane));
+}
+
+__device__ __forceinline__ void q8_act_store(uint8_t *stage, const Q8Act &s, int lane) {
+#pragma unroll
+    for (int i = 0; i < kQ8Tok; i++)
+        *reinterpret_cast<u32x2 *>(stage + i * kTokB<false> + 8 * lane) = s.tok[i];
+}
+
+// One group: the blocks of `cur`'s activations against w; w reloaded with
+// group gn block by block, and gn's activations staged into `nxt`.
+template <int MATS, int NTL>
+__device__ __forceinline__ void q8_step(g_u8 *const (&wb)[MATS], uint32_t lo, int gn,
+                                        const uint8_t *cur, uint8_t *nxt,
+                                        g_u8 *const (&tok)[kQ8Tok], WQ8<NTL> (&w)[MATS],
+                                        float4v (&acc)[MATS][NTL], int lane) {
+    const int r16 = lane & 15, c4 = lane >> 4;
+    Q8Act act;
+    q8_act_load(act, tok, gn, lane);
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads first
+    uint32_t dw[MATS][NTL][4];  // this group's scales; the next group's load in their place
+#pragma unroll
+    for (int m = 0; m < MATS; m++)
+#pragma unroll
+        for (int t = 0; t < NTL; t++) {
+            const u32x4 v = w[m].d[t];
+            dw[m][t][0] = v.x;
+            dw[m][t][1] = v.y;
+            dw[m][t][2] = v.z;
+            dw[m][t][3] = v.w;
+            w[m].d[t] = load_q8d(wb[m], lo, gn, t);
+        }
+    const uint8_t *tokrow = cur + r16 * kTokB<false>;
+    half8 a[2];  // block b's activations, and b + 1's read ahead
+    a[0] = *reinterpret_cast<const half8 *>(tokrow + 16 * c4);
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+        if (b + 1 < 8)
+            a[(b + 1) & 1] = *reinterpret_cast<const half8 *>(tokrow + 64 * (b + 1) + 16 * c4);
+        float4v S[MATS][NTL];
+#pragma unroll
+        for (int m = 0; m < MATS; m++)
+#pragma unroll
+            for (int t = 0; t < NTL; t++) {
+                const half8 bq = dec_q8(w[m].q[b][t]);
+                w[m].q[b][t] = load_q8q(wb[m], lo, gn, b, t, c4);
+                S[m][t] = mfma16(a[b & 1], bq, float4v{});
+            }
+#pragma unroll
+        for (int m = 0; m < MATS; m++)
+#pragma unroll
+            for (int t = 0; t < NTL; t++) {
+                const float db = dh2f(dw[m][t][b >> 1] >> (16 * (b & 1)));
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    acc[m][t][i] = __builtin_fmaf(db, S[m][t][i], acc[m][t][i]);
+            }
+        __builtin_amdgcn_sched_barrier(0);  // bounds the live operands to one block
+    }
+    q8_act_store(nxt, act, lane);
+    chain_detail::wave_lds_sync();
+}
+
+// grid (rows / (16 NTL) row groups, [chain row +] slots, token groups);
+// block = one wave.  MATS = 2, NTL = 1: the gate/up products (w0 = gate,
+// w1 = up, cols = d, rows = F) with the SwiGLU into H as k_mfma_gateup
+// writes it (without the sub-block sums, which no Q8_0 down reads); with
+// ch.tiles, row 0 runs the exact router chains.  MATS = 1, NTL = 2: the
+// down product (w0 = down, cols = F, rows = d), grid z = K split + ksplit *
+// token group, partial sums of split z into Y + z * split_stride.  Token
+// group z takes the slot's 16-token passes z, z + groups, ...
+template <int MATS, int NTL>
+__global__ __launch_bounds__(64, 2) void k_mfma_q8(
+    const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, int64_t estride,
+    const _Float16 *__restrict__ act, SlotArgs sa, int cols, int rows, int ksplit,
+    _Float16 *__restrict__ h16, float *__restrict__ hf, float *__restrict__ Y,
+    int64_t split_stride, ChainArgs ch) {
+    int slot = blockIdx.y;
+    if (MATS == 2 && ch.tiles) {
+        if (slot == 0) {
+            if (blockIdx.z) return;
+            // four chunks of loads in flight: small layers' expert launches
+            // are short next to a d-long chain (config 1, d = 1024: one
+            // chunk ahead left the chains ~16 us, longer than the products)
+            float *lds = reinterpret_cast<float *>(s_q8);
+            for (int tile = blockIdx.x; tile < ch.tiles; tile += gridDim.x)
+                chain_tile<8, 128, 4>(ch, tile, lds);
+            return;
+        }
+        slot -= 1;
+    }
+    int e, p0, n;
+    if (!slot_info(sa, slot, e, p0, n)) return;
+    const int lane = threadIdx.x & 63, r16 = lane & 15, c4 = lane >> 4;
+    const int rg = blockIdx.x, NG = cols >> 8;
+    constexpr int kPerTile = 4 / NTL;  // row groups per 64-row tile
+    const int ks = MATS == 1 ? ksplit : 1;
+    const int cz = blockIdx.z / ks, nz = gridDim.z / ks, bz = blockIdx.z - cz * ks;
+    const int g0 = (int)((int64_t)NG * bz / ks), g1 = (int)((int64_t)NG * (bz + 1) / ks);
+    const int64_t rbase = (int64_t)e * estride + (int64_t)(rg / kPerTile) * NG * kQ8Group +
+                          16 * NTL * (rg % kPerTile) * 16;
+    g_u8 *wbm[MATS];
+    wbm[0] = uniform(w0 + rbase);
+    if constexpr (MATS == 2) wbm[1] = uniform(w1 + rbase);
+    const uint32_t lo = r16 * 16;
+    const uint8_t *ab = reinterpret_cast<const uint8_t *>(act);
+    uint8_t *const st0 = s_q8, *const st1 = s_q8 + kQ8Stage;
+    for (int c = cz * kQ8Tok; c < n; c += nz * kQ8Tok) {
+        g_u8 *tok[kQ8Tok];
+#pragma unroll
+        for (int i = 0; i < kQ8Tok; i++) {
+            const int q = min(c + i, n - 1);
+            const int64_t row = MATS == 2 ? slot_token(sa, p0, q) : p0 + q;
+            tok[i] = uniform(ab + row * (int64_t)cols * 4);
+        }
+        float4v acc[MATS][NTL];
+#pragma unroll
+        for (int m = 0; m < MATS; m++)
+#pragma unroll
+            for (int t = 0; t < NTL; t++) acc[m][t] = float4v{};
+        WQ8<NTL> w[MATS];
+        Q8Act a0;
+        q8_act_load(a0, tok, g0, lane);
+#pragma unroll
+        for (int m = 0; m < MATS; m++)
+#pragma unroll
+            for (int t = 0; t < NTL; t++) {
+                w[m].d[t] = load_q8d(wbm[m], lo, g0, t);
+#pragma unroll
+                for (int b = 0; b < 8; b++) w[m].q[b][t] = load_q8q(wbm[m], lo, g0, b, t, c4);
+            }
+        q8_act_store(st0, a0, lane);
+        chain_detail::wave_lds_sync();
+        const int last = g1 - 1;
+        int g = g0;
+        for (; g + 2 <= g1; g += 2) {
+            q8_step<MATS, NTL>(wbm, lo, g + 1, st0, st1, tok, w, acc, lane);
+            q8_step<MATS, NTL>(wbm, lo, min(g + 2, last), st1, st0, tok, w, acc, lane);
+        }
+        if (g < g1) q8_step<MATS, NTL>(wbm, lo, g, st0, st1, tok, w, acc, lane);
+        if constexpr (MATS == 2) {
+            // SwiGLU and H out (f16 pieces and/or f32), as the 16-token
+            // passes of k_mfma_gateup
+            const int F = rows, nkb = (F + 255) >> 8;
+            int fb = rg * 16 * NTL + r16;  // opaque: output addresses are formed here
+            asm volatile("" : "+v"(fb));
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int q = c + 4 * c4 + i;
+                if (q < n) {
+                    const int64_t p = p0 + q;
+#pragma unroll
+                    for (int t = 0; t < NTL; t++) {
+                        const int ft = fb + 16 * t;
+                        const float v = silu(acc[0][t][i]) * acc[1][t][i];
+                        if (hf) hf[p * F + ft] = v;
+                        if (h16)
+                            h16[(p * nkb + (ft >> 8)) * 512 + act16_pos(ft & 255)] = (_Float16)v;
+                    }
+                }
+            }
+        } else {
+            float *Yz = Y + (int64_t)bz * split_stride;
+            int rb = rg * 16 * NTL + r16;  // opaque: output addresses are formed here
+            asm volatile("" : "+v"(rb));
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int q = c + 4 * c4 + i;
+                if (q < n) {
+                    float *yrow = Yz + (int64_t)(p0 + q) * rows + rb;
+#pragma unroll
+                    for (int t = 0; t < NTL; t++) yrow[16 * t] = acc[0][t][i];
+                }
+            }
+        }
+    }
+}
+
 // x rows -> f16 hi/lo pieces (per super-block: hi[256] then lo[256]) and
 // per-sub-block sums (hi, lo); one thread per 32-column sub-block
 __global__ __launch_bounds__(256) void k_act16(const float *__restrict__ x, int T, int d,
@@ -1357,6 +1593,33 @@ hipError_t launch_mfma_gateup(const uint8_t *gate, const uint8_t *up, int64_t es
                        dim3((groups + kWaves - 1) / kWaves, slots + (c.tiles ? 1 : 0), chunks),
                        dim3(256), 0, st, gate, up, estride, x16, xs, dev_slots(sa), d, F, h16, hs,
                        hf, c);
+    return hipGetLastError();
+}
+
+hipError_t launch_mfma_gateup_q8(const uint8_t *gate, const uint8_t *up, int64_t estride,
+                                 const _Float16 *x16, const SlotArgsHost &sa, int slots,
+                                 int groups, int d, int F, _Float16 *h16, float *hf,
+                                 const ChainArgs &ch, hipStream_t st) {
+    if (F % 64 || d % 256 || groups < 1 || groups > 65535) return hipErrorInvalidValue;
+    ChainArgs c = ch;
+    if (c.tiles) {
+        if (c.k0 % 128 || c.k1 % 128) return hipErrorInvalidValue;
+        c = with_nt(ch, 8);
+    }
+    hipLaunchKernelGGL((k_mfma_q8<2, 1>), dim3(F / 16, slots + (c.tiles ? 1 : 0), groups),
+                       dim3(64), 0, st, gate, up, estride, x16, dev_slots(sa), d, F, 1, h16, hf,
+                       nullptr, (int64_t)0, c);
+    return hipGetLastError();
+}
+
+hipError_t launch_mfma_down_q8(const uint8_t *down, int64_t estride, const _Float16 *h16,
+                               const SlotArgsHost &sa, int slots, int groups, int d, int F,
+                               int ksplit, float *Y, int64_t split_stride, hipStream_t st) {
+    if (d % 64 || F % 256 || ksplit < 1 || groups < 1 || (int64_t)groups * ksplit > 65535)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL((k_mfma_q8<1, 2>), dim3(d / 32, slots, groups * ksplit), dim3(64), 0, st,
+                       down, nullptr, estride, h16, dev_slots(sa), F, d, ksplit, nullptr, nullptr,
+                       Y, split_stride, ChainArgs{});
     return hipGetLastError();
 }
 
