@@ -1313,13 +1313,22 @@ __global__ __launch_bounds__(256, 2) void k_mfma_down_q6(
 // rust/src/kernels/mod.rs:37-51: w = q * d).  B = q is exact in f16: the
 // biased byte q ^ 0x80 under the 0x64 exponent byte is 1152 + q, and one
 // packed add leaves q.  Activations enter as one f16 per element (the
-// default mode).  A block is one wave and one 16-token pass over NTL 16-row
-// tiles of each of its MATS matrices: small layers (config 1: F = 2816,
+// default mode).  A block is one wave of 32 rows (two 16-row tiles) of its
+// MATS matrices and one 16-token pass: small layers (config 1: F = 2816,
 // d = 1024) need the many blocks, and the wave stages its own tokens'
-// activations.
+// activations, eight tokens at a time.
+//
+// H between the products: f16 pieces in the format of k_mfma_gateup, each
+// token's 32-column block (one gate/up wave's rows, one down MFMA's K)
+// scaled by 2^-e with e the smallest exponent that keeps the block's largest
+// magnitude below 2^15, and e in a byte per token and block.  e = 0 for
+// every block that f16 holds as it is (such blocks are the plain
+// conversion); the down scales each block's product back by 2^e.  Q8_0
+// weights up to the loader's |w| <= 100 can drive H past f16's range.
 constexpr int kQ8Group = 17 * 1024;  // bytes per 64-row tile and group
 constexpr int kQ8Tok = 16;
-constexpr int kQ8Stage = kQ8Tok * kTokB<false>;  // 16 token rows of 528 bytes
+constexpr int kQ8Exp = kQ8Tok * kTokB<false>;  // 16 token rows of 528 bytes
+constexpr int kQ8Stage = kQ8Exp + 8 * kQ8Tok * 4;  // then the scales 2^e, [block][token]
 constexpr int kQ8Lds = 2 * kQ8Stage > 4 * chain_lds_floats(16, 128)
                            ? 2 * kQ8Stage : 4 * chain_lds_floats(16, 128);
 __shared__ __attribute__((aligned(1024))) uint8_t s_q8[kQ8Lds];
@@ -1332,8 +1341,8 @@ struct WQ8 {
     u32x2 q[8][NTL];  // [block][tile]
 };
 
-// lo: this lane's row offset r16 * 16 from the wave's row base; tile t is
-// 16 t rows further (256 bytes in every chunk)
+// lo: this lane's row offset r16 * 16 from the wave's row base; tile 1 is
+// the 16 rows after tile 0 (256 bytes further in every chunk)
 __device__ __forceinline__ u32x4 load_q8d(g_u8 *base, uint32_t lo, int g, int t) {
     return gload<u32x4>(base + (lo + (uint32_t)(g * kQ8Group + 256 * t)));
 }
@@ -1352,34 +1361,51 @@ __device__ __forceinline__ half8 dec_q8(u32x2 q) {
     return half8{a[0], a[1], b[0], b[1], c[0], c[1], e[0], e[1]};
 }
 
-// the 16 tokens' activations of one group through this wave's registers
+// Eight tokens' activations of one group (their f16 pieces' hi halves)
+// through this wave's registers, and (down) lane i < 16's 8 block exponents
+// of token i.
 struct Q8Act {
-    u32x2 tok[kQ8Tok];
+    u32x2 tok[kQ8Tok / 2];
+    u32x2 ex;
 };
 
-__device__ __forceinline__ void q8_act_load(Q8Act &s, g_u8 *const (&tok)[kQ8Tok], int g,
-                                            int lane) {
+template <bool EXP>
+__device__ __forceinline__ void q8_act_load(Q8Act &s, g_u8 *const (&tok)[kQ8Tok], g_u8 *exb,
+                                            uint32_t exo, int g, int lane, int half) {
 #pragma unroll
-    for (int i = 0; i < kQ8Tok; i++)
-        s.tok[i] = gload<u32x2>(tok[i] + (uint32_t)(g * 1024 + 8 * lane));
+    for (int i = 0; i < kQ8Tok / 2; i++)
+        s.tok[i] = gload<u32x2>(tok[kQ8Tok / 2 * half + i] + (uint32_t)(g * 1024 + 8 * lane));
+    if (EXP && half == 0) s.ex = gload<u32x2>(exb + (exo + (uint32_t)(8 * g)));
 }
 
-__device__ __forceinline__ void q8_act_store(uint8_t *stage, const Q8Act &s, int lane) {
+template <bool EXP>
+__device__ __forceinline__ void q8_act_store(uint8_t *stage, const Q8Act &s, int lane, int half) {
 #pragma unroll
-    for (int i = 0; i < kQ8Tok; i++)
-        *reinterpret_cast<u32x2 *>(stage + i * kTokB<false> + 8 * lane) = s.tok[i];
+    for (int i = 0; i < kQ8Tok / 2; i++)
+        *reinterpret_cast<u32x2 *>(stage + (kQ8Tok / 2 * half + i) * kTokB<false> + 8 * lane) =
+            s.tok[i];
+    if (EXP && half == 1 && lane < kQ8Tok) {
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            const int e = (int)(((b < 4 ? s.ex.x : s.ex.y) >> (8 * (b & 3))) & 0xff);
+            *reinterpret_cast<float *>(stage + kQ8Exp + (b * kQ8Tok + lane) * 4) =
+                __builtin_amdgcn_ldexpf(1.0f, e);
+        }
+    }
 }
 
 // One group: the blocks of `cur`'s activations against w; w reloaded with
-// group gn block by block, and gn's activations staged into `nxt`.
+// group gn block by block, and gn's activations staged into `nxt` in two
+// halves.  MATS = 1 (down): each block's product scaled by 2^e of its token.
 template <int MATS, int NTL>
 __device__ __forceinline__ void q8_step(g_u8 *const (&wb)[MATS], uint32_t lo, int gn,
                                         const uint8_t *cur, uint8_t *nxt,
-                                        g_u8 *const (&tok)[kQ8Tok], WQ8<NTL> (&w)[MATS],
-                                        float4v (&acc)[MATS][NTL], int lane) {
+                                        g_u8 *const (&tok)[kQ8Tok], g_u8 *exb, uint32_t exo,
+                                        WQ8<NTL> (&w)[MATS], float4v (&acc)[MATS][NTL], int lane) {
+    constexpr bool EXP = MATS == 1;
     const int r16 = lane & 15, c4 = lane >> 4;
     Q8Act act;
-    q8_act_load(act, tok, gn, lane);
+    q8_act_load<EXP>(act, tok, exb, exo, gn, lane, 0);
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads first
     uint32_t dw[MATS][NTL][4];  // this group's scales; the next group's load in their place
 #pragma unroll
@@ -1409,45 +1435,54 @@ __device__ __forceinline__ void q8_step(g_u8 *const (&wb)[MATS], uint32_t lo, in
                 w[m].q[b][t] = load_q8q(wb[m], lo, gn, b, t, c4);
                 S[m][t] = mfma16(a[b & 1], bq, float4v{});
             }
+        // down: the scales 2^e of this lane's result tokens 4 c4 + i for block
+        // b (d_b 2^e is exact, so the fma rounds d_b S_b 2^e once, as before)
+        float4v sc = float4v{1.0f, 1.0f, 1.0f, 1.0f};
+        if constexpr (EXP)
+            sc = *reinterpret_cast<const float4v *>(cur + kQ8Exp + (b * kQ8Tok + 4 * c4) * 4);
 #pragma unroll
         for (int m = 0; m < MATS; m++)
 #pragma unroll
             for (int t = 0; t < NTL; t++) {
                 const float db = dh2f(dw[m][t][b >> 1] >> (16 * (b & 1)));
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    acc[m][t][i] = __builtin_fmaf(db, S[m][t][i], acc[m][t][i]);
+                for (int i = 0; i < 4; i++) {
+                    const float dbs = EXP ? db * sc[i] : db;
+                    acc[m][t][i] = __builtin_fmaf(dbs, S[m][t][i], acc[m][t][i]);
+                }
             }
+        if (b == 3) {  // the first half of gn's activations to LDS, the second half in flight
+            q8_act_store<EXP>(nxt, act, lane, 0);
+            q8_act_load<EXP>(act, tok, exb, exo, gn, lane, 1);
+        }
         __builtin_amdgcn_sched_barrier(0);  // bounds the live operands to one block
     }
-    q8_act_store(nxt, act, lane);
+    q8_act_store<EXP>(nxt, act, lane, 1);
     chain_detail::wave_lds_sync();
 }
 
 // grid (rows / (16 NTL) row groups, [chain row +] slots, token groups);
-// block = one wave.  MATS = 2, NTL = 1: the gate/up products (w0 = gate,
-// w1 = up, cols = d, rows = F) with the SwiGLU into H as k_mfma_gateup
-// writes it (without the sub-block sums, which no Q8_0 down reads); with
-// ch.tiles, row 0 runs the exact router chains.  MATS = 1, NTL = 2: the
-// down product (w0 = down, cols = F, rows = d), grid z = K split + ksplit *
-// token group, partial sums of split z into Y + z * split_stride.  Token
-// group z takes the slot's 16-token passes z, z + groups, ...
+// block = one wave.  MATS = 2, NTL = 2: the gate/up products (w0 = gate, w1 = up, cols = d,
+// rows = F) from the f16 pieces of x, with the SwiGLU into H (scaled f16
+// pieces and their exponents, no sub-block sums); with ch.tiles, row 0 runs
+// the exact router chains.  MATS = 1, NTL = 1: the down product (w0 = down, cols = F,
+// rows = d) from H, grid z = K split + ksplit * token group, partial sums
+// of split z into Y + z * split_stride.  Token group z takes the slot's
+// 16-token passes z, z + groups, ...  hexp: one byte per position and
+// 32-column block of H.
 template <int MATS, int NTL>
 __global__ __launch_bounds__(64, 2) void k_mfma_q8(
     const uint8_t *__restrict__ w0, const uint8_t *__restrict__ w1, int64_t estride,
-    const _Float16 *__restrict__ act, SlotArgs sa, int cols, int rows, int ksplit,
-    _Float16 *__restrict__ h16, float *__restrict__ hf, float *__restrict__ Y,
-    int64_t split_stride, ChainArgs ch) {
+    const _Float16 *__restrict__ act, uint8_t *__restrict__ hexp, SlotArgs sa, int cols, int rows,
+    int ksplit, _Float16 *__restrict__ h16, float *__restrict__ Y, int64_t split_stride,
+    ChainArgs ch) {
     int slot = blockIdx.y;
     if (MATS == 2 && ch.tiles) {
         if (slot == 0) {
             if (blockIdx.z) return;
-            // four chunks of loads in flight: small layers' expert launches
-            // are short next to a d-long chain (config 1, d = 1024: one
-            // chunk ahead left the chains ~16 us, longer than the products)
             float *lds = reinterpret_cast<float *>(s_q8);
             for (int tile = blockIdx.x; tile < ch.tiles; tile += gridDim.x)
-                chain_tile<8, 128, 4>(ch, tile, lds);
+                chain_tile<8, 128, 1>(ch, tile, lds);
             return;
         }
         slot -= 1;
@@ -1456,10 +1491,10 @@ __global__ __launch_bounds__(64, 2) void k_mfma_q8(
     if (!slot_info(sa, slot, e, p0, n)) return;
     const int lane = threadIdx.x & 63, r16 = lane & 15, c4 = lane >> 4;
     const int rg = blockIdx.x, NG = cols >> 8;
-    constexpr int kPerTile = 4 / NTL;  // row groups per 64-row tile
     const int ks = MATS == 1 ? ksplit : 1;
     const int cz = blockIdx.z / ks, nz = gridDim.z / ks, bz = blockIdx.z - cz * ks;
     const int g0 = (int)((int64_t)NG * bz / ks), g1 = (int)((int64_t)NG * (bz + 1) / ks);
+    constexpr int kPerTile = 4 / NTL;  // row groups per 64-row tile
     const int64_t rbase = (int64_t)e * estride + (int64_t)(rg / kPerTile) * NG * kQ8Group +
                           16 * NTL * (rg % kPerTile) * 16;
     g_u8 *wbm[MATS];
@@ -1467,6 +1502,7 @@ __global__ __launch_bounds__(64, 2) void k_mfma_q8(
     if constexpr (MATS == 2) wbm[1] = uniform(w1 + rbase);
     const uint32_t lo = r16 * 16;
     const uint8_t *ab = reinterpret_cast<const uint8_t *>(act);
+    g_u8 *const exb = uniform(hexp);
     uint8_t *const st0 = s_q8, *const st1 = s_q8 + kQ8Stage;
     for (int c = cz * kQ8Tok; c < n; c += nz * kQ8Tok) {
         g_u8 *tok[kQ8Tok];
@@ -1476,6 +1512,8 @@ __global__ __launch_bounds__(64, 2) void k_mfma_q8(
             const int64_t row = MATS == 2 ? slot_token(sa, p0, q) : p0 + q;
             tok[i] = uniform(ab + row * (int64_t)cols * 4);
         }
+        // down: lane i < 16's exponents row (token i of the pass)
+        const uint32_t exo = MATS == 1 ? (uint32_t)(p0 + min(c + (lane & 15), n - 1)) * (cols >> 5) : 0;
         float4v acc[MATS][NTL];
 #pragma unroll
         for (int m = 0; m < MATS; m++)
@@ -1483,7 +1521,7 @@ __global__ __launch_bounds__(64, 2) void k_mfma_q8(
             for (int t = 0; t < NTL; t++) acc[m][t] = float4v{};
         WQ8<NTL> w[MATS];
         Q8Act a0;
-        q8_act_load(a0, tok, g0, lane);
+        q8_act_load<MATS == 1>(a0, tok, exb, exo, g0, lane, 0);
 #pragma unroll
         for (int m = 0; m < MATS; m++)
 #pragma unroll
@@ -1492,34 +1530,45 @@ __global__ __launch_bounds__(64, 2) void k_mfma_q8(
 #pragma unroll
                 for (int b = 0; b < 8; b++) w[m].q[b][t] = load_q8q(wbm[m], lo, g0, b, t, c4);
             }
-        q8_act_store(st0, a0, lane);
+        q8_act_store<MATS == 1>(st0, a0, lane, 0);
+        q8_act_load<MATS == 1>(a0, tok, exb, exo, g0, lane, 1);
+        q8_act_store<MATS == 1>(st0, a0, lane, 1);
         chain_detail::wave_lds_sync();
         const int last = g1 - 1;
         int g = g0;
         for (; g + 2 <= g1; g += 2) {
-            q8_step<MATS, NTL>(wbm, lo, g + 1, st0, st1, tok, w, acc, lane);
-            q8_step<MATS, NTL>(wbm, lo, min(g + 2, last), st1, st0, tok, w, acc, lane);
+            q8_step<MATS, NTL>(wbm, lo, g + 1, st0, st1, tok, exb, exo, w, acc, lane);
+            q8_step<MATS, NTL>(wbm, lo, min(g + 2, last), st1, st0, tok, exb, exo, w, acc, lane);
         }
-        if (g < g1) q8_step<MATS, NTL>(wbm, lo, g, st0, st1, tok, w, acc, lane);
+        if (g < g1) q8_step<MATS, NTL>(wbm, lo, g, st0, st1, tok, exb, exo, w, acc, lane);
         if constexpr (MATS == 2) {
-            // SwiGLU and H out (f16 pieces and/or f32), as the 16-token
-            // passes of k_mfma_gateup
-            const int F = rows, nkb = (F + 255) >> 8;
-            int fb = rg * 16 * NTL + r16;  // opaque: output addresses are formed here
+            // SwiGLU; per token the 32 values of this wave (a block of H)
+            // scaled into f16's range and written as pieces, the exponent
+            // beside them
+            const int F = rows, nkb = (F + 255) >> 8, neb = F >> 5;
+            static_assert(MATS != 2 || NTL == 2, "a gate/up wave covers one H block");
+            int fb = rg * 32 + r16;  // opaque: output addresses are formed here
             asm volatile("" : "+v"(fb));
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int q = c + 4 * c4 + i;
+                float v[2];
+#pragma unroll
+                for (int t = 0; t < 2; t++) v[t] = silu(acc[0][t][i]) * acc[1][t][i];
+                float mx = fmaxf(fabsf(v[0]), fabsf(v[1]));
+#pragma unroll
+                for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+                // mx >= 2^15: e = ilogb(mx) - 14 puts the block's largest below 2^15
+                const int ex = mx >= 32768.0f ? (int)((__float_as_uint(mx) >> 23) & 0xff) - 141 : 0;
                 if (q < n) {
                     const int64_t p = p0 + q;
 #pragma unroll
-                    for (int t = 0; t < NTL; t++) {
+                    for (int t = 0; t < 2; t++) {
                         const int ft = fb + 16 * t;
-                        const float v = silu(acc[0][t][i]) * acc[1][t][i];
-                        if (hf) hf[p * F + ft] = v;
-                        if (h16)
-                            h16[(p * nkb + (ft >> 8)) * 512 + act16_pos(ft & 255)] = (_Float16)v;
+                        h16[(p * nkb + (ft >> 8)) * 512 + act16_pos(ft & 255)] =
+                            (_Float16)__builtin_amdgcn_ldexpf(v[t], -ex);
                     }
+                    if (r16 == 0) hexp[p * neb + rg] = (uint8_t)ex;
                 }
             }
         } else {
@@ -1598,7 +1647,7 @@ hipError_t launch_mfma_gateup(const uint8_t *gate, const uint8_t *up, int64_t es
 
 hipError_t launch_mfma_gateup_q8(const uint8_t *gate, const uint8_t *up, int64_t estride,
                                  const _Float16 *x16, const SlotArgsHost &sa, int slots,
-                                 int groups, int d, int F, _Float16 *h16, float *hf,
+                                 int groups, int d, int F, _Float16 *h16, uint8_t *hexp,
                                  const ChainArgs &ch, hipStream_t st) {
     if (F % 64 || d % 256 || groups < 1 || groups > 65535) return hipErrorInvalidValue;
     ChainArgs c = ch;
@@ -1606,20 +1655,21 @@ hipError_t launch_mfma_gateup_q8(const uint8_t *gate, const uint8_t *up, int64_t
         if (c.k0 % 128 || c.k1 % 128) return hipErrorInvalidValue;
         c = with_nt(ch, 8);
     }
-    hipLaunchKernelGGL((k_mfma_q8<2, 1>), dim3(F / 16, slots + (c.tiles ? 1 : 0), groups),
-                       dim3(64), 0, st, gate, up, estride, x16, dev_slots(sa), d, F, 1, h16, hf,
-                       nullptr, (int64_t)0, c);
+    hipLaunchKernelGGL((k_mfma_q8<2, 2>), dim3(F / 32, slots + (c.tiles ? 1 : 0), groups), dim3(64), 0,
+                       st, gate, up, estride, x16, hexp, dev_slots(sa), d, F, 1, h16, nullptr,
+                       (int64_t)0, c);
     return hipGetLastError();
 }
 
 hipError_t launch_mfma_down_q8(const uint8_t *down, int64_t estride, const _Float16 *h16,
-                               const SlotArgsHost &sa, int slots, int groups, int d, int F,
-                               int ksplit, float *Y, int64_t split_stride, hipStream_t st) {
+                               const uint8_t *hexp, const SlotArgsHost &sa, int slots, int groups,
+                               int d, int F, int ksplit, float *Y, int64_t split_stride,
+                               hipStream_t st) {
     if (d % 64 || F % 256 || ksplit < 1 || groups < 1 || (int64_t)groups * ksplit > 65535)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL((k_mfma_q8<1, 2>), dim3(d / 32, slots, groups * ksplit), dim3(64), 0, st,
-                       down, nullptr, estride, h16, dev_slots(sa), F, d, ksplit, nullptr, nullptr,
-                       Y, split_stride, ChainArgs{});
+    hipLaunchKernelGGL((k_mfma_q8<1, 1>), dim3(d / 16, slots, groups * ksplit), dim3(64), 0, st, down,
+                       nullptr, estride, h16, const_cast<uint8_t *>(hexp), dev_slots(sa), F, d,
+                       ksplit, nullptr, Y, split_stride, ChainArgs{});
     return hipGetLastError();
 }
 

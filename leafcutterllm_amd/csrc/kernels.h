@@ -130,18 +130,20 @@ hipError_t launch_mfma_gateup(const uint8_t *gate, const uint8_t *up, int64_t es
                               int slots, int chunks, int d, int F, _Float16 *h16, _Float16 *hs,
                               float *hf, const ChainArgs &ch, hipStream_t st, bool x_lo);
 // Q8_0 (RPL64 Q8_0 layout) on the matrix cores, one f16 per activation: a
-// one-wave block per 16-token pass and 16 gate/up rows or 32 down rows.
-// Gate/up: grid (F / 16, slots [+ chain row], groups), SwiGLU into H16 as
-// launch_mfma_gateup (no sub-block sums); down: grid (d / 32, slots, groups *
-// ksplit), partial sums into Y.  Token group z of `groups` takes the slot's
-// 16-token passes z, z + groups, ...
+// one-wave block per 16-token pass and 32 gate/up or 16 down rows.  Gate/up: grid (F / 32,
+// slots [+ chain row], groups), SwiGLU into H as f16 pieces (the format of
+// launch_mfma_gateup, no sub-block sums) scaled by 2^-e per token and
+// 32-column block, e in hexp (one byte per position and block); down: grid
+// (d / 16, slots, groups * ksplit) from those, partial sums into Y.  Token
+// group z of `groups` takes the slot's 16-token passes z, z + groups, ...
 hipError_t launch_mfma_gateup_q8(const uint8_t *gate, const uint8_t *up, int64_t estride,
                                  const _Float16 *x16, const SlotArgsHost &sa, int slots,
-                                 int groups, int d, int F, _Float16 *h16, float *hf,
+                                 int groups, int d, int F, _Float16 *h16, uint8_t *hexp,
                                  const ChainArgs &ch, hipStream_t st);
 hipError_t launch_mfma_down_q8(const uint8_t *down, int64_t estride, const _Float16 *h16,
-                               const SlotArgsHost &sa, int slots, int groups, int d, int F,
-                               int ksplit, float *Y, int64_t split_stride, hipStream_t st);
+                               const uint8_t *hexp, const SlotArgsHost &sa, int slots, int groups,
+                               int d, int F, int ksplit, float *Y, int64_t split_stride,
+                               hipStream_t st);
 hipError_t launch_mfma_down(const uint8_t *down, int64_t estride, const _Float16 *h16,
                             const _Float16 *hs, const SlotArgsHost &sa, int slots, int chunks,
                             int d, int F, int ksplit, float *Y, int64_t split_stride,

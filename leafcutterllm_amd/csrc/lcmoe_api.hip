@@ -62,6 +62,7 @@ struct ExpertSet {  // one family of experts (routed or shared)
     int8_t *hh = nullptr, *hl = nullptr;
     float *hs = nullptr, *hm = nullptr;
     _Float16 *h16 = nullptr, *h16s = nullptr;  // [positions][F/256][hi 256 | lo 256], sums
+    uint8_t *hexp = nullptr;  // Q8_0 matrix-core H: [positions][F/32] block exponents
     // down output partials [kmax][positions][d]
     float *Y = nullptr;
     int kmax = 1;
@@ -262,13 +263,13 @@ int choose_ksplit_mfma(const ExpertSet &s, int d, int active) {
     return ks;
 }
 
-// Q8_0 matrix-core down: one-wave blocks of 32 rows and 16 tokens; split K
-// until about four blocks per CU exist, keeping >= 2 groups of 256 columns
+// Q8_0 matrix-core down: one-wave blocks of 16 rows and 16 tokens; split K
+// until about eight blocks per CU exist, keeping >= 2 groups of 256 columns
 // per split.
 int choose_ksplit_q8(const ExpertSet &s, int d, int active) {
-    const int NG = s.F / 256, blocks = (d / 32) * std::max(1, active);
+    const int NG = s.F / 256, blocks = (d / 16) * std::max(1, active);
     int ks = 1;
-    while (ks < s.kmax && blocks * ks < 1024 && NG >= 2 * ks * 2) ks *= 2;
+    while (ks < s.kmax && blocks * ks < 2048 && NG >= 2 * ks * 2) ks *= 2;
     return ks;
 }
 
@@ -305,10 +306,12 @@ lcmoe_status setup_set(lcmoe_handle *h, ExpertSet &s, int F, const SanitizedStac
     } else {
         if ((st = alloc_n(h, &s.Hf, positions * F))) return st;
     }
+    if (s.q8) {  // H of the Q8_0 matrix-core products: block exponents
+        if ((st = alloc_n(h, &s.hexp, positions * F / 32))) return st;
+    }
     if (s.rpl_gu || s.q8) {
         // ceil(F / 256) pieces of 512 halves and 8 sum pairs per piece per
-        // position; the part past F is never written and stays zero (the
-        // Q8_0 matrix-core down reads the pieces only)
+        // position; the part past F is never written and stays zero
         const int64_t nkb = (F + 255) / 256;
         if ((st = alloc_n(h, &s.h16, positions * nkb * 512))) return st;
         if ((st = alloc_n(h, &s.h16s, positions * nkb * 16))) return st;
@@ -496,9 +499,12 @@ static Plan plan_set(lcmoe_handle *h, const ExpertSet &s, bool shared, int T, in
     // 11.5k / 19.0k / 34.1k / 53.1k; config 2 T = 3 / 4: 25.7k / 28.5k
     // against 22.2k / 28.4k; config 5's layer T = 4: 54.0k against 60.2k.
     const int64_t assign = shared ? T : (int64_t)T * D.n_expert_used;
-    // Q8_0 sets: the matrix-core kernels take one f16 per activation only
+    // Q8_0 sets: the matrix-core kernels take one f16 per activation only,
+    // and pay from T K > E on (config 1, row-per-lane against matrix cores:
+    // T = 4 / 8 / 12: 39.5 / 53.1 / 61.3 us against 44.8 / 46.8 / 47.0 us)
     const bool mma_ok = s.rpl_gu || (s.q8 && !h->x_lo);
-    p.mfma = mma_ok && (shared ? assign > 1 : (assign > (int64_t)D.n_expert || T >= 4));
+    p.mfma = mma_ok && (shared ? assign > 1
+                               : (assign > (int64_t)D.n_expert || (T >= 4 && !s.q8)));
     // passes per slot: all T tokens for a shared expert, the average over
     // the touched experts for the routed ones (busier experts run several
     // passes per block)
@@ -545,12 +551,12 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
     // H between the products in the form the down kernel reads: f16 pieces
     // for the matrix-core downs, int8 limbs for the row-per-lane ones (Q4_K,
     // split Q4_K and Q6_K below one token per expert), f32 for the generic one
-    const bool h16_out = pl.mfma && (s.rpl_dn || s.q6_dn || s.split_dn || s.q8);
+    const bool h16_out = pl.mfma && (s.rpl_dn || s.q6_dn || s.split_dn);
     const bool limb_out = !pl.mfma && (s.rpl_dn || s.q6_dn || s.q8 || s.split_dn);
     HIP_TRY(timed(h, st, shared || fused_only ? kSlotGateUpSh : kSlotGateUp, [&] {
         if (pl.mfma && s.q8)
             return launch_mfma_gateup_q8(s.gate, s.up, s.sz_gu, h->x16, sa, slots,
-                                         2 * pl.chunks, d, s.F, s.h16, nullptr, ch, st);
+                                         2 * pl.chunks, d, s.F, s.h16, s.hexp, ch, st);
         if (pl.mfma)
             return launch_mfma_gateup(s.gate, s.up, s.sz_gu, h->x16, h->x16s, sa, slots,
                                       pl.chunks, d, s.F, h16_out ? s.h16 : nullptr, s.h16s,
@@ -570,7 +576,7 @@ static lcmoe_status run_set(lcmoe_handle *h, ExpertSet &s, bool shared, const fl
         // down 876 us with 16-token passes, 717 with 32-token passes); with
         // two f16 per activation one pass size per launch, by the average
         if (s.q8 && pl.mfma)
-            return launch_mfma_down_q8(s.down, s.sz_dn, s.h16, sa, slots, 2 * pl.chunks, d, s.F,
+            return launch_mfma_down_q8(s.down, s.sz_dn, s.h16, s.hexp, sa, slots, 2 * pl.chunks, d, s.F,
                                        pl.ks, s.Y, s.positions * d, st);
         if (s.q6_dn && pl.mfma)
             return launch_mfma_down_q6(s.down, s.sz_dn, s.h16, sa, slots, pl.chunks, d, s.F,
