@@ -796,6 +796,7 @@ __device__ __forceinline__ void logits_and_activations(const RouterArgs &a, int 
 // grid (T [+ chain blocks]): block t routes token t; with ch.tiles, the
 // blocks past T run the first column range of the exact router chains
 // (wave 0, one tile at a time)
+template <int FBW>
 __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a, ChainArgs ch) {
     __shared__ double s_a[kMaxE], s_b[kMaxE];
     __shared__ float s_z[kMaxE], s_zlo[kMaxE], s_zhi[kMaxE], s_s[kMaxE], s_g[kMaxE];
@@ -806,8 +807,10 @@ __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a, Chain
     // x row for the logits (C <= 64 floats per lane), later the fallback's
     // chain stream (one token, 8 experts)
     // (and first, with the fused norm, its squares: kRmsnormLds floats)
+    // the fallback's chain streams: one region for each of its FBW waves
     constexpr int kXFloats = 64 * (64 + 4), kFbFloats = chain_lds_floats(1 + 8, 256);
-    constexpr int kS1 = kXFloats > kFbFloats ? kXFloats : kFbFloats;
+    constexpr int kFbAll = kFbFloats * FBW;
+    constexpr int kS1 = kXFloats > kFbAll ? kXFloats : kFbAll;
     constexpr int kS2 = rmsnorm_lds<kFusedNormChunk>();
     __shared__ __attribute__((aligned(16))) float s_x[kS1 > kS2 ? kS1 : kS2];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -899,10 +902,14 @@ __global__ __launch_bounds__(kFastThreads) void k_route_fast(RouterArgs a, Chain
     }
     __syncthreads();
     if (!s_flag) {  // 3. fallback: exact chains, exact selection
-        if (wave == 0) {
+        // the token's tiles of 8 experts side by side on FBW waves: a tile's
+        // time is its d / 256 chunk loads one after another, so the eight
+        // tiles of E = 60 on one wave took ~112 us
+        const int ne = (E + 7) / 8;
+        if (wave < FBW) {
             const ChainArgs ca = make_chains(a.x, a.wrt, a.logits, nullptr, a.T, d, E, 0, d, 1);
-            const int ne = (E + 7) / 8;
-            for (int g = 0; g < ne; g++) chain_tile<1, 256, 1>(ca, t * ne + g, s_x);
+            for (int g = wave; g < ne; g += FBW)
+                chain_tile<1, 256, 1>(ca, t * ne + g, s_x + wave * kFbFloats);
         }
         __threadfence_block();
         __syncthreads();
@@ -1276,11 +1283,13 @@ __device__ bool sig_certify(const RouterArgs &a, int t, float *s_lo, float *s_hi
     return ok;
 }
 
-template <int NC4>
+template <int NC4, int FBW>
 __global__ __launch_bounds__(64 * kSigWaves) void k_route_sig(RouterArgs a, ChainArgs ch) {
     __shared__ float s_f[3 * kMaxE + 3 * 64];  // certification: keys, group scores
     // one wave's chain stream: the chain blocks', or the one-token fallback's
-    __shared__ __attribute__((aligned(16))) float s_chain[chain_lds_floats(1 + 8, 256)];
+    // streams, one for each of its FBW waves
+    constexpr int kChainFloats = chain_lds_floats(1 + 8, 256);
+    __shared__ __attribute__((aligned(16))) float s_chain[kChainFloats * FBW];
     __shared__ int s_last;
     const int t = blockIdx.y, tid = threadIdx.x, wave = tid >> 6;
     const int nsig = a.E / kSigWaves;  // bound blocks per token
@@ -1302,25 +1311,35 @@ __global__ __launch_bounds__(64 * kSigWaves) void k_route_sig(RouterArgs a, Chai
     __syncthreads();
     if (!s_last) return;
     // the last block of token t: every bound of t is stored
+    __shared__ int s_sel[kMaxK];
+    __shared__ int s_ok;
     if (wave == 0) {
-        __shared__ int s_sel[kMaxK];
         if (tid == 0) a.tsync[t] = 0;
         const bool ok = sig_certify(a, t, s_f, s_f + a.E, s_f + 2 * a.E, s_f + 3 * a.E, s_sel);
-        if (a.T > 1) return;  // the chains, selection and dispatch launches follow
-        // one token: this wave finishes the routing itself (no launches
-        // follow): for an uncertified token the exact chains over all d
-        // columns and the exact selection, then the dispatch from LDS
-        if (!ok) {
+        if (tid == 0) s_ok = ok;
+    }
+    if (a.T > 1) return;  // the chains, selection and dispatch launches follow
+    // one token: this block finishes the routing itself (no launches
+    // follow): for an uncertified token the exact chains over all d columns
+    // (its tiles of 8 experts spread over FBW waves) and the exact
+    // selection, then the dispatch from LDS
+    __syncthreads();
+    if (!s_ok) {
+        if (wave < FBW) {
             const ChainArgs ca = make_chains(a.x, a.wrt, a.logits, nullptr, a.T, a.d, a.E, 0,
                                              a.d, 1);
-            for (int g = 0; g < ca.tiles; g++) chain_tile<1, 256, 1>(ca, g, s_chain);
-            __threadfence_block();
+            for (int g = wave; g < ca.tiles; g += FBW)
+                chain_tile<1, 256, 1>(ca, g, s_chain + wave * kChainFloats);
+        }
+        __threadfence_block();
+        __syncthreads();
+        if (wave == 0) {
             float *s_z = s_f, *s_s = s_f + kMaxE, *s_g = s_f + 2 * kMaxE;
             select_token(a, t, s_z, s_s, s_g, s_sel);
             chain_detail::wave_lds_sync();
         }
-        dispatch_one(a, s_sel);
     }
+    if (wave == 0) dispatch_one(a, s_sel);
 }
 
 // ---------------------------------------------------------------------------
@@ -1476,7 +1495,13 @@ hipError_t launch_route_fast(const RouterArgs &a, const ChainArgs &ch, hipStream
         c = with_nt(ch, ch.T == 1 ? 1 : 8);
         cb = c.tiles < 64 ? c.tiles : 64;
     }
-    hipLaunchKernelGGL(k_route_fast, dim3(a.T + cb), dim3(kFastThreads), 0, st, a, c);
+    // E > 8: the fallback's tiles on 4 waves (LDS for 4 chain streams, ~75
+    // KB; 8 do not fit beside the rest); E <= 8 has one tile and keeps the
+    // small LDS footprint
+    if (a.E > 8)
+        hipLaunchKernelGGL(k_route_fast<4>, dim3(a.T + cb), dim3(kFastThreads), 0, st, a, c);
+    else
+        hipLaunchKernelGGL(k_route_fast<1>, dim3(a.T + cb), dim3(kFastThreads), 0, st, a, c);
     return hipGetLastError();
 }
 
@@ -1487,6 +1512,20 @@ bool route_sig_ok(const RouterArgs &a) {
     return a.wlc && a.bnd && a.tsync && a.flag && a.E % kSigWaves == 0 && a.E <= 256 &&
            a.d % 256 == 0 && sig_nc4_ok(a.d / 256) && groups && a.K <= kMaxK &&
            route_chains_ok(a);
+}
+
+template <int FBW>
+static void launch_sig(int c4, dim3 grid, dim3 block, hipStream_t st, const RouterArgs &a,
+                       const ChainArgs &c) {
+    switch (c4) {
+    case 1: hipLaunchKernelGGL((k_route_sig<1, FBW>), grid, block, 0, st, a, c); break;
+    case 2: hipLaunchKernelGGL((k_route_sig<2, FBW>), grid, block, 0, st, a, c); break;
+    case 4: hipLaunchKernelGGL((k_route_sig<4, FBW>), grid, block, 0, st, a, c); break;
+    case 8: hipLaunchKernelGGL((k_route_sig<8, FBW>), grid, block, 0, st, a, c); break;
+    case 16: hipLaunchKernelGGL((k_route_sig<16, FBW>), grid, block, 0, st, a, c); break;
+    case 28: hipLaunchKernelGGL((k_route_sig<28, FBW>), grid, block, 0, st, a, c); break;
+    default: hipLaunchKernelGGL((k_route_sig<32, FBW>), grid, block, 0, st, a, c); break;
+    }
 }
 
 hipError_t launch_route_sig(const RouterArgs &a, const ChainArgs &ch, hipStream_t st) {
@@ -1500,15 +1539,12 @@ hipError_t launch_route_sig(const RouterArgs &a, const ChainArgs &ch, hipStream_
         cb = c.tiles < 64 ? c.tiles : 64;
     }
     const dim3 grid(a.E / kSigWaves + cb, a.T), block(64 * kSigWaves);
-    switch (a.d / 256) {
-    case 1: hipLaunchKernelGGL(k_route_sig<1>, grid, block, 0, st, a, c); break;
-    case 2: hipLaunchKernelGGL(k_route_sig<2>, grid, block, 0, st, a, c); break;
-    case 4: hipLaunchKernelGGL(k_route_sig<4>, grid, block, 0, st, a, c); break;
-    case 8: hipLaunchKernelGGL(k_route_sig<8>, grid, block, 0, st, a, c); break;
-    case 16: hipLaunchKernelGGL(k_route_sig<16>, grid, block, 0, st, a, c); break;
-    case 28: hipLaunchKernelGGL(k_route_sig<28>, grid, block, 0, st, a, c); break;
-    default: hipLaunchKernelGGL(k_route_sig<32>, grid, block, 0, st, a, c); break;
-    }
+    // one token: its fallback chains on every wave of the block (LDS for
+    // kSigWaves chain streams); more tokens keep the small LDS footprint
+    if (a.T == 1)
+        launch_sig<kSigWaves>(a.d / 256, grid, block, st, a, c);
+    else
+        launch_sig<1>(a.d / 256, grid, block, st, a, c);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.T == 1) return e;  // one token: the launch dispatched it
     // the exact chains and selection for the marked tokens; the activations
