@@ -369,6 +369,30 @@ def test_wide_softmax_router_exact_tie_falls_back():
     assert res["rel_l2"] < 1e-3
 
 
+@pytest.mark.parametrize("E,T", [(40, 3), (40, 16), (64, 5)])
+def test_fast_router_multi_tile_fallback(E, T):
+    """More than 8 experts at several tokens (the per-token fast router):
+    experts 5 and 9 share a router row that leads every token's logits (all
+    token rows carry token 0's sign pattern), so no token can be certified
+    and each block runs its token's exact chains, its tiles of 8 experts
+    spread over four waves (E = 40: five tiles, so one wave runs two; E =
+    64: eight, two per wave).  Identical rows give identical bounds, which
+    never order the pair, so every token takes the fallback; the selection
+    ranks 5 before 9 for every token."""
+    cfg = small_config(f"fb{E}", 512, 256, E, 4, L.ROUTE_SOFTMAX_RENORM, Q4, Q4)
+    layer = L.synth_layer(cfg, seed=47)
+    x = L.synth_x(cfg, T, seed=47, index=T)
+    x = (np.abs(x) * np.sign(x[0])[None, :]).astype(np.float32)
+    r = layer["router"].copy()
+    r[:, 5] = 4.0 * np.sign(x[0]) / np.sqrt(cfg.d_model)
+    r[:, 9] = r[:, 5]
+    layer["router"] = r
+    res = run_and_check(cfg, layer, x)
+    idx = res["topk_idx"].reshape(T, cfg.n_expert_used)
+    assert np.all(idx[:, 0] == 5) and np.all(idx[:, 1] == 9)
+    assert res["rel_l2"] < 1e-3
+
+
 def test_e1_k1_reduces_to_dense_ffn():
     """E = 1, K = 1, renormalised: weight exactly 1.0 and the layer is the
     dense SwiGLU ffn_forward (engine.rs:146-164) of the one expert."""
