@@ -1496,9 +1496,10 @@ hipError_t launch_route_fast(const RouterArgs &a, const ChainArgs &ch, hipStream
         cb = c.tiles < 64 ? c.tiles : 64;
     }
     // E > 8: the fallback's tiles on 4 waves (LDS for 4 chain streams, ~75
-    // KB; 8 do not fit beside the rest); E <= 8 has one tile and keeps the
-    // small LDS footprint
-    if (a.E > 8)
+    // KB; 8 do not fit beside the rest), which leaves one block per CU, so
+    // only while the grid fits one round of the CUs; E <= 8 has one tile and
+    // keeps the small LDS footprint
+    if (a.E > 8 && a.T <= 256)
         hipLaunchKernelGGL(k_route_fast<4>, dim3(a.T + cb), dim3(kFastThreads), 0, st, a, c);
     else
         hipLaunchKernelGGL(k_route_fast<1>, dim3(a.T + cb), dim3(kFastThreads), 0, st, a, c);

@@ -369,14 +369,15 @@ def test_wide_softmax_router_exact_tie_falls_back():
     assert res["rel_l2"] < 1e-3
 
 
-@pytest.mark.parametrize("E,T", [(40, 3), (40, 16), (64, 5)])
+@pytest.mark.parametrize("E,T", [(40, 3), (40, 16), (64, 5), (40, 300)])
 def test_fast_router_multi_tile_fallback(E, T):
     """More than 8 experts at several tokens (the per-token fast router):
     experts 5 and 9 share a router row that leads every token's logits (all
     token rows carry token 0's sign pattern), so no token can be certified
     and each block runs its token's exact chains, its tiles of 8 experts
     spread over four waves (E = 40: five tiles, so one wave runs two; E =
-    64: eight, two per wave).  Identical rows give identical bounds, which
+    64: eight, two per wave; past 256 tokens one wave runs them all, as at
+    E <= 8).  Identical rows give identical bounds, which
     never order the pair, so every token takes the fallback; the selection
     ranks 5 before 9 for every token."""
     cfg = small_config(f"fb{E}", 512, 256, E, 4, L.ROUTE_SOFTMAX_RENORM, Q4, Q4)
