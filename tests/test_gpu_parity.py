@@ -394,6 +394,31 @@ def test_fast_router_multi_tile_fallback(E, T):
     assert res["rel_l2"] < 1e-3
 
 
+@pytest.mark.parametrize("T", [3, 16, 64])
+def test_q8_large_weights_h_beyond_f16(T):
+    """Q8_0 experts whose every block has scale 1 and |q| <= 100 (the largest
+    weights the loader keeps): gate and up sums reach ~1e3 and H ~1e6, far
+    past the f16 range.  The matrix-core path (T * K > E) carries H as f16
+    scaled by a power of two per token and 32-column block; the row-per-lane
+    path (T = 3) as int8 limbs.  Both stay within the layer bar."""
+    cfg = small_config("q8big", 512, 512, 8, 2, L.ROUTE_SOFTMAX_RENORM, Q8, Q8, n_shared=1,
+                       d_ff_shared=512)
+    layer = L.synth_layer(cfg, seed=53)
+    rng = np.random.default_rng(53)
+    for k, n in (("gate", 8), ("up", 8), ("down", 8), ("gate_sh", 1), ("up_sh", 1),
+                 ("down_sh", 1)):
+        nb = layer[k].size // 34
+        q = rng.integers(-100, 101, (nb, 32))
+        blocks = np.zeros((nb, 34), np.uint8)
+        blocks[:, :2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+        blocks[:, 2:] = q.astype(np.int8).view(np.uint8)
+        layer[k] = blocks.reshape(-1)
+    x = L.synth_x(cfg, T, seed=53, index=T)
+    res = run_and_check(cfg, layer, x)
+    assert np.all(np.isfinite(res["y"]))
+    assert res["rel_l2"] < 1e-3
+
+
 def test_e1_k1_reduces_to_dense_ffn():
     """E = 1, K = 1, renormalised: weight exactly 1.0 and the layer is the
     dense SwiGLU ffn_forward (engine.rs:146-164) of the one expert."""
